@@ -1,0 +1,153 @@
+"""ctypes bindings of the HIP backend's C ABI (include/frizzle_hip.h).
+
+The library is libfrizzle_hip.so next to this file, built by
+``python -m frizzle_amd.build``. There is no fallback: if the library is
+missing, loading raises, naming how to build it.
+"""
+import ctypes
+import os
+from ctypes import (POINTER, c_char, c_double, c_float, c_int, c_uint16,
+                    c_uint32, c_uint64, c_void_p)
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libfrizzle_hip.so"
+
+FRZ_OK = 0
+ROLE = {
+    "q": 0, "k": 1, "v": 2, "o": 3, "gate": 4, "up": 5, "down": 6,
+    "attn_norm": 7, "q_norm": 8, "k_norm": 9, "post_attn_norm": 10,
+    "ffn_norm": 11, "post_ffn_norm": 12, "embedding": 13, "output_norm": 14,
+}
+LAYER_ROLES = [r for r, i in ROLE.items() if i <= 12]
+
+
+class FrzError(RuntimeError):
+    """A call across the C ABI returned a non-zero status."""
+
+    def __init__(self, status, message):
+        super().__init__(f"frizzle_hip status {status}: {message}")
+        self.status = status
+
+
+class Limits(ctypes.Structure):
+    _fields_ = [("name", c_char * 64), ("memory_bytes", c_uint64),
+                ("compute_units", c_int), ("lds_bytes_per_block", c_int)]
+
+
+class Sampling(ctypes.Structure):
+    _fields_ = [("top_k", c_uint32), ("temperature", c_float),
+                ("top_p", c_float), ("min_p", c_float), ("seed", c_uint64)]
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in (
+        "hidden", "ffn", "head_dim", "query_heads", "kv_heads", "layers",
+        "vocab", "window", "pattern", "context", "local_slots")] + [
+        ("rope_local", c_float), ("rope_global", c_float), ("epsilon", c_float)]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+class Edit(ctypes.Structure):
+    _fields_ = [("layer", c_uint32), ("neuron", c_uint32), ("kind", c_uint32),
+                ("value", c_float), ("from_", c_uint32), ("until", c_uint32)]
+
+
+_P = c_void_p
+_SIGS = {
+    "frz_last_error": (ctypes.c_char_p, []),
+    "frz_open": (c_int, [c_int, POINTER(c_void_p), POINTER(Limits)]),
+    "frz_close": (None, [_P]),
+    "frz_sync": (c_int, [_P]),
+    "frz_alloc": (c_int, [_P, c_uint64, POINTER(c_void_p)]),
+    "frz_free": (c_int, [_P, _P]),
+    "frz_write": (c_int, [_P, _P, _P, c_uint64]),
+    "frz_read": (c_int, [_P, _P, _P, c_uint64]),
+    "frz_fill_zero": (c_int, [_P, _P, c_uint64]),
+    "frz_q4_0_split": (c_int, [_P, c_uint64, _P, _P]),
+    "frz_op_gemv": (c_int, [_P, _P, _P, c_int, c_int, _P, c_int, _P, c_int,
+                            c_uint32, c_int]),
+    "frz_op_gated": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P, _P,
+                             c_uint32, c_uint32, _P, c_int]),
+    "frz_op_norm": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_float, c_uint32,
+                            c_int]),
+    "frz_op_rope": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P,
+                            c_int, c_int, c_int, c_int, c_float, c_uint32,
+                            c_uint32]),
+    "frz_op_attention": (c_int, [_P, _P, c_int, _P, _P, _P, c_int, c_int,
+                                 c_int, c_int, c_int, c_float, c_uint32,
+                                 c_uint32]),
+    "frz_op_gather": (c_int, [_P, _P, _P, c_int, c_int, _P, c_uint32, c_float,
+                              _P]),
+    "frz_op_edit": (c_int, [_P, _P, c_int, _P, c_int, c_uint32, c_uint32]),
+    "frz_op_topk": (c_int, [_P, _P, c_int, _P]),
+    "frz_op_draw": (c_int, [_P, _P, POINTER(Sampling), c_uint32, c_uint32,
+                            _P]),
+    "frz_op_numerics": (c_int, [_P, c_int, _P, _P, c_int]),
+    "frz_bench_gemv": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p), c_int,
+                               c_int, c_int, _P, _P, c_int, POINTER(c_double)]),
+    "frz_bench_gated": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p),
+                                POINTER(c_void_p), POINTER(c_void_p), c_int,
+                                c_int, c_int, _P, _P, c_int,
+                                POINTER(c_double)]),
+    "frz_rope_turns": (None, [c_float, c_int, POINTER(c_float)]),
+    "frz_edit_check": (c_int, [_P, c_uint32, c_uint32, c_uint32,
+                               POINTER(c_uint32)]),
+    "frz_edit_table_words": (c_uint32, [c_uint32, c_uint32]),
+    "frz_edit_table": (c_int, [_P, c_uint32, c_uint32, c_uint32, _P]),
+    "frz_edit_apply": (c_float, [c_uint32, c_float, c_float]),
+    "frz_gemma3_1b_config": (None, [POINTER(ModelConfig), c_int]),
+    "frz_tensor_bytes": (c_uint64, [POINTER(ModelConfig), c_int]),
+    "frz_synth_tensor": (c_int, [POINTER(ModelConfig), c_uint64, c_int, c_int,
+                                 _P, c_uint64]),
+    "frz_model_create": (c_int, [_P, POINTER(ModelConfig), POINTER(c_void_p)]),
+    "frz_model_destroy": (None, [_P]),
+    "frz_model_set_tensor": (c_int, [_P, c_int, c_int, _P, c_uint64]),
+    "frz_model_synthesize": (c_int, [_P, c_uint64]),
+    "frz_model_set_edits": (c_int, [_P, _P, c_uint32]),
+    "frz_model_step": (c_int, [_P, c_uint32, c_uint32, _P, c_int,
+                               POINTER(Sampling)]),
+    "frz_model_decode": (c_int, [_P, c_uint32, c_uint32, POINTER(Sampling),
+                                 _P, _P]),
+    "frz_model_read_logits": (c_int, [_P, _P, c_uint32]),
+    "frz_model_read_record": (c_int, [_P, _P]),
+    "frz_model_read_candidates": (c_int, [_P, _P]),
+    "frz_model_read_hidden": (c_int, [_P, _P, c_uint32]),
+    "frz_model_read_cache": (c_int, [_P, c_int, c_int, _P, c_uint64]),
+    "frz_model_time_decode": (c_int, [_P, c_uint32, c_uint32,
+                                      POINTER(Sampling), POINTER(c_double)]),
+    "frz_generate": (c_int, [_P, _P, c_uint32, _P, c_uint32, POINTER(Sampling),
+                             c_uint32, _P, c_uint32, _P, POINTER(c_uint32)]),
+}
+
+_lib = None
+
+
+def load():
+    """The loaded library, with every entry point's signature set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise OSError(
+            f"{LIB_PATH} is missing: build it with `python -m frizzle_amd.build` "
+            "(there is no CPU fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    """Every entry point this binding declares (all must exist in the .so)."""
+    return sorted(_SIGS)
+
+
+def check(status):
+    if status != FRZ_OK:
+        raise FrzError(status, load().frz_last_error().decode(errors="replace"))
+    return status

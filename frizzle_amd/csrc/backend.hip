@@ -1,0 +1,420 @@
+// The C ABI's device, buffer and one-kernel entry points (include/
+// frizzle_hip.h). Each op call fills a device-side step record on the
+// device's stream and launches one kernel family there; ops wait for their
+// work so their host arguments need not outlive the call.
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/frizzle_hip.h"
+#include "backend.h"
+#include "kernels.h"
+#include "numerics.h"
+
+namespace frz {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& message) {
+  g_last_error = message;
+  return status;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FRZ_OK;
+  return fail(FRZ_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+// The shared numerics run on the device, one value a lane.
+__global__ void numerics_kernel(int which, const float* in, float* out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = in[i];
+  float r = 0.0f;
+  switch (which) {
+    case 0: r = exp2f_fixed(x); break;
+    case 1: { float s, c; sincos_fixed(x, &s, &c); r = c; break; }
+    case 2: { float s, c; sincos_fixed(x, &s, &c); r = s; break; }
+    case 3: r = inverse_sqrt(x); break;
+    case 4: r = gelu_tanh(x); break;
+    case 5: r = exp_nonpositive(x); break;
+    case 6: r = bits_to_float((uint32_t)f16_pack(x)); break;
+    case 7: r = __builtin_sqrtf(x); break;
+    case 8: r = in[2 * (i / 2)] / in[2 * (i / 2) + 1]; break;
+    default: break;
+  }
+  out[i] = r;
+}
+
+DevStep host_step(uint32_t position, uint32_t tokens) {
+  DevStep s;
+  std::memset(&s, 0, sizeof s);
+  s.position = position;
+  s.tokens = tokens;
+  s.top_k = 1;
+  s.top_p = 1.0f;
+  return s;
+}
+
+}  // namespace
+
+int device_put_step(frz_device* dev, const DevStep& s) {
+  int rc = check_hip(hipMemcpyAsync(dev->step, &s, sizeof s, hipMemcpyHostToDevice, dev->stream),
+                     "hipMemcpyAsync(step)");
+  if (rc) return rc;
+  return check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+int device_finish(frz_device* dev, hipError_t launched, const char* what) {
+  if (launched != hipSuccess) return check_hip(launched, what);
+  return check_hip(hipStreamSynchronize(dev->stream), what);
+}
+
+int attention_max_chunks(int window, int slots) {
+  const int by_window = (window + kChunkKeys - 1) / kChunkKeys + 1;
+  const int by_slots = (slots + kChunkKeys - 1) / kChunkKeys + 1;
+  return by_window < by_slots ? by_window : by_slots;
+}
+
+void fill_sampling(DevStep& s, const frz_sampling* sampling) {
+  s.top_k = sampling ? sampling->top_k : 1;
+  s.temperature = sampling ? sampling->temperature : 0.0f;
+  s.top_p = sampling ? sampling->top_p : 1.0f;
+  s.min_p = sampling ? sampling->min_p : 0.0f;
+  s.log_min_p = s.min_p > 0.0f ? std::log(s.min_p) : 0.0f;
+  const uint64_t seed = sampling ? sampling->seed : 0;
+  s.seed[0] = (uint32_t)seed;
+  s.seed[1] = (uint32_t)(seed >> 32);
+}
+
+}  // namespace frz
+
+using namespace frz;
+
+extern "C" {
+
+const char* frz_last_error(void) { return g_last_error.c_str(); }
+
+int frz_open(int ordinal, frz_device** out, frz_limits* limits) {
+  if (!out) return fail(FRZ_ERR_ARGUMENT, "frz_open: null out");
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    return fail(FRZ_ERR_DEVICE, "frz_open: no HIP device");
+  }
+  if (ordinal < 0 || ordinal >= count) return fail(FRZ_ERR_ARGUMENT, "frz_open: no such device");
+  if (int rc = check_hip(hipSetDevice(ordinal), "hipSetDevice")) return rc;
+  hipDeviceProp_t prop;
+  if (int rc = check_hip(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties")) return rc;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    return fail(FRZ_ERR_DEVICE, std::string("frz_open: built for gfx950, device is ") +
+                                    prop.gcnArchName);
+  }
+  frz_device* dev = new frz_device();
+  dev->ordinal = ordinal;
+  dev->props = prop;
+  if (int rc = check_hip(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking),
+                         "hipStreamCreate")) {
+    delete dev;
+    return rc;
+  }
+  if (int rc = check_hip(hipMalloc(&dev->step, sizeof(DevStep)), "hipMalloc(step)")) {
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+    return rc;
+  }
+  if (limits) {
+    std::memset(limits, 0, sizeof *limits);
+    std::strncpy(limits->name, prop.gcnArchName, sizeof(limits->name) - 1);
+    limits->memory_bytes = prop.totalGlobalMem;
+    limits->compute_units = prop.multiProcessorCount;
+    limits->lds_bytes_per_block = (int)prop.sharedMemPerBlock;
+  }
+  *out = dev;
+  return FRZ_OK;
+}
+
+void frz_close(frz_device* dev) {
+  if (!dev) return;
+  (void)hipSetDevice(dev->ordinal);
+  (void)hipStreamSynchronize(dev->stream);
+  (void)hipFree(dev->step);
+  (void)hipStreamDestroy(dev->stream);
+  delete dev;
+}
+
+int frz_sync(frz_device* dev) {
+  return check_hip(hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+int frz_alloc(frz_device* dev, uint64_t bytes, void** dev_ptr) {
+  if (!dev || !dev_ptr) return fail(FRZ_ERR_ARGUMENT, "frz_alloc: null argument");
+  (void)hipSetDevice(dev->ordinal);
+  return check_hip(hipMalloc(dev_ptr, bytes ? bytes : 1), "hipMalloc");
+}
+
+int frz_free(frz_device* dev, void* dev_ptr) {
+  if (!dev) return fail(FRZ_ERR_ARGUMENT, "frz_free: null device");
+  return check_hip(hipFree(dev_ptr), "hipFree");
+}
+
+int frz_write(frz_device* dev, void* dev_dst, const void* host_src, uint64_t bytes) {
+  if (int rc = check_hip(hipMemcpyAsync(dev_dst, host_src, bytes, hipMemcpyHostToDevice,
+                                        dev->stream),
+                         "hipMemcpyAsync(H2D)"))
+    return rc;
+  return frz_sync(dev);
+}
+
+int frz_read(frz_device* dev, void* host_dst, const void* dev_src, uint64_t bytes) {
+  if (int rc = check_hip(hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost,
+                                        dev->stream),
+                         "hipMemcpyAsync(D2H)"))
+    return rc;
+  return frz_sync(dev);
+}
+
+int frz_fill_zero(frz_device* dev, void* dev_dst, uint64_t bytes) {
+  if (int rc = check_hip(hipMemsetAsync(dev_dst, 0, bytes, dev->stream), "hipMemsetAsync"))
+    return rc;
+  return frz_sync(dev);
+}
+
+int frz_q4_0_split(const void* gguf_blocks, uint64_t blocks, void* codes_out,
+                   void* scales_out) {
+  if (!gguf_blocks || !codes_out || !scales_out) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_q4_0_split: null argument");
+  }
+  const uint8_t* in = static_cast<const uint8_t*>(gguf_blocks);
+  uint8_t* codes = static_cast<uint8_t*>(codes_out);
+  uint8_t* scales = static_cast<uint8_t*>(scales_out);
+  for (uint64_t b = 0; b < blocks; ++b) {
+    std::memcpy(codes + 16 * b, in + 18 * b + 2, 16);
+    std::memcpy(scales + 2 * b, in + 18 * b, 2);
+  }
+  return FRZ_OK;
+}
+
+static Q4Matrix q4(const void* codes, const void* scales, int rows, int cols) {
+  return Q4Matrix{static_cast<const uint8_t*>(codes), static_cast<const uint16_t*>(scales), rows,
+                  cols};
+}
+
+static bool shape_ok(int rows, int cols) { return rows > 0 && cols > 0 && cols % 32 == 0; }
+
+int frz_op_gemv(frz_device* dev, const void* codes, const void* scales, int rows, int cols,
+                const float* x, int x_stride, float* y, int y_stride, uint32_t tokens,
+                int last_token) {
+  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gemv: bad shape or tokens");
+  }
+  if (int rc = device_put_step(dev, host_step(0, tokens))) return rc;
+  return device_finish(dev,
+                       launch_gemv(dev->stream, dev->step, q4(codes, scales, rows, cols), x,
+                                   x_stride, y, y_stride, (int)tokens, last_token != 0),
+                       "frz_op_gemv");
+}
+
+int frz_op_gated(frz_device* dev, const void* gate_codes, const void* gate_scales,
+                 const void* up_codes, const void* up_scales, int rows, int cols, const float* x,
+                 float* act, uint32_t tokens, uint32_t position, const uint32_t* edits_dev,
+                 int layer) {
+  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gated: bad shape or tokens");
+  }
+  if (int rc = device_put_step(dev, host_step(position, tokens))) return rc;
+  return device_finish(
+      dev,
+      launch_gated(dev->stream, dev->step, q4(gate_codes, gate_scales, rows, cols),
+                   q4(up_codes, up_scales, rows, cols), x, act, (int)tokens, edits_dev, layer),
+      "frz_op_gated");
+}
+
+int frz_op_norm(frz_device* dev, const float* gain, const float* post_gain, const float* output,
+                float* hidden, float* normed, int width, float epsilon, uint32_t tokens,
+                int last_token) {
+  if (width <= 0 || width % 4 != 0 || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_norm: bad width or tokens");
+  }
+  if (int rc = device_put_step(dev, host_step(0, tokens))) return rc;
+  NormArgs a{gain, post_gain, output, hidden, normed, epsilon, width, last_token != 0};
+  return device_finish(dev, launch_norm(dev->stream, dev->step, a, (int)tokens), "frz_op_norm");
+}
+
+int frz_op_rope(frz_device* dev, const float* turns, const float* query_gain,
+                const float* key_gain, float* query, const float* key, const float* value,
+                int q_stride, int kv_stride, uint16_t* key_cache, uint16_t* value_cache,
+                int slots, int head_dim, int query_heads, int kv_heads, float epsilon,
+                uint32_t position, uint32_t tokens) {
+  if (tokens == 0 || tokens > (uint32_t)kPrefillBlock || slots < (int)tokens) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope: bad tokens or slots");
+  }
+  if (int rc = device_put_step(dev, host_step(position, tokens))) return rc;
+  RopeArgs a{turns, query_gain, key_gain, query, key, value, q_stride, kv_stride,
+             key_cache, value_cache, slots, head_dim, query_heads, kv_heads, epsilon};
+  return device_finish(dev, launch_rope(dev->stream, dev->step, a, (int)tokens), "frz_op_rope");
+}
+
+int frz_op_attention(frz_device* dev, const float* query, int q_stride,
+                     const uint16_t* key_cache, const uint16_t* value_cache, float* out,
+                     int slots, int window, int head_dim, int query_heads, int kv_heads,
+                     float scale, uint32_t position, uint32_t tokens) {
+  if (tokens == 0 || tokens > (uint32_t)kPrefillBlock || head_dim != 256 ||
+      query_heads != 4 * kv_heads || window <= 0 || slots <= 0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_attention: unsupported shape");
+  }
+  const int max_chunks = attention_max_chunks(window, slots);
+  const size_t part_floats = (size_t)tokens * max_chunks * query_heads * head_dim;
+  const size_t stat_floats = (size_t)tokens * max_chunks * query_heads * 4;
+  float* partials = nullptr;
+  if (int rc = check_hip(hipMalloc(&partials, (part_floats + stat_floats) * sizeof(float)),
+                         "hipMalloc(partials)"))
+    return rc;
+  int rc = device_put_step(dev, host_step(position, tokens));
+  if (rc == FRZ_OK) {
+    const float scale_log2e = (float)((double)scale * 1.4426950408889634);
+    AttentionArgs a{query,    q_stride, key_cache,  value_cache, out,       partials,
+                    partials + part_floats, slots, window, head_dim, query_heads,
+                    kv_heads, max_chunks, scale_log2e};
+    rc = device_finish(dev, launch_attention(dev->stream, dev->step, a, (int)tokens),
+                       "frz_op_attention");
+  }
+  (void)hipFree(partials);
+  return rc;
+}
+
+int frz_op_gather(frz_device* dev, const void* codes, const void* scales, int rows, int cols,
+                  const uint32_t* ids, uint32_t tokens, float scale, float* hidden) {
+  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gather: bad shape or tokens");
+  }
+  DevStep s = host_step(0, tokens);
+  std::memcpy(s.ids, ids, tokens * sizeof(uint32_t));
+  if (int rc = device_put_step(dev, s)) return rc;
+  return device_finish(dev,
+                       launch_gather(dev->stream, dev->step, q4(codes, scales, rows, cols),
+                                     nullptr, hidden, scale, (int)tokens),
+                       "frz_op_gather");
+}
+
+int frz_op_edit(frz_device* dev, const uint32_t* edits_dev, int layer, float* act, int width,
+                uint32_t position, uint32_t tokens) {
+  if (tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_edit: bad tokens");
+  }
+  if (int rc = device_put_step(dev, host_step(position, tokens))) return rc;
+  return device_finish(
+      dev, launch_edit(dev->stream, dev->step, edits_dev, layer, act, width, (int)tokens),
+      "frz_op_edit");
+}
+
+int frz_op_topk(frz_device* dev, const float* logits, int count, uint32_t* candidates_dev) {
+  if (count < kCandidates) return fail(FRZ_ERR_ARGUMENT, "frz_op_topk: fewer than 64 logits");
+  const int tiles = (count + kSelectionTile - 1) / kSelectionTile;
+  const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
+  uint32_t* scratch = nullptr;
+  if (int rc = check_hip(hipMalloc(&scratch, (size_t)2 * kCandidates * (tiles + second) * 4),
+                         "hipMalloc(topk)"))
+    return rc;
+  const int rc =
+      device_finish(dev, launch_topk(dev->stream, logits, count, scratch, candidates_dev),
+                    "frz_op_topk");
+  (void)hipFree(scratch);
+  return rc;
+}
+
+int frz_op_draw(frz_device* dev, const uint32_t* candidates_dev, const frz_sampling* sampling,
+                uint32_t position, uint32_t tokens, uint32_t* record_dev) {
+  if (sampling && (sampling->top_k < 1 || sampling->top_k > (uint32_t)kCandidates)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_draw: top_k outside 1..64");
+  }
+  DevStep s = host_step(position, tokens);
+  fill_sampling(s, sampling);
+  if (int rc = device_put_step(dev, s)) return rc;
+  return device_finish(
+      dev, launch_draw(dev->stream, dev->step, candidates_dev, record_dev, nullptr),
+      "frz_op_draw");
+}
+
+int frz_op_numerics(frz_device* dev, int which, const float* in_dev, float* out_dev, int n) {
+  if (n <= 0) return fail(FRZ_ERR_ARGUMENT, "frz_op_numerics: n <= 0");
+  hipLaunchKernelGGL(numerics_kernel, dim3((n + 255) / 256), dim3(256), 0, dev->stream, which,
+                     in_dev, out_dev, n);
+  return device_finish(dev, hipGetLastError(), "frz_op_numerics");
+}
+
+int frz_bench_gemv(frz_device* dev, const void* const* codes, const void* const* scales,
+                   int copies, int rows, int cols, const float* x, float* y, int iters,
+                   double* us_per_launch) {
+  if (!shape_ok(rows, cols) || copies <= 0 || iters <= 0 || !us_per_launch) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_bench_gemv: bad argument");
+  }
+  if (int rc = device_put_step(dev, host_step(0, 1))) return rc;
+  hipEvent_t start, stop;
+  (void)hipEventCreate(&start);
+  (void)hipEventCreate(&stop);
+  for (int i = 0; i < copies; ++i) {  // warm: every copy once
+    (void)launch_gemv(dev->stream, dev->step, q4(codes[i], scales[i], rows, cols), x, cols, y, rows, 1,
+                false);
+  }
+  (void)hipEventRecord(start, dev->stream);
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < iters && e == hipSuccess; ++i) {
+    const int c = i % copies;
+    e = launch_gemv(dev->stream, dev->step, q4(codes[c], scales[c], rows, cols), x, cols, y,
+                    rows, 1, false);
+  }
+  (void)hipEventRecord(stop, dev->stream);
+  int rc = check_hip(e, "frz_bench_gemv launch");
+  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), "hipEventSynchronize");
+  float ms = 0.0f;
+  if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, start, stop);
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
+  *us_per_launch = (double)ms * 1000.0 / iters;
+  return rc;
+}
+
+int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
+                    const void* const* gate_scales, const void* const* up_codes,
+                    const void* const* up_scales, int copies, int rows, int cols,
+                    const float* x, float* act, int iters, double* us_per_launch) {
+  if (!shape_ok(rows, cols) || copies <= 0 || iters <= 0 || !us_per_launch) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_bench_gated: bad argument");
+  }
+  if (int rc = device_put_step(dev, host_step(0, 1))) return rc;
+  hipEvent_t start, stop;
+  (void)hipEventCreate(&start);
+  (void)hipEventCreate(&stop);
+  auto launch = [&](int c) {
+    return launch_gated(dev->stream, dev->step, q4(gate_codes[c], gate_scales[c], rows, cols),
+                        q4(up_codes[c], up_scales[c], rows, cols), x, act, 1, nullptr, 0);
+  };
+  for (int i = 0; i < copies; ++i) (void)launch(i);
+  (void)hipEventRecord(start, dev->stream);
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < iters && e == hipSuccess; ++i) e = launch(i % copies);
+  (void)hipEventRecord(stop, dev->stream);
+  int rc = check_hip(e, "frz_bench_gated launch");
+  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), "hipEventSynchronize");
+  float ms = 0.0f;
+  if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, start, stop);
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
+  *us_per_launch = (double)ms * 1000.0 / iters;
+  return rc;
+}
+
+void frz_rope_turns(float base, int head_dim, float* turns) {
+  const double pi = 3.14159265358979323846;
+  for (int k = 0; k < head_dim / 2; ++k) {
+    const double theta = std::pow((double)base, -2.0 * k / head_dim);
+    turns[k] = (float)(theta / (2 * pi));
+  }
+}
+
+}  // extern "C"

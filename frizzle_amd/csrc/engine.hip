@@ -1,0 +1,717 @@
+// The Gemma-3 model on the device and its steps: weights in the split Q4_0
+// layout, F16 KV caches (a ring for sliding layers), the working buffers of a
+// 512-token block, the graph of launches in the reference's order
+// (src/core/graph/graph.cpp:290-470), one captured HIP graph for a fed decode
+// step, and generation with prefix reuse.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <tuple>
+#include <vector>
+
+#include "../../include/frizzle_hip.h"
+#include "backend.h"
+#include "kernels.h"
+#include "numerics.h"
+
+using namespace frz;
+
+namespace {
+
+constexpr uint32_t kToTheEnd = 0xFFFFFFFFu;  // edit/edit.h: kToTheEnd
+constexpr int kMaxEdits = 4096;              // edit/edit.h: kMaxEdits
+
+// ---- the synthetic weights -------------------------------------------------
+// SplitMix64 (Steele, Lea, Flood 2014), one stream per (seed, layer, role).
+struct SplitMix64 {
+  uint64_t state;
+  uint64_t next() {
+    uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  // Uniform in (0, 1): 53 bits, offset by half a unit.
+  double uniform() { return ((double)(next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+  // N(0, 1) by Box-Muller in f64, one value per two uniforms.
+  double normal() {
+    const double u1 = uniform(), u2 = uniform();
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+  }
+};
+
+SplitMix64 stream_of(uint64_t seed, int layer, int role) {
+  SplitMix64 s{seed ^ (0x6A09E667F3BCC909ull * (uint64_t)(layer + 2)) ^
+               (0xBB67AE8584CAA73Bull * (uint64_t)(role + 1))};
+  s.next();
+  return s;
+}
+
+bool is_matrix(int role) { return role <= FRZ_ROLE_DOWN || role == FRZ_ROLE_EMBEDDING; }
+
+// A matrix role's rows and columns (N rows of K, matmul.h:19-22).
+void matrix_shape(const frz_model_config& c, int role, int* rows, int* cols) {
+  const int q = c.query_heads * c.head_dim, kv = c.kv_heads * c.head_dim;
+  switch (role) {
+    case FRZ_ROLE_Q: *rows = q; *cols = c.hidden; break;
+    case FRZ_ROLE_K:
+    case FRZ_ROLE_V: *rows = kv; *cols = c.hidden; break;
+    case FRZ_ROLE_O: *rows = c.hidden; *cols = q; break;
+    case FRZ_ROLE_GATE:
+    case FRZ_ROLE_UP: *rows = c.ffn; *cols = c.hidden; break;
+    case FRZ_ROLE_DOWN: *rows = c.hidden; *cols = c.ffn; break;
+    case FRZ_ROLE_EMBEDDING: *rows = c.vocab; *cols = c.hidden; break;
+    default: *rows = 0; *cols = 0; break;
+  }
+}
+
+int gain_width(const frz_model_config& c, int role) {
+  return (role == FRZ_ROLE_Q_NORM || role == FRZ_ROLE_K_NORM) ? c.head_dim : c.hidden;
+}
+
+bool is_global(const frz_model_config& c, int layer) {
+  return layer % c.pattern == c.pattern - 1;
+}
+
+struct Layer {
+  Q4Matrix qkv;  // Q rows, then K, then V (one product, matmul.h:27-33)
+  Q4Matrix o, gate, up, down;
+  float* gains[6];  // attn, q, k, post_attn, ffn, post_ffn
+  uint16_t* kcache;
+  uint16_t* vcache;
+  float* turns;
+  int slots;
+  int window;
+  int max_chunks;
+};
+
+}  // namespace
+
+struct frz_model {
+  frz_device* dev = nullptr;
+  frz_model_config c{};
+  std::vector<void*> owned;
+  std::vector<Layer> layers;
+  Q4Matrix embedding{};
+  float* output_norm = nullptr;
+  // working buffers, a prefill block of rows each
+  float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr,
+        *output = nullptr, *act = nullptr, *logits = nullptr, *partials = nullptr,
+        *stats = nullptr;
+  uint32_t *topk_scratch = nullptr, *candidates = nullptr, *sampled = nullptr,
+           *token_log = nullptr, *edits = nullptr;
+  uint32_t token_log_capacity = 0;
+  size_t partial_floats = 0;
+  DevStep* step = nullptr;       // device
+  DevStep* step_host = nullptr;  // pinned
+  hipGraphExec_t decode_exec = nullptr;
+  hipGraph_t decode_graph = nullptr;
+  // generation state: the tokens whose keys and values the caches hold, and
+  // the placed edit table they were computed under
+  std::vector<uint32_t> cached;
+  std::vector<uint32_t> cached_edits;
+  uint64_t written_end = 0;  // one past the last position any step wrote
+  std::vector<uint32_t> edit_words;
+};
+
+namespace {
+
+template <typename T>
+int alloc(frz_model* m, T** p, size_t bytes) {
+  void* v = nullptr;
+  if (int rc = check_hip(hipMalloc(&v, bytes ? bytes : 1), "hipMalloc")) return rc;
+  m->owned.push_back(v);
+  *p = static_cast<T*>(v);
+  return FRZ_OK;
+}
+
+int alloc_q4(frz_model* m, Q4Matrix* w, int rows, int cols) {
+  const size_t blocks = (size_t)rows * cols / 32;
+  uint8_t* codes;
+  uint16_t* scales;
+  if (int rc = alloc(m, &codes, blocks * 16)) return rc;
+  if (int rc = alloc(m, &scales, blocks * 2)) return rc;
+  *w = Q4Matrix{codes, scales, rows, cols};
+  return FRZ_OK;
+}
+
+// Writes GGUF Q4_0 blocks into rows [row0, row0 + rows) of a device matrix.
+int upload_q4(frz_model* m, const Q4Matrix& w, int row0, int rows, const void* data) {
+  const size_t blocks = (size_t)rows * w.cols / 32;
+  const size_t first = (size_t)row0 * w.cols / 32;
+  std::vector<uint8_t> codes(blocks * 16), scales(blocks * 2);
+  frz_q4_0_split(data, blocks, codes.data(), scales.data());
+  hipStream_t s = m->dev->stream;
+  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint8_t*>(w.codes) + first * 16, codes.data(),
+                                        codes.size(), hipMemcpyHostToDevice, s),
+                         "upload codes"))
+    return rc;
+  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint16_t*>(w.scales) + first, scales.data(),
+                                        scales.size(), hipMemcpyHostToDevice, s),
+                         "upload scales"))
+    return rc;
+  return check_hip(hipStreamSynchronize(s), "upload sync");
+}
+
+// Enqueues one step's launches, in the graph's order: the embedding; per
+// layer the attention norm (adding the last block's post-normed output),
+// Q/K/V, rope and the cache append, attention, O; the feed-forward norm,
+// gate-up with GELU and the pins, down; then the final norm of the last row
+// and, with logits, the head, the selection and the draw.
+int enqueue_step(frz_model* m, int max_tokens, bool logits) {
+  const frz_model_config& c = m->c;
+  hipStream_t s = m->dev->stream;
+  const int H = c.hidden, qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
+  const int qkv_stride = qw + 2 * kvw;
+  const float scale_log2e = (float)((double)(1.0f / std::sqrt((float)c.head_dim)) *
+                                    1.4426950408889634);
+  hipError_t e = launch_gather(s, m->step, m->embedding, m->sampled, m->hidden,
+                               std::sqrt((float)H), max_tokens);
+  const float* pending = nullptr;
+  for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+    const Layer& L = m->layers[l];
+    NormArgs attn_norm{L.gains[0], pending, m->output, m->hidden, m->normed,
+                       c.epsilon, H, false};
+    e = launch_norm(s, m->step, attn_norm, max_tokens);
+    if (e == hipSuccess)
+      e = launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens, false);
+    if (e == hipSuccess) {
+      RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     m->qkv + qw,
+                 m->qkv + qw + kvw, qkv_stride, qkv_stride, L.kcache, L.vcache,
+                 L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon};
+      e = launch_rope(s, m->step, r, max_tokens);
+    }
+    if (e == hipSuccess) {
+      AttentionArgs a{m->qkv,     qkv_stride, L.kcache,     L.vcache,       m->attn,
+                      m->partials, m->partials + m->partial_floats, L.slots, L.window,
+                      c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e};
+      e = launch_attention(s, m->step, a, max_tokens);
+    }
+    if (e == hipSuccess)
+      e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);
+    if (e == hipSuccess) {
+      NormArgs ffn_norm{L.gains[4], L.gains[3], m->output, m->hidden, m->normed,
+                        c.epsilon, H, false};
+      e = launch_norm(s, m->step, ffn_norm, max_tokens);
+    }
+    if (e == hipSuccess)
+      e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens, m->edits, l);
+    if (e == hipSuccess)
+      e = launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
+    pending = L.gains[5];
+  }
+  if (e == hipSuccess) {
+    NormArgs final_norm{m->output_norm, pending, m->output, m->hidden, m->normed,
+                        c.epsilon, H, true};
+    e = launch_norm(s, m->step, final_norm, max_tokens);
+  }
+  if (logits && e == hipSuccess) {
+    e = launch_gemv(s, m->step, m->embedding, m->normed, H, m->logits, c.vocab, max_tokens, true);
+    if (e == hipSuccess) e = launch_topk(s, m->logits, c.vocab, m->topk_scratch, m->candidates);
+    if (e == hipSuccess) e = launch_draw(s, m->step, m->candidates, m->sampled, m->token_log);
+  }
+  return check_hip(e, "enqueue_step");
+}
+
+int build_decode_graph(frz_model* m) {
+  if (m->decode_exec) return FRZ_OK;
+  hipStream_t s = m->dev->stream;
+  if (int rc = check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal),
+                         "hipStreamBeginCapture"))
+    return rc;
+  int rc = enqueue_step(m, 1, true);
+  if (rc == FRZ_OK) rc = check_hip(launch_advance(s, m->step), "advance");
+  hipGraph_t graph = nullptr;
+  const int end_rc = check_hip(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+  if (rc != FRZ_OK) return rc;
+  if (end_rc != FRZ_OK) return end_rc;
+  m->decode_graph = graph;
+  return check_hip(hipGraphInstantiate(&m->decode_exec, graph, nullptr, nullptr, 0),
+                   "hipGraphInstantiate");
+}
+
+int put_step(frz_model* m) {
+  hipStream_t s = m->dev->stream;
+  if (int rc = check_hip(hipMemcpyAsync(m->step, m->step_host, sizeof(DevStep),
+                                        hipMemcpyHostToDevice, s),
+                         "step copy"))
+    return rc;
+  // The pinned record may be rewritten by the next call only once copied.
+  return check_hip(hipStreamSynchronize(s), "step copy sync");
+}
+
+// The placed edit table (edit.cpp:136-161 with place(), edit.cpp:35-38):
+// step-relative ranges moved to positions origin + step, saturating.
+std::vector<uint32_t> place_table(const frz_model_config& c, const uint32_t* table,
+                                  uint32_t words, uint32_t origin) {
+  std::vector<uint32_t> out(table, table + words);
+  if (words < (uint32_t)(2 * c.layers)) out.assign(2 * c.layers, 0);
+  auto place = [origin](uint32_t step) -> uint32_t {
+    if (step == kToTheEnd || step > kToTheEnd - origin) return kToTheEnd;
+    return step + origin;
+  };
+  for (int l = 0; l < c.layers; ++l) {
+    const uint32_t first = out[2 * l], count = out[2 * l + 1];
+    for (uint32_t i = 0; i < count; ++i) {
+      const size_t at = first + 5 * (size_t)i;
+      if (at + 4 >= out.size()) break;
+      out[at + 3] = place(out[at + 3]);
+      out[at + 4] = place(out[at + 4]);
+    }
+  }
+  return out;
+}
+
+// The first position at which two placed tables can act differently: the
+// least first position among edits one holds and the other does not
+// (cache/prefix.h:87-94, first_edit_difference).
+uint32_t first_edit_difference(const frz_model_config& c, const std::vector<uint32_t>& a,
+                               const std::vector<uint32_t>& b) {
+  using Key = std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;
+  auto edits_of = [&c](const std::vector<uint32_t>& t) {
+    std::map<Key, int> out;
+    for (int l = 0; l < c.layers && (size_t)(2 * l + 1) < t.size(); ++l) {
+      const uint32_t first = t[2 * l], count = t[2 * l + 1];
+      for (uint32_t i = 0; i < count; ++i) {
+        const size_t at = first + 5 * (size_t)i;
+        if (at + 4 >= t.size()) break;
+        out[Key{(uint32_t)l, t[at], t[at + 1], t[at + 2], t[at + 3], t[at + 4]}] += 1;
+      }
+    }
+    return out;
+  };
+  const auto ea = edits_of(a), eb = edits_of(b);
+  uint32_t least = kToTheEnd;
+  for (const auto& [k, n] : ea) {
+    if (eb.find(k) == eb.end()) least = std::min(least, std::get<4>(k));
+  }
+  for (const auto& [k, n] : eb) {
+    if (ea.find(k) == ea.end()) least = std::min(least, std::get<4>(k));
+  }
+  return least;
+}
+
+}  // namespace
+
+extern "C" {
+
+void frz_gemma3_1b_config(frz_model_config* out, int context) {
+  frz_model_config c{};
+  c.hidden = 1152;
+  c.ffn = 6912;
+  c.head_dim = 256;
+  c.query_heads = 4;
+  c.kv_heads = 1;
+  c.layers = 26;
+  c.vocab = 262144;
+  c.window = 512;
+  c.pattern = 6;
+  c.context = context > 0 ? context : 8192;
+  c.local_slots = 512 + 512 + 4096;  // plan.h:50-55: window + block + reserve
+  c.rope_local = 10000.0f;
+  c.rope_global = 1000000.0f;
+  c.epsilon = 1e-6f;
+  *out = c;
+}
+
+uint64_t frz_tensor_bytes(const frz_model_config* config, int role) {
+  if (is_matrix(role)) {
+    int rows, cols;
+    matrix_shape(*config, role, &rows, &cols);
+    return (uint64_t)rows * cols / 32 * 18;
+  }
+  if (role == FRZ_ROLE_OUTPUT_NORM) return (uint64_t)config->hidden * 4;
+  if (role >= FRZ_ROLE_ATTN_NORM && role <= FRZ_ROLE_POST_FFN_NORM)
+    return (uint64_t)gain_width(*config, role) * 4;
+  return 0;
+}
+
+int frz_synth_tensor(const frz_model_config* config, uint64_t seed, int layer, int role,
+                     void* out, uint64_t bytes) {
+  if (!config || !out) return fail(FRZ_ERR_ARGUMENT, "frz_synth_tensor: null argument");
+  if (bytes != frz_tensor_bytes(config, role) || bytes == 0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_synth_tensor: wrong size for the role");
+  }
+  SplitMix64 rng = stream_of(seed, layer, role);
+  if (is_matrix(role)) {
+    uint8_t* p = static_cast<uint8_t*>(out);
+    const uint64_t blocks = bytes / 18;
+    for (uint64_t b = 0; b < blocks; ++b) {
+      const uint16_t d = f16_pack((float)std::fabs(0.02 * rng.normal()));
+      p[18 * b] = (uint8_t)(d & 0xFF);
+      p[18 * b + 1] = (uint8_t)(d >> 8);
+      const uint64_t c0 = rng.next(), c1 = rng.next();
+      for (int i = 0; i < 8; ++i) {
+        p[18 * b + 2 + i] = (uint8_t)(c0 >> (8 * i));
+        p[18 * b + 10 + i] = (uint8_t)(c1 >> (8 * i));
+      }
+    }
+  } else {
+    float* g = static_cast<float*>(out);
+    for (uint64_t i = 0; i < bytes / 4; ++i) g[i] = (float)(1.0 + 0.1 * rng.normal());
+  }
+  return FRZ_OK;
+}
+
+int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model** out) {
+  if (!dev || !config || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_create: null argument");
+  const frz_model_config& c = *config;
+  if (c.head_dim != 256 || c.query_heads != 4 * c.kv_heads || c.hidden % 32 != 0 ||
+      c.ffn % 32 != 0 || c.vocab < kCandidates || c.layers <= 0 || c.pattern <= 0 ||
+      c.window <= 0 || c.context < kPrefillBlock || c.local_slots < c.window + kPrefillBlock ||
+      c.hidden > 4096) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_create: unsupported shape");
+  }
+  (void)hipSetDevice(dev->ordinal);
+  frz_model* m = new frz_model();
+  m->dev = dev;
+  m->c = c;
+  auto bail = [m](int rc) {
+    frz_model_destroy(m);
+    return rc;
+  };
+  const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
+  size_t max_partials = 0;
+  m->layers.resize(c.layers);
+  for (int l = 0; l < c.layers; ++l) {
+    Layer& L = m->layers[l];
+    if (int rc = alloc_q4(m, &L.qkv, qw + 2 * kvw, c.hidden)) return bail(rc);
+    if (int rc = alloc_q4(m, &L.o, c.hidden, qw)) return bail(rc);
+    if (int rc = alloc_q4(m, &L.gate, c.ffn, c.hidden)) return bail(rc);
+    if (int rc = alloc_q4(m, &L.up, c.ffn, c.hidden)) return bail(rc);
+    if (int rc = alloc_q4(m, &L.down, c.hidden, c.ffn)) return bail(rc);
+    for (int g = 0; g < 6; ++g) {
+      const int role = FRZ_ROLE_ATTN_NORM + g;
+      if (int rc = alloc(m, &L.gains[g], (size_t)gain_width(c, role) * 4)) return bail(rc);
+    }
+    const bool global = is_global(c, l);
+    L.slots = global ? c.context : c.local_slots;
+    L.window = global ? c.context : c.window;
+    L.max_chunks = attention_max_chunks(L.window, L.slots);
+    max_partials = std::max(max_partials, (size_t)kPrefillBlock * L.max_chunks * qw);
+    const size_t cache = (size_t)L.slots * kvw * 2;
+    if (int rc = alloc(m, &L.kcache, cache)) return bail(rc);
+    if (int rc = alloc(m, &L.vcache, cache)) return bail(rc);
+    (void)hipMemsetAsync(L.kcache, 0, cache, dev->stream);
+    (void)hipMemsetAsync(L.vcache, 0, cache, dev->stream);
+    std::vector<float> turns(c.head_dim / 2);
+    frz_rope_turns(global ? c.rope_global : c.rope_local, c.head_dim, turns.data());
+    if (int rc = alloc(m, &L.turns, turns.size() * 4)) return bail(rc);
+    (void)hipMemcpy(L.turns, turns.data(), turns.size() * 4, hipMemcpyHostToDevice);
+  }
+  if (int rc = alloc_q4(m, &m->embedding, c.vocab, c.hidden)) return bail(rc);
+  if (int rc = alloc(m, &m->output_norm, (size_t)c.hidden * 4)) return bail(rc);
+  const size_t B = kPrefillBlock;
+  m->partial_floats = max_partials;
+  if (int rc = alloc(m, &m->hidden, B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->normed, B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->qkv, B * (qw + 2 * kvw) * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->attn, B * qw * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->output, B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->act, B * c.ffn * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->logits, (size_t)c.vocab * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
+  const int tiles = (c.vocab + kSelectionTile - 1) / kSelectionTile;
+  const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
+  if (int rc = alloc(m, &m->topk_scratch, (size_t)2 * kCandidates * (tiles + second) * 4))
+    return bail(rc);
+  if (int rc = alloc(m, &m->candidates, 2 * kCandidates * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->sampled, 4 * 4)) return bail(rc);
+  m->token_log_capacity = 1u << 16;
+  if (int rc = alloc(m, &m->token_log, (size_t)2 * m->token_log_capacity * 4)) return bail(rc);
+  const size_t edit_words = 2 * (size_t)c.layers + 5 * (size_t)kMaxEdits;
+  if (int rc = alloc(m, &m->edits, edit_words * 4)) return bail(rc);
+  (void)hipMemsetAsync(m->edits, 0, edit_words * 4, dev->stream);
+  (void)hipMemsetAsync(m->sampled, 0, 16, dev->stream);
+  (void)hipMemsetAsync(m->output, 0, B * c.hidden * 4, dev->stream);
+  if (int rc = alloc(m, &m->step, sizeof(DevStep))) return bail(rc);
+  if (int rc = check_hip(hipHostMalloc((void**)&m->step_host, sizeof(DevStep)), "hipHostMalloc"))
+    return bail(rc);
+  std::memset(m->step_host, 0, sizeof(DevStep));
+  m->edit_words.assign(2 * c.layers, 0);
+  if (int rc = check_hip(hipStreamSynchronize(dev->stream), "create sync")) return bail(rc);
+  *out = m;
+  return FRZ_OK;
+}
+
+void frz_model_destroy(frz_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->dev->ordinal);
+  (void)hipStreamSynchronize(m->dev->stream);
+  if (m->decode_exec) hipGraphExecDestroy(m->decode_exec);
+  if (m->decode_graph) hipGraphDestroy(m->decode_graph);
+  for (void* p : m->owned) hipFree(p);
+  if (m->step_host) hipHostFree(m->step_host);
+  delete m;
+}
+
+int frz_model_set_tensor(frz_model* m, int layer, int role, const void* data, uint64_t bytes) {
+  if (!m || !data) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: null argument");
+  const frz_model_config& c = m->c;
+  if (bytes != frz_tensor_bytes(&c, role) || bytes == 0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: wrong size for the role");
+  }
+  if (role == FRZ_ROLE_EMBEDDING || role == FRZ_ROLE_OUTPUT_NORM) {
+    if (layer != -1) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: global tensor, layer -1");
+    if (role == FRZ_ROLE_EMBEDDING) return upload_q4(m, m->embedding, 0, c.vocab, data);
+    return check_hip(hipMemcpy(m->output_norm, data, bytes, hipMemcpyHostToDevice), "upload");
+  }
+  if (layer < 0 || layer >= c.layers) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: layer");
+  Layer& L = m->layers[layer];
+  const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
+  switch (role) {
+    case FRZ_ROLE_Q: return upload_q4(m, L.qkv, 0, qw, data);
+    case FRZ_ROLE_K: return upload_q4(m, L.qkv, qw, kvw, data);
+    case FRZ_ROLE_V: return upload_q4(m, L.qkv, qw + kvw, kvw, data);
+    case FRZ_ROLE_O: return upload_q4(m, L.o, 0, c.hidden, data);
+    case FRZ_ROLE_GATE: return upload_q4(m, L.gate, 0, c.ffn, data);
+    case FRZ_ROLE_UP: return upload_q4(m, L.up, 0, c.ffn, data);
+    case FRZ_ROLE_DOWN: return upload_q4(m, L.down, 0, c.hidden, data);
+    default:
+      return check_hip(hipMemcpy(L.gains[role - FRZ_ROLE_ATTN_NORM], data, bytes,
+                                 hipMemcpyHostToDevice),
+                       "upload gain");
+  }
+}
+
+int frz_model_synthesize(frz_model* m, uint64_t seed) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_synthesize: null model");
+  std::vector<uint8_t> buf;
+  auto one = [&](int layer, int role) {
+    const uint64_t bytes = frz_tensor_bytes(&m->c, role);
+    buf.resize(bytes);
+    if (int rc = frz_synth_tensor(&m->c, seed, layer, role, buf.data(), bytes)) return rc;
+    return frz_model_set_tensor(m, layer, role, buf.data(), bytes);
+  };
+  for (int l = 0; l < m->c.layers; ++l) {
+    for (int role = FRZ_ROLE_Q; role <= FRZ_ROLE_POST_FFN_NORM; ++role) {
+      if (int rc = one(l, role)) return rc;
+    }
+  }
+  if (int rc = one(-1, FRZ_ROLE_EMBEDDING)) return rc;
+  return one(-1, FRZ_ROLE_OUTPUT_NORM);
+}
+
+int frz_model_set_edits(frz_model* m, const uint32_t* table, uint32_t words) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: null model");
+  const size_t cap = 2 * (size_t)m->c.layers + 5 * (size_t)kMaxEdits;
+  std::vector<uint32_t> t;
+  if (table && words) t.assign(table, table + words);
+  if (t.size() < (size_t)(2 * m->c.layers)) t.resize(2 * m->c.layers, 0);
+  if (t.size() > cap) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: more than 4096 edits");
+  for (int l = 0; l < m->c.layers; ++l) {
+    const uint64_t first = t[2 * l], count = t[2 * l + 1];
+    if (count && first + 5 * count > t.size()) {
+      return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: a layer's edits run past the table");
+    }
+    for (uint64_t i = 0; i < count; ++i) {
+      const uint32_t* e = t.data() + first + 5 * i;
+      if (e[0] >= (uint32_t)m->c.ffn || e[1] > 2u) {
+        return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: neuron or kind out of range");
+      }
+      if (i > 0 && e[0] < e[-5]) {
+        return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: a layer's edits are not by neuron");
+      }
+    }
+  }
+  m->edit_words = t;
+  if (int rc = check_hip(hipMemcpyAsync(m->edits, t.data(), t.size() * 4, hipMemcpyHostToDevice,
+                                        m->dev->stream),
+                         "edit table"))
+    return rc;
+  return check_hip(hipStreamSynchronize(m->dev->stream), "edit table sync");
+}
+
+int frz_model_step(frz_model* m, uint32_t position, uint32_t tokens, const uint32_t* ids,
+                   int logits, const frz_sampling* sampling) {
+  if (!m || !ids || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_step: 1 to 512 tokens");
+  }
+  if ((uint64_t)position + tokens > (uint64_t)m->c.context) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_step: past the context");
+  }
+  for (uint32_t i = 0; i < tokens; ++i) {
+    if (ids[i] >= (uint32_t)m->c.vocab) return fail(FRZ_ERR_ARGUMENT, "frz_model_step: token id");
+  }
+  if (sampling && (sampling->top_k < 1 || sampling->top_k > (uint32_t)kCandidates)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_step: top_k outside 1..64");
+  }
+  DevStep& s = *m->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.position = position;
+  s.tokens = tokens;
+  s.logits = logits ? 1 : 0;
+  s.fed = 0;
+  s.drawn = 0;
+  fill_sampling(s, sampling);
+  std::memcpy(s.ids, ids, tokens * 4);
+  if (int rc = put_step(m)) return rc;
+  return enqueue_step(m, (int)tokens, logits != 0);
+}
+
+int frz_model_decode(frz_model* m, uint32_t position, uint32_t steps,
+                     const frz_sampling* sampling, uint32_t* tokens_out, uint32_t* failed_out) {
+  if (!m || !tokens_out) return fail(FRZ_ERR_ARGUMENT, "frz_model_decode: null argument");
+  if (steps == 0) return FRZ_OK;
+  if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_decode: too many steps for the context");
+  }
+  if (int rc = build_decode_graph(m)) return rc;
+  DevStep& s = *m->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.position = position;
+  s.tokens = 1;
+  s.logits = 1;
+  s.fed = 1;
+  s.drawn = 0;
+  fill_sampling(s, sampling);
+  if (int rc = put_step(m)) return rc;
+  for (uint32_t i = 0; i < steps; ++i) {
+    if (int rc = check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch"))
+      return rc;
+  }
+  std::vector<uint32_t> log(2 * (size_t)steps);
+  if (int rc = check_hip(hipMemcpyAsync(log.data(), m->token_log, log.size() * 4,
+                                        hipMemcpyDeviceToHost, m->dev->stream),
+                         "token log"))
+    return rc;
+  if (int rc = check_hip(hipStreamSynchronize(m->dev->stream), "decode sync")) return rc;
+  for (uint32_t i = 0; i < steps; ++i) {
+    tokens_out[i] = log[2 * i];
+    if (failed_out) failed_out[i] = log[2 * i + 1];
+  }
+  return FRZ_OK;
+}
+
+int frz_model_time_decode(frz_model* m, uint32_t position, uint32_t steps,
+                          const frz_sampling* sampling, double* us_per_step) {
+  if (!m || !us_per_step || steps == 0) return fail(FRZ_ERR_ARGUMENT, "frz_model_time_decode");
+  if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_time_decode: too many steps for the context");
+  }
+  if (int rc = build_decode_graph(m)) return rc;
+  DevStep& s = *m->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.position = position;
+  s.tokens = 1;
+  s.logits = 1;
+  s.fed = 1;
+  fill_sampling(s, sampling);
+  if (int rc = put_step(m)) return rc;
+  hipEvent_t a, b;
+  (void)hipEventCreate(&a);
+  (void)hipEventCreate(&b);
+  (void)hipEventRecord(a, m->dev->stream);
+  int rc = FRZ_OK;
+  for (uint32_t i = 0; i < steps && rc == FRZ_OK; ++i) {
+    rc = check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch");
+  }
+  (void)hipEventRecord(b, m->dev->stream);
+  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(b), "hipEventSynchronize");
+  float ms = 0.0f;
+  if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *us_per_step = (double)ms * 1000.0 / steps;
+  return rc;
+}
+
+static int read_back(frz_model* m, void* out, const void* src, size_t bytes) {
+  if (int rc = check_hip(hipMemcpyAsync(out, src, bytes, hipMemcpyDeviceToHost, m->dev->stream),
+                         "read back"))
+    return rc;
+  return check_hip(hipStreamSynchronize(m->dev->stream), "read back sync");
+}
+
+int frz_model_read_logits(frz_model* m, float* out, uint32_t count) {
+  if (!m || !out || count > (uint32_t)m->c.vocab) return fail(FRZ_ERR_ARGUMENT, "read_logits");
+  return read_back(m, out, m->logits, (size_t)count * 4);
+}
+
+int frz_model_read_record(frz_model* m, uint32_t record[4]) {
+  if (!m || !record) return fail(FRZ_ERR_ARGUMENT, "read_record");
+  return read_back(m, record, m->sampled, 16);
+}
+
+int frz_model_read_candidates(frz_model* m, uint32_t out[128]) {
+  if (!m || !out) return fail(FRZ_ERR_ARGUMENT, "read_candidates");
+  return read_back(m, out, m->candidates, 128 * 4);
+}
+
+int frz_model_read_hidden(frz_model* m, float* out, uint32_t rows) {
+  if (!m || !out || rows > (uint32_t)kPrefillBlock) return fail(FRZ_ERR_ARGUMENT, "read_hidden");
+  return read_back(m, out, m->normed, (size_t)rows * m->c.hidden * 4);
+}
+
+int frz_model_read_cache(frz_model* m, int layer, int values, uint16_t* out, uint64_t count) {
+  if (!m || !out || layer < 0 || layer >= m->c.layers) return fail(FRZ_ERR_ARGUMENT, "read_cache");
+  const Layer& L = m->layers[layer];
+  const uint64_t cap = (uint64_t)L.slots * m->c.kv_heads * m->c.head_dim;
+  if (count > cap) return fail(FRZ_ERR_ARGUMENT, "read_cache: more than the cache holds");
+  return read_back(m, out, values ? L.vcache : L.kcache, count * 2);
+}
+
+int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
+                 const uint32_t* edit_table, uint32_t edit_words, const frz_sampling* sampling,
+                 uint32_t max_tokens, const uint32_t* stop_ids, uint32_t stops,
+                 uint32_t* tokens_out, uint32_t* drawn) {
+  if (!m || !prompt || prompt_len == 0 || !tokens_out || !drawn) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_generate: null argument or empty prompt");
+  }
+  *drawn = 0;
+  const frz_model_config& c = m->c;
+  if ((uint64_t)prompt_len + max_tokens > (uint64_t)c.context) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_generate: prompt and reply exceed the context");
+  }
+  const uint32_t origin = prompt_len - 1;
+  std::vector<uint32_t> placed =
+      place_table(c, edit_table ? edit_table : nullptr, edit_table ? edit_words : 0, origin);
+  if (int rc = frz_model_set_edits(m, placed.data(), (uint32_t)placed.size())) return rc;
+  // Reuse: the longest prefix of cached tokens the prompt repeats, cut at the
+  // first position the edits act differently, and never past the prompt's
+  // last token, whose row draws the first reply token.
+  uint32_t common = 0;
+  while (common < m->cached.size() && common < prompt_len && m->cached[common] == prompt[common])
+    ++common;
+  common = std::min(common, first_edit_difference(c, m->cached_edits, placed));
+  common = std::min(common, prompt_len - 1);
+  // A sliding layer's ring must still hold the window before the resume.
+  if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
+  uint32_t pos = common;
+  while (pos < prompt_len) {
+    const uint32_t n = std::min<uint32_t>(kPrefillBlock, prompt_len - pos);
+    const bool last = pos + n == prompt_len;
+    if (int rc = frz_model_step(m, pos, n, prompt + pos, last ? 1 : 0, sampling)) return rc;
+    pos += n;
+  }
+  m->cached.assign(prompt, prompt + prompt_len);
+  m->cached_edits = placed;
+  m->written_end = prompt_len;
+  if (max_tokens == 0) return check_hip(hipStreamSynchronize(m->dev->stream), "generate sync");
+  uint32_t record[4];
+  if (int rc = frz_model_read_record(m, record)) return rc;
+  std::vector<uint32_t> out{record[0]};
+  bool stopped = record[1] != 0 || std::find(stop_ids, stop_ids + stops, record[0]) != stop_ids + stops;
+  if (!stopped && max_tokens > 1) {
+    std::vector<uint32_t> more(max_tokens - 1), failed(max_tokens - 1);
+    if (int rc = frz_model_decode(m, prompt_len, max_tokens - 1, sampling, more.data(),
+                                  failed.data()))
+      return rc;
+    m->written_end = (uint64_t)prompt_len + max_tokens - 1;
+    for (uint32_t i = 0; i + 1 < max_tokens; ++i) {
+      out.push_back(more[i]);
+      if (failed[i] || std::find(stop_ids, stop_ids + stops, more[i]) != stop_ids + stops) break;
+    }
+    // The caches now hold every fed token; the last drawn is not yet fed.
+    for (uint32_t i = 0; i + 1 < out.size(); ++i) m->cached.push_back(out[i]);
+    // Decode ran past a stop: those positions hold tokens the reply does not
+    // keep, so the cached prefix ends at the reply's last fed token.
+  }
+  std::copy(out.begin(), out.end(), tokens_out);
+  *drawn = (uint32_t)out.size();
+  return FRZ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,135 @@
+// Host-side launchers of the forward path's HIP kernels, and the device
+// structures they share. Every launcher enqueues on the given stream and
+// returns the launch's hipError_t; none allocates or synchronizes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frz {
+
+constexpr int kRanges = 32;        // a row's K-ranges (matmul.h:88-97)
+constexpr int kChunkKeys = 64;     // attention chunk (attention.wgsl:60)
+constexpr int kTileKeys = 8;       // attention tile at d = 256
+constexpr int kCandidates = 64;    // top-k kept (residency/plan.h:195)
+constexpr int kSelectionTile = 1024;
+constexpr int kPrefillBlock = 512; // most tokens a step holds
+constexpr int kMaxHeadDim = 256;
+
+// The step's parameters, read by kernels from device memory, as the
+// reference's Step uniform (kernels/interface.h:163-188, step.wgsl). A
+// decode graph advances it on the device, so replays need no host write.
+struct DevStep {
+  uint32_t position;
+  uint32_t tokens;
+  uint32_t logits;
+  uint32_t fed;
+  uint32_t seed[2];
+  uint32_t top_k;
+  float temperature;
+  float top_p;
+  float min_p;
+  float log_min_p;
+  uint32_t drawn;     // draws recorded so far (index into the token log)
+  uint32_t pad[4];
+  uint32_t ids[kPrefillBlock];
+};
+
+// A Q4_0 matrix on the device: `rows` rows of `cols` weights as two streams,
+// every block's 16 code bytes in row-major block order, then every block's
+// fp16 scale (the reference's device layout, device_layout.h:114-115).
+struct Q4Matrix {
+  const uint8_t* codes;    // rows * cols / 32 blocks of 16 bytes
+  const uint16_t* scales;  // rows * cols / 32 halves
+  int rows;
+  int cols;
+};
+
+// ---- products ----------------------------------------------------------
+// y[t][o] = sum_k W[o][k] x[t][k] for t < step.tokens (or only the last
+// token when last_token), in the reference's order. Decode form when the
+// step holds one token; tiled form otherwise.
+hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
+                       const float* x, int x_stride, float* y, int y_stride,
+                       int max_tokens, bool last_token);
+// act[t][j] = gelu_tanh(gate_j) * up_j, then layer `layer`'s pins at the
+// row's position (edit table in the reference's layout; null for none).
+hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
+                        Q4Matrix up, const float* x, float* act,
+                        int max_tokens, const uint32_t* edits, int layer);
+
+// ---- per-row kernels ---------------------------------------------------
+struct NormArgs {
+  const float* gain;
+  const float* post_gain;  // null: no add
+  const float* output;     // the block's output y, added when post_gain
+  float* hidden;
+  float* normed;
+  float epsilon;
+  int width;
+  bool last_token;         // only the step's last row
+};
+hipError_t launch_norm(hipStream_t s, const DevStep* step, const NormArgs& a,
+                       int max_tokens);
+
+struct RopeArgs {
+  const float* turns;       // head_dim / 2
+  const float* query_gain;  // head_dim
+  const float* key_gain;
+  float* query;             // token t's heads at query + t * q_stride, in place
+  const float* key;         // token t's at key + t * kv_stride
+  const float* value;       // token t's at value + t * kv_stride
+  int q_stride;
+  int kv_stride;
+  uint16_t* key_cache;      // [slots][kv_heads][head_dim] F16
+  uint16_t* value_cache;
+  int slots;
+  int head_dim;
+  int query_heads;
+  int kv_heads;
+  float epsilon;
+};
+hipError_t launch_rope(hipStream_t s, const DevStep* step, const RopeArgs& a,
+                       int max_tokens);
+
+struct AttentionArgs {
+  const float* query;         // token t's roped heads at query + t * q_stride
+  int q_stride;
+  const uint16_t* key_cache;
+  const uint16_t* value_cache;
+  float* out;                 // [tokens][query_heads * head_dim]
+  float* partials;            // [tokens][max_chunks][query_heads][head_dim]
+  float* stats;               // [tokens][max_chunks][query_heads][4]
+  int slots;
+  int window;
+  int head_dim;
+  int query_heads;
+  int kv_heads;
+  int max_chunks;             // chunks a row may reach: the grid's width
+  float scale_log2e;
+};
+hipError_t launch_attention(hipStream_t s, const DevStep* step,
+                            const AttentionArgs& a, int max_tokens);
+
+hipError_t launch_gather(hipStream_t s, const DevStep* step, Q4Matrix table,
+                         const uint32_t* sampled, float* hidden, float scale,
+                         int max_tokens);
+hipError_t launch_edit(hipStream_t s, const DevStep* step,
+                       const uint32_t* edits, int layer, float* act,
+                       int width, int max_tokens);
+
+// ---- output ------------------------------------------------------------
+// Top-64 of `count` logits into candidates (64 x {bits, token}); `scratch`
+// holds 2 * 64 * ceil(count / 1024) + 2 * 64 * ceil(that / 1024) words.
+hipError_t launch_topk(hipStream_t s, const float* logits, int count,
+                       uint32_t* scratch, uint32_t* candidates);
+// The draw: record {token, failed, u bits, 0} into sampled; also appends
+// the token to token_log[step.drawn] when token_log is not null.
+hipError_t launch_draw(hipStream_t s, const DevStep* step,
+                       const uint32_t* candidates, uint32_t* sampled,
+                       uint32_t* token_log);
+// A fed step's advance: position += tokens, tokens = 1, fed = 1,
+// drawn += 1.
+hipError_t launch_advance(hipStream_t s, DevStep* step);
+
+}  // namespace frz

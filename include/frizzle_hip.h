@@ -1,0 +1,318 @@
+/*
+ * frizzle_hip.h — the C ABI of the MI355X (gfx950) backend for the Gemma-3-1B
+ * Q4_0 forward path.
+ *
+ * It takes the place of the reference's executor boundary: the Dawn/WebGPU
+ * device (src/core/gpu/device.h:132-198), buffer residency and upload
+ * (src/core/residency/upload.h:263-300), and the program that runs a step's
+ * launches (src/core/kernels/program.h:330-402), together with the WGSL
+ * kernels those launches name. Everything here is plain C: opaque handles,
+ * plain pointers and sizes, an int status (0 = ok) and a thread-local message
+ * from frz_last_error(). Nothing throws across this boundary.
+ *
+ * Device pointers ("dev") are addresses from frz_alloc on the same device.
+ * Host pointers are ordinary memory. Unless stated, calls enqueue work on the
+ * device's one stream and return without waiting; frz_sync waits.
+ */
+#ifndef FRIZZLE_HIP_H
+#define FRIZZLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, as the reference's ProgramError (src/core/kernels/program.h:
+ * 264-278) plus argument refusals. */
+enum frz_status {
+  FRZ_OK = 0,
+  FRZ_ERR_ARGUMENT = 1,    /* refused before any work: a bad size or shape */
+  FRZ_ERR_DEVICE = 2,      /* no device, or a HIP call failed */
+  FRZ_ERR_BUILD = 3,       /* a program could not be built */
+  FRZ_ERR_STEP = 4,        /* a step failed on the device */
+  FRZ_ERR_DEVICE_LOST = 5, /* the device stopped answering */
+  FRZ_ERR_CANCELLED = 6
+};
+
+/* The message of the calling thread's last failed call ("" when none). */
+const char* frz_last_error(void);
+
+/* ---- device (replaces gpu::Device::request, src/core/gpu/device.h:152-198) */
+typedef struct frz_device frz_device;
+
+typedef struct frz_limits {
+  char name[64];              /* the device's architecture name, "gfx950" */
+  uint64_t memory_bytes;      /* HBM on the device */
+  int compute_units;
+  int lds_bytes_per_block;
+} frz_limits;
+
+int frz_open(int ordinal, frz_device** out, frz_limits* limits);
+void frz_close(frz_device* dev);
+int frz_sync(frz_device* dev);
+
+/* ---- buffers (replaces residency::Upload::begin/write/buffer,
+ *      src/core/residency/upload.h:276-300) --------------------------------- */
+int frz_alloc(frz_device* dev, uint64_t bytes, void** dev_ptr);
+int frz_free(frz_device* dev, void* dev_ptr);
+/* Host to device and back; both wait for the copy. */
+int frz_write(frz_device* dev, void* dev_dst, const void* host_src, uint64_t bytes);
+int frz_read(frz_device* dev, void* host_dst, const void* dev_src, uint64_t bytes);
+int frz_fill_zero(frz_device* dev, void* dev_dst, uint64_t bytes);
+
+/* The Q4_0 upload transform (replaces residency::PieceWriter,
+ * src/core/residency/piece_writer.h:44-60, with the device layout of
+ * src/core/formats/device_layout.h:114-115): `blocks` GGUF Q4_0 blocks of 18
+ * bytes (an fp16 scale, then 16 code bytes) become two streams, every
+ * block's 16 code bytes, then every block's scale. Host to host. */
+int frz_q4_0_split(const void* gguf_blocks, uint64_t blocks, void* codes_out,
+                   void* scales_out);
+
+/* ---- one kernel at a time (the reference's launchers, each a Launch of
+ *      src/core/kernels/interface.h:320-363, run alone as the kernel contract
+ *      tests do, tests/support/scratch_program.h:62-80) -----------------------
+ * A Q4_0 matrix is `rows` rows of `cols` weights in the split layout above:
+ * codes (rows * cols / 32 * 16 bytes) and scales (rows * cols / 32 halves).
+ * `tokens` rows of input are processed from `position`. */
+
+/* y[t][o] = sum_k W[o][k] x[t][k] in the reference's order of addition
+ * (src/core/kernels/matmul/matmul.wgsl:154-244, 390-465): the decode form
+ * when tokens == 1 or last_token, the tiled form otherwise. */
+int frz_op_gemv(frz_device* dev, const void* codes, const void* scales,
+                int rows, int cols, const float* x, int x_stride, float* y,
+                int y_stride, uint32_t tokens, int last_token);
+/* act[t][j] = gelu_tanh(gate_j) * up_j with layer `layer`'s pins applied at
+ * position + t (matmul.wgsl:247-276 and src/core/edit/edit.wgsl:55-76 fused);
+ * edits_dev may be null for none. */
+int frz_op_gated(frz_device* dev, const void* gate_codes,
+                 const void* gate_scales, const void* up_codes,
+                 const void* up_scales, int rows, int cols, const float* x,
+                 float* act, uint32_t tokens, uint32_t position,
+                 const uint32_t* edits_dev, int layer);
+/* RMSNorm with the residual add and post-norm (kernels/norm/norm.wgsl:96-198).
+ * post_gain null: no add; otherwise hidden += postnorm(output). last_token:
+ * the step's last row only. */
+int frz_op_norm(frz_device* dev, const float* gain, const float* post_gain,
+                const float* output, float* hidden, float* normed, int width,
+                float epsilon, uint32_t tokens, int last_token);
+/* QK-norm, rope and the F16 KV append (kernels/rope/rope.wgsl,
+ * rope_cache.wgsl). turns: head_dim/2 floats from frz_rope_turns. Rows of
+ * query/key/value are q_stride / kv_stride floats apart. */
+int frz_op_rope(frz_device* dev, const float* turns, const float* query_gain,
+                const float* key_gain, float* query, const float* key,
+                const float* value, int q_stride, int kv_stride,
+                uint16_t* key_cache, uint16_t* value_cache, int slots,
+                int head_dim, int query_heads, int kv_heads, float epsilon,
+                uint32_t position, uint32_t tokens);
+/* Attention over the F16 cache (kernels/attention/attention.wgsl:166-438).
+ * out: tokens x query_heads x head_dim. */
+int frz_op_attention(frz_device* dev, const float* query, int q_stride,
+                     const uint16_t* key_cache, const uint16_t* value_cache,
+                     float* out, int slots, int window, int head_dim,
+                     int query_heads, int kv_heads, float scale,
+                     uint32_t position, uint32_t tokens);
+/* Embedding rows times scale (kernels/gather/gather.wgsl:25-48). */
+int frz_op_gather(frz_device* dev, const void* codes, const void* scales,
+                  int rows, int cols, const uint32_t* ids, uint32_t tokens,
+                  float scale, float* hidden);
+/* One layer's pins alone (src/core/edit/edit.wgsl:55-76). */
+int frz_op_edit(frz_device* dev, const uint32_t* edits_dev, int layer,
+                float* act, int width, uint32_t position, uint32_t tokens);
+/* Top-64 (kernels/topk/topk.wgsl): candidates_dev gets 64 x {bits, token}. */
+int frz_op_topk(frz_device* dev, const float* logits, int count,
+                uint32_t* candidates_dev);
+
+/* Sampling settings of a turn (src/core/policy/policy.h:41-46) with its seed
+ * (policy::Seed), as sampler::apply puts them in a step
+ * (src/core/sampler/sampler.cpp:51-62). */
+typedef struct frz_sampling {
+  uint32_t top_k;
+  float temperature;
+  float top_p;
+  float min_p;
+  uint64_t seed;
+} frz_sampling;
+
+/* The draw (src/core/sampler/draw.wgsl:77-170): record_dev gets
+ * {token, failed, u bits, 0} for the position position + tokens. */
+int frz_op_draw(frz_device* dev, const uint32_t* candidates_dev,
+                const frz_sampling* sampling, uint32_t position,
+                uint32_t tokens, uint32_t* record_dev);
+
+/* The shared numerics on the device, for their contract tests: which = 0
+ * exp2, 1 cos, 2 sin, 3 inverse sqrt, 4 gelu_tanh, 5 exp_nonpositive,
+ * 6 f16 pack (out holds the halves' bits as floats' low 16 bits, via
+ * uint32), 7 sqrt, 8 division in[2i] / in[2i+1]. */
+int frz_op_numerics(frz_device* dev, int which, const float* in_dev,
+                    float* out_dev, int n);
+
+/* Times `iters` launches of the decode GEMV over `copies` distinct weight
+ * copies in turn (so the weights stream from HBM, not a cache), with HIP
+ * events on the launching stream; writes the mean microseconds a launch. */
+int frz_bench_gemv(frz_device* dev, const void* const* codes,
+                   const void* const* scales, int copies, int rows, int cols,
+                   const float* x, float* y, int iters, double* us_per_launch);
+/* The same for the gated product (gate and up copies in turn). */
+int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
+                    const void* const* gate_scales,
+                    const void* const* up_codes, const void* const* up_scales,
+                    int copies, int rows, int cols, const float* x, float* act,
+                    int iters, double* us_per_launch);
+
+/* Each pair's turns a position for a rotary base (src/core/kernels/rope/
+ * rope.cpp:95-106): theta_k / 2 pi in f64, rounded once to f32. */
+void frz_rope_turns(float base, int head_dim, float* turns);
+
+/* ---- neuron pins (src/core/edit/edit.h:10-167) ---------------------------- */
+/* An edit pins one neuron of a layer's feed-forward activation over the
+ * steps [from, until) of a run (until 0xFFFFFFFF: to the end). */
+enum frz_edit_kind { FRZ_EDIT_SET = 0, FRZ_EDIT_SCALE = 1, FRZ_EDIT_ZERO = 2 };
+typedef struct frz_edit {
+  uint32_t layer;
+  uint32_t neuron;
+  uint32_t kind;
+  float value;
+  uint32_t from;
+  uint32_t until;
+} frz_edit;
+/* edit::EditError (src/core/edit/edit.h:131-141). */
+enum frz_edit_error {
+  FRZ_EDIT_OK = 0,
+  FRZ_EDIT_ERR_KIND = 1,
+  FRZ_EDIT_ERR_LAYER = 2,
+  FRZ_EDIT_ERR_NEURON = 3,
+  FRZ_EDIT_ERR_NOT_FINITE = 4,
+  FRZ_EDIT_ERR_ZERO_VALUE = 5,
+  FRZ_EDIT_ERR_RANGE = 6,
+  FRZ_EDIT_ERR_OVERLAP = 7,
+  FRZ_EDIT_ERR_TOO_MANY = 8
+};
+/* edit::check (src/core/edit/edit.cpp:105-134): the set's first fault and
+ * the offending edit's index, or FRZ_EDIT_OK. */
+int frz_edit_check(const frz_edit* edits, uint32_t count, uint32_t layers,
+                   uint32_t ffn, uint32_t* offending);
+/* Words of the table for `count` edits: 2 a layer + 5 an edit. */
+uint32_t frz_edit_table_words(uint32_t count, uint32_t layers);
+/* edit::table (src/core/edit/edit.cpp:136-161), ranges placed at origin
+ * (origin 0 keeps them in steps). Precondition: frz_edit_check passed. */
+int frz_edit_table(const frz_edit* edits, uint32_t count, uint32_t layers,
+                   uint32_t origin, uint32_t* out_words);
+/* edit::apply (src/core/edit/edit.cpp:93-103). */
+float frz_edit_apply(uint32_t kind, float value, float neuron);
+
+/* ---- the model and its steps (replaces Engine::finish_load +
+ *      Program::build / Program::run, src/core/runtime/engine.cpp:342-394,
+ *      src/core/kernels/program.h:338-387) ----------------------------------- */
+typedef struct frz_model_config {
+  int hidden;      /* 1152 */
+  int ffn;         /* 6912 */
+  int head_dim;    /* 256 */
+  int query_heads; /* 4 */
+  int kv_heads;    /* 1 */
+  int layers;      /* 26 */
+  int vocab;       /* 262144 */
+  int window;      /* 512: a sliding layer's keys */
+  int pattern;     /* 6: layer l is global when l % pattern == pattern - 1 */
+  int context;     /* positions a global layer's cache holds */
+  int local_slots; /* a sliding layer's ring: window + 512 + reserve */
+  float rope_local;  /* 10,000 */
+  float rope_global; /* 1,000,000 */
+  float epsilon;     /* 1e-6 */
+} frz_model_config;
+
+/* Gemma-3-1B's shapes (src/core/arch/gemma3/gemma3.h:60-76). */
+void frz_gemma3_1b_config(frz_model_config* out, int context);
+
+/* Tensor roles a layer holds (src/core/arch/gemma3/gemma3.cpp:21-35), and the
+ * two global tensors (layer -1). Matrices are Q4_0; norms are F32. */
+enum frz_role {
+  FRZ_ROLE_Q = 0,
+  FRZ_ROLE_K = 1,
+  FRZ_ROLE_V = 2,
+  FRZ_ROLE_O = 3,
+  FRZ_ROLE_GATE = 4,
+  FRZ_ROLE_UP = 5,
+  FRZ_ROLE_DOWN = 6,
+  FRZ_ROLE_ATTN_NORM = 7,
+  FRZ_ROLE_Q_NORM = 8,
+  FRZ_ROLE_K_NORM = 9,
+  FRZ_ROLE_POST_ATTN_NORM = 10,
+  FRZ_ROLE_FFN_NORM = 11,
+  FRZ_ROLE_POST_FFN_NORM = 12,
+  FRZ_ROLE_EMBEDDING = 13,   /* layer -1: the tied token embedding / head */
+  FRZ_ROLE_OUTPUT_NORM = 14  /* layer -1 */
+};
+
+/* Bytes of a tensor as a GGUF file holds it (Q4_0 blocks or F32). */
+uint64_t frz_tensor_bytes(const frz_model_config* config, int role);
+
+/* The seeded synthetic weights, host bytes of one tensor: Q4_0 blocks with
+ * d = fp16(|N(0, 0.02)|) and codes uniform in 0..15; norm gains 1 +
+ * 0.1 N(0, 1) (the file stores 1 + w). SplitMix64 streams keyed by (seed,
+ * layer, role); normals by Box-Muller in f64. */
+int frz_synth_tensor(const frz_model_config* config, uint64_t seed, int layer,
+                     int role, void* out, uint64_t bytes);
+
+typedef struct frz_model frz_model;
+
+int frz_model_create(frz_device* dev, const frz_model_config* config,
+                     frz_model** out);
+void frz_model_destroy(frz_model* model);
+/* One tensor from host bytes as a GGUF file holds it (Upload::write). */
+int frz_model_set_tensor(frz_model* model, int layer, int role,
+                         const void* data, uint64_t bytes);
+/* Every tensor from frz_synth_tensor(seed). */
+int frz_model_synthesize(frz_model* model, uint64_t seed);
+/* The edit table, u32 words in the reference's layout (src/core/edit/
+ * edit.h: per layer [first, count], then [neuron, kind, value bits, first
+ * position, end position] per edit), used by every later step. */
+int frz_model_set_edits(frz_model* model, const uint32_t* table,
+                        uint32_t words);
+
+/* One step of `tokens` (1 .. 512) token ids from `position`
+ * (kernels::Step, src/core/kernels/interface.h:163-188). With logits, the
+ * step also computes the last row's logits, selects and draws. Enqueued. */
+int frz_model_step(frz_model* model, uint32_t position, uint32_t tokens,
+                   const uint32_t* ids, int logits,
+                   const frz_sampling* sampling);
+/* `steps` fed decode steps, each from the last draw, after a step with
+ * logits at `position` (the next token's position). Token i's id goes to
+ * tokens_out[i] (and its failed flag to failed_out[i] when not null).
+ * Replays one captured HIP graph per step; waits for the last. */
+int frz_model_decode(frz_model* model, uint32_t position, uint32_t steps,
+                     const frz_sampling* sampling, uint32_t* tokens_out,
+                     uint32_t* failed_out);
+/* Reads after a step (each waits for the device). */
+int frz_model_read_logits(frz_model* model, float* out, uint32_t count);
+int frz_model_read_record(frz_model* model, uint32_t record[4]);
+int frz_model_read_candidates(frz_model* model, uint32_t out[128]);
+int frz_model_read_hidden(frz_model* model, float* out, uint32_t rows);
+int frz_model_read_cache(frz_model* model, int layer, int values,
+                         uint16_t* out, uint64_t count);
+/* Mean microseconds of each decode step over `steps` graph replays timed
+ * with HIP events on the model's stream (the timed region of bench.py). */
+int frz_model_time_decode(frz_model* model, uint32_t position, uint32_t steps,
+                          const frz_sampling* sampling, double* us_per_step);
+
+/* ---- generation (replaces Engine::generate, src/core/runtime/engine.h:
+ *      366-412, and the native tool's paired runs, tools/frizzle/main.cpp:
+ *      53-55) ------------------------------------------------------------- */
+/* Runs the prompt (prefill blocks of 512), then draws up to max_tokens
+ * tokens with `edits` (the reference's edit table, placed at origin =
+ * prompt_len - 1; null for none). Stops after a token in stop_ids. Returns
+ * the tokens drawn in tokens_out and their count in *drawn. Reuses the cached
+ * prefix of the model's last run where its tokens and placed edits agree
+ * (src/core/cache/prefix.h:87-94). */
+int frz_generate(frz_model* model, const uint32_t* prompt, uint32_t prompt_len,
+                 const uint32_t* edit_table, uint32_t edit_words,
+                 const frz_sampling* sampling, uint32_t max_tokens,
+                 const uint32_t* stop_ids, uint32_t stops,
+                 uint32_t* tokens_out, uint32_t* drawn);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRIZZLE_HIP_H */

@@ -1,0 +1,230 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) for the tests.
+
+The oracle is the checker: tests compare the HIP backend against it, and pin
+the oracle itself against closed forms, brute force and the reference's own
+fixtures. Nothing in the product imports this module.
+"""
+import ctypes
+import subprocess
+from ctypes import POINTER, c_float, c_int, c_uint16, c_uint32, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_LIB = ORACLE_DIR / "liboracle.so"
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in (
+        "hidden", "ffn", "head_dim", "query_heads", "kv_heads", "layers",
+        "vocab", "window", "pattern", "context", "local_slots")] + [
+        ("rope_local", c_float), ("rope_global", c_float), ("epsilon", c_float)]
+
+
+class OrcLayer(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in (
+        "q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm",
+        "k_norm", "post_attn_norm", "ffn_norm", "post_ffn_norm")]
+
+
+_P = c_void_p
+_SIGS = {
+    "orc_exp_nonpositive": (c_float, [c_float]),
+    "orc_gelu_tanh": (c_float, [c_float]),
+    "orc_exp2": (c_float, [c_float]),
+    "orc_cos": (c_float, [c_float]),
+    "orc_sin": (c_float, [c_float]),
+    "orc_inverse_sqrt": (c_float, [c_float]),
+    "orc_f16_pack": (c_uint16, [c_float]),
+    "orc_f16_unpack": (c_float, [c_uint16]),
+    "orc_dot4": (c_float, [_P, _P]),
+    "orc_q4_0_unpack": (None, [_P, _P]),
+    "orc_gemv": (None, [_P, c_int, c_int, _P, _P]),
+    "orc_gated": (None, [_P, _P, c_int, c_int, _P, _P]),
+    "orc_norm_row": (None, [_P, _P, c_int, c_int, c_float, c_float, c_int, _P,
+                            _P, _P]),
+    "orc_rope_turns": (None, [c_float, c_int, _P]),
+    "orc_rope_row": (None, [c_int, c_int, c_int, c_int, c_int, c_float, _P, _P,
+                            _P, _P, _P, _P, _P, _P]),
+    "orc_attention_row": (None, [c_int, c_int, c_int, c_int, c_int, c_int,
+                                 c_float, _P, _P, _P, _P]),
+    "orc_gather_row": (None, [_P, c_int, c_uint32, c_float, _P]),
+    "orc_edit_row": (None, [_P, c_int, c_uint32, c_int, _P]),
+    "orc_topk": (None, [_P, c_int, _P, _P]),
+    "orc_philox": (None, [_P, _P, _P]),
+    "orc_mulhi": (c_uint32, [c_uint32, c_uint32]),
+    "orc_draw": (None, [_P, _P, c_uint32, c_uint32, c_float, c_float, c_float,
+                        c_float, c_uint32, c_uint32, c_uint32, _P]),
+    "orc_model_create": (c_void_p, [POINTER(OrcConfig), POINTER(OrcLayer), _P,
+                                    _P]),
+    "orc_model_destroy": (None, [_P]),
+    "orc_model_set_edits": (None, [_P, _P, c_int]),
+    "orc_model_token": (None, [_P, c_uint32, c_int, _P]),
+    "orc_model_normed": (c_void_p, [_P]),
+    "orc_model_key_cache": (c_void_p, [_P, c_int]),
+    "orc_model_value_cache": (c_void_p, [_P, c_int]),
+    "orc_model_slots": (c_int, [_P, c_int]),
+}
+
+_lib = None
+_libm = ctypes.CDLL("libm.so.6")
+_libm.logf.restype = c_float
+_libm.logf.argtypes = [c_float]
+
+
+def _logf(x):
+    return _libm.logf(x)
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not ORACLE_LIB.exists():
+            build()
+        L = ctypes.CDLL(str(ORACLE_LIB))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def gemv(w_blocks, rows, cols, x):
+    y = np.empty(rows, dtype=np.float32)
+    x = f32(x)
+    lib().orc_gemv(_p(w_blocks), rows, cols, _p(x), _p(y))
+    return y
+
+
+def gated(gate_blocks, up_blocks, rows, cols, x):
+    y = np.empty(rows, dtype=np.float32)
+    x = f32(x)
+    lib().orc_gated(_p(gate_blocks), _p(up_blocks), rows, cols, _p(x), _p(y))
+    return y
+
+
+def q4_0_unpack(block):
+    out = np.empty(32, dtype=np.float32)
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    lib().orc_q4_0_unpack(_p(b), _p(out))
+    return out
+
+
+def norm_row(gain, hidden, output=None, post_gain=None, epsilon=1e-6):
+    hidden = f32(hidden).copy()
+    normed = np.empty_like(hidden)
+    add = post_gain is not None
+    out = f32(output) if add else hidden
+    pg = f32(post_gain) if add else f32(gain)
+    lib().orc_norm_row(_p(f32(gain)), _p(pg), int(add), int(add), 1.0, epsilon,
+                       hidden.size, _p(hidden), _p(out), _p(normed))
+    return hidden, normed
+
+
+def rope_turns(base, head_dim):
+    t = np.empty(head_dim // 2, dtype=np.float32)
+    lib().orc_rope_turns(base, head_dim, _p(t))
+    return t
+
+
+def topk(logits):
+    bits = np.empty(64, dtype=np.uint32)
+    ids = np.empty(64, dtype=np.uint32)
+    lg = f32(logits)
+    lib().orc_topk(_p(lg), lg.size, _p(bits), _p(ids))
+    return bits, ids
+
+
+def philox(counter, key):
+    c = np.ascontiguousarray(counter, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, dtype=np.uint32)
+    lib().orc_philox(_p(c), _p(k), _p(out))
+    return out
+
+
+def draw(cand_bits, cand_ids, top_k=1, temperature=0.0, top_p=1.0, min_p=0.0,
+         counter=0, seed=0):
+    b = np.ascontiguousarray(cand_bits, dtype=np.uint32)
+    i = np.ascontiguousarray(cand_ids, dtype=np.uint32)
+    rec = np.empty(4, dtype=np.uint32)
+    # ln min_p in f32 by the C library, as sampler::apply takes it
+    # (src/core/sampler/sampler.cpp:61) and as the backend does.
+    log_min_p = _logf(min_p) if min_p > 0 else 0.0
+    lib().orc_draw(_p(b), _p(i), 64, top_k, temperature, top_p, min_p,
+                   np.float32(log_min_p), counter, seed & 0xFFFFFFFF,
+                   (seed >> 32) & 0xFFFFFFFF, _p(rec))
+    return rec
+
+
+class OracleModel:
+    """The oracle's model over host weight arrays (kept alive here)."""
+
+    def __init__(self, cfg_dict, tensors):
+        self.cfg = OrcConfig(**cfg_dict)
+        self.tensors = tensors  # {(layer, role): array}
+        n = self.cfg.layers
+        self.layers = (OrcLayer * n)()
+        for l in range(n):
+            fields = {}
+            for role in ("q", "k", "v", "o", "gate", "up", "down", "attn_norm",
+                         "q_norm", "k_norm", "post_attn_norm", "ffn_norm",
+                         "post_ffn_norm"):
+                fields[role] = tensors[(l, role)].ctypes.data
+            self.layers[l] = OrcLayer(**fields)
+        self.handle = lib().orc_model_create(
+            ctypes.byref(self.cfg), self.layers,
+            tensors[(-1, "embedding")].ctypes.data,
+            tensors[(-1, "output_norm")].ctypes.data)
+
+    def set_edits(self, table):
+        self._edits = np.ascontiguousarray(table, dtype=np.uint32)
+        lib().orc_model_set_edits(self.handle, _p(self._edits), self._edits.size)
+
+    def token(self, token, position, want_logits=True):
+        logits = np.empty(self.cfg.vocab, dtype=np.float32) if want_logits else None
+        lib().orc_model_token(self.handle, int(token), int(position),
+                              _p(logits) if want_logits else None)
+        return logits
+
+    def key_cache(self, layer):
+        slots = lib().orc_model_slots(self.handle, layer)
+        n = slots * self.cfg.kv_heads * self.cfg.head_dim
+        ptr = lib().orc_model_key_cache(self.handle, layer)
+        return np.ctypeslib.as_array((c_uint16 * n).from_address(ptr)).copy()
+
+    def value_cache(self, layer):
+        slots = lib().orc_model_slots(self.handle, layer)
+        n = slots * self.cfg.kv_heads * self.cfg.head_dim
+        ptr = lib().orc_model_value_cache(self.handle, layer)
+        return np.ctypeslib.as_array((c_uint16 * n).from_address(ptr)).copy()
+
+    def normed(self):
+        ptr = lib().orc_model_normed(self.handle)
+        return np.ctypeslib.as_array((c_float * self.cfg.hidden).from_address(ptr)).copy()
+
+    def close(self):
+        if self.handle:
+            lib().orc_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,143 @@
+"""The whole forward path on the GPU against the oracle: prefill in one or
+several steps, greedy and seeded decode, pins, the KV caches, bit for bit."""
+import numpy as np
+import pytest
+
+import _oracle as orc
+import frizzle_amd as fz
+from helpers import assert_same_bits
+
+pytestmark = pytest.mark.gpu
+
+ROLES = ["q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm", "k_norm",
+         "post_attn_norm", "ffn_norm", "post_ffn_norm"]
+
+
+def small_config(**kw):
+    """Gemma-3-1B's layer shapes with 3 layers (the third global), a 4,096
+    vocabulary and a 64-token window, so short runs cross the window."""
+    base = dict(layers=3, vocab=4096, window=64, pattern=3, context=1024,
+                local_slots=64 + 512 + 64)
+    base.update(kw)
+    return fz.gemma3_1b_config(**base)
+
+
+def build_pair(device, cfg, seed):
+    """The same synthetic weights on the GPU and in the oracle."""
+    tensors = {}
+    for l in range(cfg.layers):
+        for r in ROLES:
+            tensors[(l, r)] = fz.synth_tensor(cfg, seed, l, r)
+    tensors[(-1, "embedding")] = fz.synth_tensor(cfg, seed, -1, "embedding")
+    tensors[(-1, "output_norm")] = fz.synth_tensor(cfg, seed, -1, "output_norm")
+    model = fz.Model(device, cfg)
+    for (l, r), a in tensors.items():
+        model.set_tensor(l, r, a)
+    oracle = orc.OracleModel(cfg.as_dict(), tensors)
+    return model, oracle
+
+
+def oracle_run(oracle, prompt, steps, cfg, edits_table=None, greedy=True, samp=None):
+    """Token by token: the prompt, then `steps` draws fed back. Returns the
+    drawn tokens and the logits at the prompt's end."""
+    if edits_table is not None:
+        oracle.set_edits(edits_table)
+    end_logits = None
+    for p, tok in enumerate(prompt):
+        lg = oracle.token(tok, p, want_logits=(p == len(prompt) - 1))
+        if p == len(prompt) - 1:
+            end_logits = lg
+    out = []
+    lg = end_logits
+    pos = len(prompt)
+    for i in range(steps):
+        bits, ids = orc.topk(lg)
+        if greedy:
+            tok = int(ids[0])
+        else:
+            rec = orc.draw(bits, ids, samp.top_k, samp.temperature, samp.top_p, samp.min_p,
+                           counter=pos, seed=samp.seed)
+            tok = int(rec[0])
+        out.append(tok)
+        if i + 1 < steps:
+            lg = oracle.token(tok, pos)
+            pos += 1
+    return np.array(out, dtype=np.uint32), end_logits
+
+
+def placed(cfg, edits, origin):
+    return fz.edit_table(edits, cfg.layers, origin)
+
+
+def test_prefill_logits_and_cache_bit_exact(device):
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=7)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, cfg.vocab, 100).astype(np.uint32)
+    model.set_edits(np.zeros(2 * cfg.layers, dtype=np.uint32))
+    model.step(0, prompt[:37], logits=False)
+    model.step(37, prompt[37:], logits=True)
+    got = model.logits()
+    _, want = oracle_run(oracle, prompt, 0, cfg)
+    assert_same_bits(got, want, "prompt-end logits")
+    for l in range(cfg.layers):
+        n = oracle.key_cache(l).size
+        assert np.array_equal(model.cache(l, False, n), oracle.key_cache(l)), f"keys {l}"
+        assert np.array_equal(model.cache(l, True, n), oracle.value_cache(l)), f"values {l}"
+    model.close()
+
+
+@pytest.mark.parametrize("split", [None, 1])
+def test_greedy_decode_token_identical(device, split):
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=11)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, cfg.vocab, 70).astype(np.uint32)
+    steps = 40
+    want, _ = oracle_run(oracle, prompt, steps, cfg)
+    if split is None:
+        got = model.generate(prompt, max_tokens=steps)
+    else:
+        model.set_edits(np.zeros(2 * cfg.layers, dtype=np.uint32))
+        for p, tok in enumerate(prompt):  # every position decoded alone
+            model.step(p, [tok], logits=(p == len(prompt) - 1))
+        first = model.record()[0]
+        rest, _ = model.decode(len(prompt), steps - 1)
+        got = np.concatenate([[first], rest]).astype(np.uint32)
+    assert np.array_equal(got, want), (got, want)
+    model.close()
+
+
+def test_steered_and_original_token_identical(device):
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=13)
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, cfg.vocab, 50).astype(np.uint32)
+    steps = 24
+    edits = [fz.Edit(int(l), int(n), fz.EditKind.SET, float(v))
+             for l, n, v in zip(rng.integers(0, cfg.layers, 8), rng.integers(0, cfg.ffn, 8),
+                                rng.uniform(-10, 10, 8))]
+    edits = list({(e.layer, e.neuron): e for e in edits}.values())
+    edits.append(fz.Edit(0, 5, fz.EditKind.SCALE, 3.0, 4, 9))
+    original, steered = model.paired(prompt, edits, max_tokens=steps)
+    want_o, _ = oracle_run(oracle, prompt, steps, cfg,
+                           np.zeros(2 * cfg.layers, dtype=np.uint32))
+    oracle2 = orc.OracleModel(cfg.as_dict(), oracle.tensors)
+    want_s, _ = oracle_run(oracle2, prompt, steps, cfg, placed(cfg, edits, len(prompt) - 1))
+    assert np.array_equal(original, want_o)
+    assert np.array_equal(steered, want_s)
+    assert not np.array_equal(original, steered)
+    model.close()
+
+
+def test_seeded_sampling_token_identical(device):
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=17)
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, cfg.vocab, 30).astype(np.uint32)
+    samp = fz.sampling(temperature=1.0, top_k=64, top_p=1.0, min_p=0.0, seed=0xC0FFEE)
+    steps = 20
+    want, _ = oracle_run(oracle, prompt, steps, cfg, greedy=False, samp=samp)
+    got = model.generate(prompt, samp=samp, max_tokens=steps)
+    assert np.array_equal(got, want)
+    model.close()
