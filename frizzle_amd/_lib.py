@@ -78,6 +78,8 @@ _SIGS = {
     "frz_op_attention": (c_int, [_P, _P, c_int, _P, _P, _P, c_int, c_int,
                                  c_int, c_int, c_int, c_float, c_uint32,
                                  c_uint32]),
+    "frz_op_rope_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int,
+                                      c_int, c_float, c_float, c_uint32]),
     "frz_op_gather": (c_int, [_P, _P, _P, c_int, c_int, _P, c_uint32, c_float,
                               _P]),
     "frz_op_edit": (c_int, [_P, _P, c_int, _P, c_int, c_uint32, c_uint32]),
@@ -106,6 +108,7 @@ _SIGS = {
     "frz_model_set_tensor": (c_int, [_P, c_int, c_int, _P, c_uint64]),
     "frz_model_synthesize": (c_int, [_P, c_uint64]),
     "frz_model_set_edits": (c_int, [_P, _P, c_uint32]),
+    "frz_model_set_graphs": (c_int, [_P, c_int]),
     "frz_model_step": (c_int, [_P, c_uint32, c_uint32, _P, c_int,
                                POINTER(Sampling)]),
     "frz_model_decode": (c_int, [_P, c_uint32, c_uint32, POINTER(Sampling),

@@ -287,6 +287,37 @@ int frz_op_attention(frz_device* dev, const float* query, int q_stride,
   return rc;
 }
 
+int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
+                          const float* query_gain, const float* key_gain, uint16_t* key_cache,
+                          uint16_t* value_cache, float* out, int slots, int window,
+                          float epsilon, float scale, uint32_t position) {
+  if (window <= 0 || slots <= 0 || (int)position >= 0x7fffffff) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention: bad window or slots");
+  }
+  const int max_chunks = attention_max_chunks(window, slots);
+  const size_t part_floats = (size_t)max_chunks * 4 * 256;
+  float* partials = nullptr;
+  uint32_t* counter = nullptr;
+  if (int rc = check_hip(hipMalloc(&partials, (part_floats + part_floats / 64) * sizeof(float)),
+                         "hipMalloc(partials)"))
+    return rc;
+  int rc = check_hip(hipMalloc(&counter, 4), "hipMalloc(counter)");
+  if (rc == FRZ_OK) rc = check_hip(hipMemsetAsync(counter, 0, 4, dev->stream), "hipMemsetAsync");
+  if (rc == FRZ_OK) rc = device_put_step(dev, host_step(position, 1));
+  if (rc == FRZ_OK) {
+    const float scale_log2e = (float)((double)scale * 1.4426950408889634);
+    DecodeAttentionArgs a{qkv,        turns,      query_gain, key_gain,   key_cache,
+                          value_cache, out,       partials,   partials + part_floats,
+                          counter,    slots,      window,     256,        4,
+                          1,          max_chunks, epsilon,    scale_log2e};
+    rc = device_finish(dev, launch_attention_decode(dev->stream, dev->step, a),
+                       "frz_op_rope_attention");
+  }
+  (void)hipFree(partials);
+  if (counter) (void)hipFree(counter);
+  return rc;
+}
+
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales, int rows, int cols,
                   const uint32_t* ids, uint32_t tokens, float scale, float* hidden) {
   if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {

@@ -97,17 +97,19 @@ struct frz_model {
   Q4Matrix embedding{};
   float* output_norm = nullptr;
   // working buffers, a prefill block of rows each
-  float *hidden = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr,
+  float *hidden = nullptr, *hidden_b = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr,
         *output = nullptr, *act = nullptr, *logits = nullptr, *partials = nullptr,
         *stats = nullptr;
   uint32_t *topk_scratch = nullptr, *candidates = nullptr, *sampled = nullptr,
            *token_log = nullptr, *edits = nullptr;
+  uint32_t* counters = nullptr;  // a layer's decode-attention arrivals, zero between steps
   uint32_t token_log_capacity = 0;
   size_t partial_floats = 0;
   DevStep* step = nullptr;       // device
   DevStep* step_host = nullptr;  // pinned
   hipGraphExec_t decode_exec = nullptr;
   hipGraph_t decode_graph = nullptr;
+  bool use_graphs = true;  // false: decode steps launch their kernels one by one
   // generation state: the tokens whose keys and values the caches hold, and
   // the placed edit table they were computed under
   std::vector<uint32_t> cached;
@@ -155,18 +157,32 @@ int upload_q4(frz_model* m, const Q4Matrix& w, int row0, int rows, const void* d
   return check_hip(hipStreamSynchronize(s), "upload sync");
 }
 
-// Enqueues one step's launches, in the graph's order: the embedding; per
-// layer the attention norm (adding the last block's post-normed output),
-// Q/K/V, rope and the cache append, attention, O; the feed-forward norm,
-// gate-up with GELU and the pins, down; then the final norm of the last row
-// and, with logits, the head, the selection and the draw.
-int enqueue_step(frz_model* m, int max_tokens, bool logits) {
+// The head, the selection and the draw, after the final norm wrote the step's
+// last row into `normed`.
+hipError_t enqueue_output(frz_model* m, int max_tokens) {
+  hipStream_t s = m->dev->stream;
+  hipError_t e = launch_gemv(s, m->step, m->embedding, m->normed, m->c.hidden, m->logits,
+                             m->c.vocab, max_tokens, true);
+  if (e == hipSuccess) e = launch_topk(s, m->logits, m->c.vocab, m->topk_scratch, m->candidates);
+  if (e == hipSuccess) e = launch_draw(s, m->step, m->candidates, m->sampled, m->token_log);
+  return e;
+}
+
+float scale_log2e_of(const frz_model_config& c) {
+  return (float)((double)(1.0f / std::sqrt((float)c.head_dim)) * 1.4426950408889634);
+}
+
+// A step of several tokens, in the graph's order (graph.cpp:290-470): the
+// embedding; per layer the attention norm (adding the last block's
+// post-normed output), Q/K/V, rope and the cache append, attention, O; the
+// feed-forward norm, gate-up with GELU and the pins, down; then the final
+// norm of the last row and, with logits, the output block.
+int enqueue_prefill(frz_model* m, int max_tokens, bool logits) {
   const frz_model_config& c = m->c;
   hipStream_t s = m->dev->stream;
   const int H = c.hidden, qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
   const int qkv_stride = qw + 2 * kvw;
-  const float scale_log2e = (float)((double)(1.0f / std::sqrt((float)c.head_dim)) *
-                                    1.4426950408889634);
+  const float scale_log2e = scale_log2e_of(c);
   hipError_t e = launch_gather(s, m->step, m->embedding, m->sampled, m->hidden,
                                std::sqrt((float)H), max_tokens);
   const float* pending = nullptr;
@@ -207,12 +223,75 @@ int enqueue_step(frz_model* m, int max_tokens, bool logits) {
                         c.epsilon, H, true};
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
-  if (logits && e == hipSuccess) {
-    e = launch_gemv(s, m->step, m->embedding, m->normed, H, m->logits, c.vocab, max_tokens, true);
-    if (e == hipSuccess) e = launch_topk(s, m->logits, c.vocab, m->topk_scratch, m->candidates);
-    if (e == hipSuccess) e = launch_draw(s, m->step, m->candidates, m->sampled, m->token_log);
+  if (logits && e == hipSuccess) e = enqueue_output(m, max_tokens);
+  return check_hip(e, "enqueue_prefill");
+}
+
+// A step of one token: five launches a layer, each norm inside the product
+// that reads it. The hidden row alternates between two buffers: Q/K/V's
+// prologue reads hidden_b (layer 0: the embedding) and writes hidden;
+// gate-up's reads hidden and writes hidden_b.
+int enqueue_decode(frz_model* m, bool logits) {
+  const frz_model_config& c = m->c;
+  hipStream_t s = m->dev->stream;
+  const int H = c.hidden, qw = c.query_heads * c.head_dim;
+  const float scale_log2e = scale_log2e_of(c);
+  hipError_t e = hipSuccess;
+  const float* pending = nullptr;
+  for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
+    const Layer& L = m->layers[l];
+    GemvInput in{};
+    in.hidden = m->hidden_b;
+    in.output = m->output;
+    in.post_gain = pending;
+    in.gain = L.gains[0];
+    in.hidden_out = m->hidden;
+    in.table = m->embedding;
+    in.sampled = m->sampled;
+    in.scale = std::sqrt((float)H);
+    in.epsilon = c.epsilon;
+    e = launch_gemv_decode(s, m->step, L.qkv, in, l == 0 ? 2 : 1, m->qkv);
+    if (e == hipSuccess) {
+      DecodeAttentionArgs d{m->qkv,      L.turns,      L.gains[1], L.gains[2],
+                            L.kcache,    L.vcache,     m->attn,    m->partials,
+                            m->partials + m->partial_floats, m->counters + l, L.slots,
+                            L.window,    c.head_dim,   c.query_heads, c.kv_heads,
+                            L.max_chunks, c.epsilon,   scale_log2e};
+      e = launch_attention_decode(s, m->step, d);
+    }
+    if (e == hipSuccess) {
+      GemvInput x{};
+      x.x = m->attn;
+      e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+    }
+    if (e == hipSuccess) {
+      GemvInput g{};
+      g.hidden = m->hidden;
+      g.output = m->output;
+      g.post_gain = L.gains[3];
+      g.gain = L.gains[4];
+      g.hidden_out = m->hidden_b;
+      g.epsilon = c.epsilon;
+      e = launch_gated_decode(s, m->step, L.gate, L.up, g, 1, m->act, m->edits, l);
+    }
+    if (e == hipSuccess) {
+      GemvInput x{};
+      x.x = m->act;
+      e = launch_gemv_decode(s, m->step, L.down, x, 0, m->output);
+    }
+    pending = L.gains[5];
   }
-  return check_hip(e, "enqueue_step");
+  if (e == hipSuccess) {
+    NormArgs final_norm{m->output_norm, pending, m->output, m->hidden_b, m->normed,
+                        c.epsilon, H, true};
+    e = launch_norm(s, m->step, final_norm, 1);
+  }
+  if (logits && e == hipSuccess) e = enqueue_output(m, 1);
+  return check_hip(e, "enqueue_decode");
+}
+
+int enqueue_step(frz_model* m, int max_tokens, bool logits) {
+  return max_tokens == 1 ? enqueue_decode(m, logits) : enqueue_prefill(m, max_tokens, logits);
 }
 
 int build_decode_graph(frz_model* m) {
@@ -230,6 +309,15 @@ int build_decode_graph(frz_model* m) {
   m->decode_graph = graph;
   return check_hip(hipGraphInstantiate(&m->decode_exec, graph, nullptr, nullptr, 0),
                    "hipGraphInstantiate");
+}
+
+// One fed decode step: the captured graph, or its launches one by one.
+int launch_decode_step(frz_model* m) {
+  if (m->use_graphs) {
+    return check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch");
+  }
+  if (int rc = enqueue_step(m, 1, true)) return rc;
+  return check_hip(launch_advance(m->dev->stream, m->step), "advance");
 }
 
 int put_step(frz_model* m) {
@@ -406,6 +494,7 @@ int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model*
   const size_t B = kPrefillBlock;
   m->partial_floats = max_partials;
   if (int rc = alloc(m, &m->hidden, B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->hidden_b, (size_t)c.hidden * 4)) return bail(rc);
   if (int rc = alloc(m, &m->normed, B * c.hidden * 4)) return bail(rc);
   if (int rc = alloc(m, &m->qkv, B * (qw + 2 * kvw) * 4)) return bail(rc);
   if (int rc = alloc(m, &m->attn, B * qw * 4)) return bail(rc);
@@ -413,6 +502,8 @@ int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model*
   if (int rc = alloc(m, &m->act, B * c.ffn * 4)) return bail(rc);
   if (int rc = alloc(m, &m->logits, (size_t)c.vocab * 4)) return bail(rc);
   if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->counters, (size_t)c.layers * 4)) return bail(rc);
+  (void)hipMemsetAsync(m->counters, 0, (size_t)c.layers * 4, dev->stream);
   const int tiles = (c.vocab + kSelectionTile - 1) / kSelectionTile;
   const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
   if (int rc = alloc(m, &m->topk_scratch, (size_t)2 * kCandidates * (tiles + second) * 4))
@@ -494,6 +585,12 @@ int frz_model_synthesize(frz_model* m, uint64_t seed) {
   return one(-1, FRZ_ROLE_OUTPUT_NORM);
 }
 
+int frz_model_set_graphs(frz_model* m, int enabled) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_graphs: null model");
+  m->use_graphs = enabled != 0;
+  return FRZ_OK;
+}
+
 int frz_model_set_edits(frz_model* m, const uint32_t* table, uint32_t words) {
   if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: null model");
   const size_t cap = 2 * (size_t)m->c.layers + 5 * (size_t)kMaxEdits;
@@ -558,7 +655,9 @@ int frz_model_decode(frz_model* m, uint32_t position, uint32_t steps,
   if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_decode: too many steps for the context");
   }
-  if (int rc = build_decode_graph(m)) return rc;
+  if (m->use_graphs) {
+    if (int rc = build_decode_graph(m)) return rc;
+  }
   DevStep& s = *m->step_host;
   std::memset(&s, 0, sizeof s);
   s.position = position;
@@ -569,8 +668,7 @@ int frz_model_decode(frz_model* m, uint32_t position, uint32_t steps,
   fill_sampling(s, sampling);
   if (int rc = put_step(m)) return rc;
   for (uint32_t i = 0; i < steps; ++i) {
-    if (int rc = check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch"))
-      return rc;
+    if (int rc = launch_decode_step(m)) return rc;
   }
   std::vector<uint32_t> log(2 * (size_t)steps);
   if (int rc = check_hip(hipMemcpyAsync(log.data(), m->token_log, log.size() * 4,
@@ -591,7 +689,9 @@ int frz_model_time_decode(frz_model* m, uint32_t position, uint32_t steps,
   if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_time_decode: too many steps for the context");
   }
-  if (int rc = build_decode_graph(m)) return rc;
+  if (m->use_graphs) {
+    if (int rc = build_decode_graph(m)) return rc;
+  }
   DevStep& s = *m->step_host;
   std::memset(&s, 0, sizeof s);
   s.position = position;
@@ -606,7 +706,7 @@ int frz_model_time_decode(frz_model* m, uint32_t position, uint32_t steps,
   (void)hipEventRecord(a, m->dev->stream);
   int rc = FRZ_OK;
   for (uint32_t i = 0; i < steps && rc == FRZ_OK; ++i) {
-    rc = check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch");
+    rc = launch_decode_step(m);
   }
   (void)hipEventRecord(b, m->dev->stream);
   if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(b), "hipEventSynchronize");

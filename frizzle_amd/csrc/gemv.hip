@@ -23,110 +23,6 @@ __device__ __forceinline__ float half_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// One group's 32 products chained into acc, weights in order: the 16 low
-// nibbles (weights 0..15, code byte j's low nibble is weight j), then the 16
-// high nibbles (weights 16..31).
-__device__ __forceinline__ float chain_group(float acc, uint4 c, float d,
-                                             const float* xv) {
-  const float m8d = -8.0f * d;
-  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float q = (float)((words[w] >> (8 * b)) & 0xFu);
-      acc = fmaf_(fmaf_(q, d, m8d), xv[4 * w + b], acc);
-    }
-  }
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float q = (float)((words[w] >> (8 * b + 4)) & 0xFu);
-      acc = fmaf_(fmaf_(q, d, m8d), xv[16 + 4 * w + b], acc);
-    }
-  }
-  return acc;
-}
-
-// Stages one input row into LDS, group g at xs[g * kXStride].
-__device__ __forceinline__ void stage_x(float* xs, const float* x, int cols) {
-  for (int i = threadIdx.x; i < cols; i += kThreads) {
-    xs[(i >> 5) * kXStride + (i & 31)] = x[i];
-  }
-}
-
-// The range sums of `SET` rows, for lane r's range: the decode form
-// (matmul.wgsl:154-176), one lane a range, the input's group loaded once and
-// used by each row.
-template <int SET>
-__device__ __forceinline__ void range_sums(const uint8_t* __restrict__ codes,
-                                           const uint16_t* __restrict__ scales,
-                                           int cols, const int* rows,
-                                           const float* xs, int r,
-                                           float* acc) {
-  const int groups = cols >> 5;
-  const int lo = r * groups / kRanges;
-  const int hi = (r + 1) * groups / kRanges;
-#pragma unroll
-  for (int j = 0; j < SET; ++j) acc[j] = 0.0f;
-  for (int g = lo; g < hi; ++g) {
-    float xv[32];
-    const float* xg = xs + g * kXStride;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) xv[i] = xg[i];
-#pragma unroll
-    for (int j = 0; j < SET; ++j) {
-      if (rows[j] >= 0) {
-        const size_t blk = (size_t)rows[j] * groups + g;
-        const uint4 c = reinterpret_cast<const uint4*>(codes)[blk];
-        const float d = half_to_float(scales[blk]);
-        acc[j] = chain_group(acc[j], c, d, xv);
-      }
-    }
-  }
-}
-
-// The 32 range sums of a row, added in order to a total from zero
-// (matmul.wgsl:179-185).
-__device__ __forceinline__ float row_total(const float* parts) {
-  float total = 0.0f;
-#pragma unroll
-  for (int r = 0; r < kRanges; ++r) total = total + parts[r];
-  return total;
-}
-
-// Decode form, Write epilogue: each wave is two sets of 32 lanes, each set
-// SET rows; a workgroup of 4 waves covers 8 * SET rows.
-template <int SET>
-__global__ __launch_bounds__(kThreads) void gemv_decode(
-    const DevStep* __restrict__ step, Q4Matrix w, const float* __restrict__ x,
-    int x_stride, float* __restrict__ y, int last_token) {
-  extern __shared__ float smem[];
-  const int groups = w.cols >> 5;
-  float* xs = smem;
-  float* parts = smem + groups * kXStride;
-  const int token = last_token ? (int)step->tokens - 1 : 0;
-  stage_x(xs, x + (size_t)token * x_stride, w.cols);
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int set = lane >> 5, r = lane & 31;
-  const int slot0 = wave * 2 * SET + set * SET;
-  const int row0 = blockIdx.x * 8 * SET + slot0;
-  int rows[SET];
-#pragma unroll
-  for (int j = 0; j < SET; ++j) rows[j] = row0 + j < w.rows ? row0 + j : -1;
-  float acc[SET];
-  range_sums<SET>(w.codes, w.scales, w.cols, rows, xs, r, acc);
-#pragma unroll
-  for (int j = 0; j < SET; ++j) parts[(slot0 + j) * 33 + r] = acc[j];
-  __syncthreads();
-  if (threadIdx.x < 8 * SET) {
-    const int row = blockIdx.x * 8 * SET + threadIdx.x;
-    if (row < w.rows) y[row] = row_total(parts + threadIdx.x * 33);
-  }
-}
-
 // A layer's pins on neuron n at `position` (edit.wgsl:55-76): the layer's
 // edits are sorted by neuron then first position (edit.cpp:20-31), so a
 // binary search finds the neuron's; its ranges never overlap.
@@ -152,44 +48,6 @@ __device__ __forceinline__ float apply_edits(const uint32_t* __restrict__ t,
     }
   }
   return value;
-}
-
-// Decode form, gated epilogue (matmul.wgsl:247-271): each set takes gate rows
-// p, p + 1 and up rows p, p + 1; a workgroup covers 16 neurons.
-__global__ __launch_bounds__(kThreads) void gated_decode(
-    const DevStep* __restrict__ step, Q4Matrix gate, Q4Matrix up,
-    const float* __restrict__ x, float* __restrict__ act,
-    const uint32_t* __restrict__ edits, int layer) {
-  extern __shared__ float smem[];
-  const int groups = gate.cols >> 5;
-  float* xs = smem;
-  float* parts = smem + groups * kXStride;
-  stage_x(xs, x, gate.cols);
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int set = lane >> 5, r = lane & 31;
-  const int p = blockIdx.x * 16 + wave * 4 + set * 2;
-  int rows[2] = {p < gate.rows ? p : -1, p + 1 < gate.rows ? p + 1 : -1};
-  float ga[2], ua[2];
-  range_sums<2>(gate.codes, gate.scales, gate.cols, rows, xs, r, ga);
-  range_sums<2>(up.codes, up.scales, up.cols, rows, xs, r, ua);
-  const int slot = (wave * 2 + set) * 4;
-  parts[(slot + 0) * 33 + r] = ga[0];
-  parts[(slot + 1) * 33 + r] = ga[1];
-  parts[(slot + 2) * 33 + r] = ua[0];
-  parts[(slot + 3) * 33 + r] = ua[1];
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    const int s = threadIdx.x >> 1, k = threadIdx.x & 1;
-    const int n = blockIdx.x * 16 + threadIdx.x;
-    if (n < gate.rows) {
-      const float g = row_total(parts + (s * 4 + k) * 33);
-      const float u = row_total(parts + (s * 4 + 2 + k) * 33);
-      float v = gelu_tanh(g) * u;
-      if (edits) v = apply_edits(edits, layer, (uint32_t)n, step->position, v);
-      act[n] = v;
-    }
-  }
 }
 
 // ---- tiled form ----------------------------------------------------------
@@ -333,18 +191,10 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token) {
   if (w.cols % 32 != 0 || w.rows <= 0) return hipErrorInvalidValue;
-  const int groups = w.cols / 32;
   if (max_tokens <= 1 || last_token) {
-    if (w.rows >= 16384) {
-      const size_t lds = (size_t)(groups * kXStride + 32 * 33) * sizeof(float);
-      hipLaunchKernelGGL(gemv_decode<4>, dim3((w.rows + 31) / 32), dim3(kThreads), lds, s,
-                         step, w, x, x_stride, y, last_token ? 1 : 0);
-    } else {
-      const size_t lds = (size_t)(groups * kXStride + 8 * 33) * sizeof(float);
-      hipLaunchKernelGGL(gemv_decode<1>, dim3((w.rows + 7) / 8), dim3(kThreads), lds, s,
-                         step, w, x, x_stride, y, last_token ? 1 : 0);
-    }
-    return hipGetLastError();
+    GemvInput in{};
+    in.x = x + (size_t)(last_token ? max_tokens - 1 : 0) * x_stride;
+    return launch_gemv_decode(s, step, w, in, 0, y);
   }
   const dim3 grid((w.rows + kTileRows - 1) / kTileRows,
                   (max_tokens + kTileTokens - 1) / kTileTokens);
@@ -358,12 +208,10 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
                         int max_tokens, const uint32_t* edits, int layer) {
   if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols)
     return hipErrorInvalidValue;
-  const int groups = gate.cols / 32;
   if (max_tokens <= 1) {
-    const size_t lds = (size_t)(groups * kXStride + 32 * 33) * sizeof(float);
-    hipLaunchKernelGGL(gated_decode, dim3((gate.rows + 15) / 16), dim3(kThreads), lds, s,
-                       step, gate, up, x, act, edits, layer);
-    return hipGetLastError();
+    GemvInput in{};
+    in.x = x;
+    return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
   }
   const dim3 grid((gate.rows + 31) / 32, (max_tokens + kTileTokens - 1) / kTileTokens);
   hipLaunchKernelGGL(gemm_tiled<true>, grid, dim3(kThreads), 0, s, step, gate, up, x,

@@ -1,0 +1,568 @@
+// Decode (one token) Q4_0 products with their input's RMSNorm fused in
+// front, so each layer runs its norms inside the products that read them:
+//   the attention norm (and layer 0's embedding gather) before Q/K/V,
+//   the feed-forward norm before gate/up (GELU and the pins after it).
+// Every workgroup computes its input row itself, redundantly, with the
+// reference's 256-invocation reduction tree (norm.wgsl:75-198), so every
+// workgroup holds the same bits; the first also writes the new hidden row.
+// Hidden rows ping-pong between two buffers, so no workgroup rewrites a row
+// another is still reading.
+//
+// The products keep the reference's order of addition (matmul.h:88-97):
+// range r of a row is groups floor(r G / 32) .. floor((r + 1) G / 32), its
+// products chained by fma from zero; the 32 range sums add in order to a
+// total from zero. Lane r of a half-wave takes range (r + j) mod 32 of the
+// half-wave's row j: the rotation spreads each row's longer ranges over
+// different lanes (at K = 1,152, four ranges of 32 hold two groups).
+//
+// Latency: a workgroup issues its input loads, then all its weight loads,
+// then makes the input row while the weights are in flight (loads return in
+// issue order, so the input row waits only for its own loads).
+
+#include "kernels.h"
+#include "numerics.h"
+
+namespace frz {
+namespace {
+
+constexpr int kWaves = 2;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kXStride = 36;     // a staged group of x: 32 floats + 4 of padding
+constexpr int kNormLanes = 256;  // the norm's reduction width
+constexpr int kLanesPer = kNormLanes / kThreads;  // norm lanes a thread holds
+constexpr int kRedFloats = 260;  // the tree's sums, its total at [256], padding to 16 B
+constexpr int kNormMaxCols = 2 * 4 * kNormLanes;  // two vec4s a norm lane
+
+__device__ __forceinline__ float half_to_float(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// One group's 32 products chained into acc, weights in order: the 16 low
+// nibbles (code byte j's low nibble is weight j), then the 16 high nibbles.
+// Weight j is (q_j - 8) d (q4_0.wgsl:71-83), formed exactly: the nibble goes
+// into the mantissa of the half 1024 + q, and fma(1024 + q, d, -1032 d) in
+// single precision is (q - 8) d before its one rounding, which is exact, as
+// is -1032 d (1032 = 8 * 129 needs 8 bits, d 11). Two nibbles make a half2
+// with one bitwise select, and the fma reads the half operands directly.
+__device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits, const float* xg) {
+  const _Float16 dh = __builtin_bit_cast(_Float16, dbits);
+  const float bias = -1032.0f * (float)dh;
+  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+  constexpr uint32_t kMask = 0x000F000Fu;
+  // The exponent bits come from a register the compiler cannot see into, so
+  // that (s & mask) | (exp & ~mask) stays one bitfield insert.
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float4 x = *reinterpret_cast<const float4*>(xg + 16 * hi + 4 * w);
+      const uint32_t s = words[w] >> (4 * hi);
+      // a: bytes 0 and 2 of the word; b: bytes 1 and 3.
+      const half2v a = __builtin_bit_cast(half2v, (s & kMask) | (kExp & ~kMask));
+      const half2v b = __builtin_bit_cast(half2v, ((s >> 8) & kMask) | (kExp & ~kMask));
+      acc = fmaf_(__builtin_fmaf((float)a.x, (float)dh, bias), x.x, acc);
+      acc = fmaf_(__builtin_fmaf((float)b.x, (float)dh, bias), x.y, acc);
+      acc = fmaf_(__builtin_fmaf((float)a.y, (float)dh, bias), x.z, acc);
+      acc = fmaf_(__builtin_fmaf((float)b.y, (float)dh, bias), x.w, acc);
+    }
+  }
+  return acc;
+}
+
+// The norm's halving tree over its 256 lane sums (norm.wgsl:75-85). Thread t
+// holds lanes t + k kThreads; the levels above kThreads add in registers, the
+// next in LDS, the last six across wave 0. Every thread gets the total.
+__device__ __forceinline__ float tree_total(float* red, const float (&lanes)[kLanesPer]) {
+  const int t = threadIdx.x;
+  float v[kLanesPer];
+#pragma unroll
+  for (int k = 0; k < kLanesPer; ++k) v[k] = lanes[k];
+#pragma unroll
+  for (int width = kLanesPer; width > 1; width >>= 1) {
+#pragma unroll
+    for (int k = 0; k < width / 2; ++k) v[k] = v[k] + v[k + width / 2];
+  }
+  float s = v[0];
+  if (kThreads > 64) {
+    red[t] = s;
+    __syncthreads();
+#pragma unroll
+    for (int stride = kThreads / 2; stride > 64; stride >>= 1) {
+      if (t < stride) red[t] = red[t] + red[t + stride];
+      __syncthreads();
+    }
+    if (t < 64) s = red[t] + red[t + 64];
+  }
+  if (t < 64) {
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) s = s + __shfl_down(s, stride, 64);
+    if (t == 0) red[kNormLanes] = s;
+  }
+  __syncthreads();
+  return red[kNormLanes];
+}
+
+__device__ __forceinline__ void stage4(float* xs, int q, float4 v) {
+  *reinterpret_cast<float4*>(xs + (q >> 3) * kXStride + 4 * (q & 7)) = v;
+}
+
+// A prologue's loads. Plain rows: vec4s t + j kThreads. Norm rows: lane
+// t + k kThreads holds vec4s lane and lane + 256, in slot 2 k + m.
+template <int X4>
+struct Prologue {
+  float4 plain[X4];
+  float4 v[2 * kLanesPer];   // hidden (MODE 1) or the embedding row (MODE 2)
+  float4 y[2 * kLanesPer];   // the block output (MODE 1)
+  float4 pg[2 * kLanesPer];  // its post-norm gain
+  float4 g[2 * kLanesPer];   // the norm gain
+  uint32_t word[2 * kLanesPer];
+  uint16_t d[2 * kLanesPer];
+};
+
+__device__ __forceinline__ int norm_vec4(int k, int m) {
+  return (int)threadIdx.x + k * kThreads + m * kNormLanes;
+}
+
+// Issues the input row's loads: MODE 0 a plain row x; 1 hidden, output and
+// the gains; 2 the embedding of the step's token (gather.wgsl:25-48).
+template <int MODE, int X4>
+__device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& in,
+                                              const DevStep* __restrict__ step, int width) {
+  const int vec4s = width >> 2;
+  if (MODE == 0) {
+#pragma unroll
+    for (int j = 0; j < X4; ++j) {
+      const int q = (int)threadIdx.x + j * kThreads;
+      if (q < vec4s) P.plain[j] = ld4(in.x + 4 * q);
+    }
+    return;
+  }
+  uint32_t token = 0;
+  if (MODE == 2) token = step->fed ? in.sampled[0] : step->ids[0];
+  const int groups = width >> 5;
+#pragma unroll
+  for (int k = 0; k < kLanesPer; ++k) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int q = norm_vec4(k, m), s = 2 * k + m;
+      if (q < vec4s) {
+        if (MODE == 1) {
+          P.v[s] = ld4(in.hidden + 4 * q);
+          P.y[s] = ld4(in.output + 4 * q);
+          P.pg[s] = ld4(in.post_gain + 4 * q);
+        } else {
+          const size_t blk = (size_t)token * groups + (q >> 3);
+          const int j = (4 * q) & 31;
+          P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
+          P.d[s] = in.table.scales[blk];
+        }
+        P.g[s] = ld4(in.gain + 4 * q);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float squares4(float4 a) {
+  return dot4(a.x, a.y, a.z, a.w, a.x, a.y, a.z, a.w);
+}
+
+// Makes the input row from the loads and stages it into xs.
+template <int MODE, int X4>
+__device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<X4>& P,
+                                                const GemvInput& in, int width) {
+  const int vec4s = width >> 2;
+  if (MODE == 0) {
+#pragma unroll
+    for (int j = 0; j < X4; ++j) {
+      const int q = (int)threadIdx.x + j * kThreads;
+      if (q < vec4s) stage4(xs, q, P.plain[j]);
+    }
+    return;
+  }
+  const float n = (float)width;
+  float lanes[kLanesPer];
+  if (MODE == 1) {
+    // hidden + post-normed block output (norm.wgsl:120-160)
+#pragma unroll
+    for (int k = 0; k < kLanesPer; ++k) {
+      lanes[k] = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        if (norm_vec4(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.y[2 * k + m]);
+      }
+    }
+    const float ry = inverse_sqrt(tree_total(red, lanes) / n + in.epsilon);
+#pragma unroll
+    for (int s = 0; s < 2 * kLanesPer; ++s) {
+      if (norm_vec4(s >> 1, s & 1) < vec4s) {
+        float4& x = P.v[s];
+        const float4 y = P.y[s], g = P.pg[s];
+        x.x = x.x + ((y.x * ry) * g.x) * 1.0f;
+        x.y = x.y + ((y.y * ry) * g.y) * 1.0f;
+        x.z = x.z + ((y.z * ry) * g.z) * 1.0f;
+        x.w = x.w + ((y.w * ry) * g.w) * 1.0f;
+      }
+    }
+  } else {
+    // weight j of the token's group, times the scale
+#pragma unroll
+    for (int s = 0; s < 2 * kLanesPer; ++s) {
+      const int q = norm_vec4(s >> 1, s & 1);
+      if (q < vec4s) {
+        const int shift = ((4 * q) & 31) < 16 ? 0 : 4;
+        const float d = half_to_float(P.d[s]);
+        float e[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float code = (float)((P.word[s] >> (8 * b + shift)) & 0xFu);
+          e[b] = fmaf_(code, d, -8.0f * d) * in.scale;
+        }
+        P.v[s] = make_float4(e[0], e[1], e[2], e[3]);
+      }
+    }
+  }
+  if (blockIdx.x == 0 && in.hidden_out) {
+#pragma unroll
+    for (int s = 0; s < 2 * kLanesPer; ++s) {
+      const int q = norm_vec4(s >> 1, s & 1);
+      if (q < vec4s) *reinterpret_cast<float4*>(in.hidden_out + 4 * q) = P.v[s];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kLanesPer; ++k) {
+    lanes[k] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (norm_vec4(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.v[2 * k + m]);
+    }
+  }
+  const float r = inverse_sqrt(tree_total(red, lanes) / n + in.epsilon);
+#pragma unroll
+  for (int s = 0; s < 2 * kLanesPer; ++s) {
+    const int q = norm_vec4(s >> 1, s & 1);
+    if (q < vec4s) {
+      const float4 x = P.v[s], g = P.g[s];
+      stage4(xs, q, make_float4((x.x * r) * g.x, (x.y * r) * g.y, (x.z * r) * g.z,
+                                (x.w * r) * g.w));
+    }
+  }
+}
+
+// A lane's work: up to MAXI (row, group) items over its RH rows, ranges
+// rotated, their weights loaded up front. xoff is the item's group offset
+// in xs (-1: no item); dest the parts index its range's sum goes to when the
+// item closes the range (-1: it does not).
+template <int RH, int MAXI>
+struct LaneWork {
+  uint4 codes[MAXI];
+  uint16_t scale[MAXI];
+  int xoff[MAXI];
+  int dest[MAXI];
+  int empty_dest[RH];  // parts index of an empty range's zero (-1: none)
+};
+
+template <int RH, int MAXI>
+__device__ __forceinline__ void lane_work(LaneWork<RH, MAXI>& L, const Q4Matrix (&mats)[RH],
+                                          const int (&rows)[RH], const int (&slots)[RH], int r) {
+  const int groups = mats[0].cols >> 5;
+  int lo[RH], len[RH];
+#pragma unroll
+  for (int j = 0; j < RH; ++j) {
+    const int rr = (r + j) & 31;
+    lo[j] = rr * groups / kRanges;
+    len[j] = (rr + 1) * groups / kRanges - lo[j];
+    L.empty_dest[j] = len[j] == 0 ? slots[j] * 33 + rr : -1;
+  }
+#pragma unroll
+  for (int it = 0; it < MAXI; ++it) {
+    // Item it is the k-th group of the first row j whose ranges it reaches.
+    int k = it, g = -1, last = -1, row = -1, dest = -1;
+    const uint8_t* codes = mats[0].codes;
+    const uint16_t* scales = mats[0].scales;
+#pragma unroll
+    for (int j = 0; j < RH; ++j) {
+      if (g < 0) {
+        if (k < len[j]) {
+          g = lo[j] + k;
+          last = lo[j] + len[j] - 1;
+          row = rows[j];
+          dest = slots[j] * 33 + ((r + j) & 31);
+          codes = mats[j].codes;
+          scales = mats[j].scales;
+        } else {
+          k -= len[j];
+        }
+      }
+    }
+    L.xoff[it] = g < 0 ? -1 : g * kXStride;
+    L.dest[it] = g >= 0 && g == last ? dest : -1;
+    L.codes[it] = make_uint4(0, 0, 0, 0);
+    L.scale[it] = 0;
+    if (g >= 0 && row >= 0) {
+      const size_t blk = (size_t)row * groups + g;
+      L.codes[it] = reinterpret_cast<const uint4*>(codes)[blk];
+      L.scale[it] = scales[blk];
+    }
+  }
+}
+
+// The lane's chains; each range's sum goes to its parts entry.
+template <int RH, int MAXI>
+__device__ __forceinline__ void lane_chains(const LaneWork<RH, MAXI>& L, const float* xs,
+                                            float* parts) {
+#pragma unroll
+  for (int j = 0; j < RH; ++j) {
+    if (L.empty_dest[j] >= 0) parts[L.empty_dest[j]] = 0.0f;
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int it = 0; it < MAXI; ++it) {
+    if (L.xoff[it] >= 0) {
+      acc = chain_group(acc, L.codes[it], L.scale[it], xs + L.xoff[it]);
+      if (L.dest[it] >= 0) {
+        parts[L.dest[it]] = acc;
+        acc = 0.0f;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float row_total(const float* parts) {
+  float total = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kRanges; ++r) total = total + parts[r];
+  return total;
+}
+
+// A layer's pins on neuron n at `position` (edit.wgsl:55-76): the layer's
+// edits are sorted by neuron then first position (edit.cpp:20-31), so a
+// binary search finds the neuron's; its ranges never overlap.
+__device__ __forceinline__ float apply_pins(const uint32_t* __restrict__ t, int layer,
+                                            uint32_t n, uint32_t position, float value) {
+  const uint32_t first = t[2 * layer];
+  const uint32_t count = t[2 * layer + 1];
+  uint32_t lo = 0, hi = count;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (t[first + 5 * mid] < n) lo = mid + 1; else hi = mid;
+  }
+  for (uint32_t i = lo; i < count; ++i) {
+    const uint32_t* e = t + first + 5 * i;
+    if (e[0] != n) break;
+    if (position < e[3] || position >= e[4]) continue;
+    const float v = bits_to_float(e[2]);
+    if (e[1] == 1u) {
+      if (v != 1.0f) value = value * v;
+    } else {
+      value = v;
+    }
+  }
+  return value;
+}
+
+// A plain row's vec4s a thread loads: RH = 1 products take K up to 1,024
+// MAXI; RH = 2 ones (items of two rows' ranges at most 3) K below 1,536.
+template <int RH, int MAXI>
+constexpr int plain_vec4s() {
+  return RH == 1 ? (1024 * MAXI / 4 + kThreads - 1) / kThreads : (1536 / 4 + kThreads - 1) / kThreads;
+}
+
+// Write products: a tile is 2 RH kWaves rows, each wave two half-waves of RH
+// rows. A workgroup stages its input row once and takes tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ..., loading the next tile's weights before it
+// computes the current one.
+template <int RH, int MAXI, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __restrict__ step,
+                                                              Q4Matrix w, GemvInput in,
+                                                              float* __restrict__ y) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int kRows = 2 * RH * kWaves;
+  constexpr int X4 = plain_vec4s<RH, MAXI>();
+  float* parts = smem;
+  float* red = parts + kRows * 33;
+  float* xs = red + kRedFloats;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31;
+  const int slot0 = (wave * 2 + (lane >> 5)) * RH;
+  const int tiles = (w.rows + kRows - 1) / kRows;
+  int slots[RH];
+  Q4Matrix mats[RH];
+#pragma unroll
+  for (int j = 0; j < RH; ++j) {
+    slots[j] = slot0 + j;
+    mats[j] = w;
+  }
+  auto work_of = [&](LaneWork<RH, MAXI>& L, int tile) {
+    int rows[RH];
+#pragma unroll
+    for (int j = 0; j < RH; ++j) {
+      const int row = tile * kRows + slot0 + j;
+      rows[j] = row < w.rows ? row : -1;
+    }
+    lane_work<RH, MAXI>(L, mats, rows, slots, r);
+  };
+  int tile = blockIdx.x;
+  Prologue<X4> pro;
+  prologue_load<MODE, X4>(pro, in, step, w.cols);
+  LaneWork<RH, MAXI> cur;
+  work_of(cur, tile);
+  prologue_finish<MODE, X4>(xs, red, pro, in, w.cols);
+  __syncthreads();
+  for (;;) {
+    const int next = tile + gridDim.x;
+    LaneWork<RH, MAXI> nxt;
+    if (next < tiles) work_of(nxt, next);
+    lane_chains<RH, MAXI>(cur, xs, parts);
+    __syncthreads();
+    if (threadIdx.x < kRows) {
+      const int row = tile * kRows + threadIdx.x;
+      if (row < w.rows) y[row] = row_total(parts + threadIdx.x * 33);
+    }
+    if (next >= tiles) break;
+    __syncthreads();
+    cur = nxt;
+    tile = next;
+  }
+}
+
+// Gated product: each half-wave one neuron n, its gate row and its up row
+// (rotated ranges), then gelu_tanh(gate) * up and the layer's pins.
+template <int MAXI, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_gated_kernel(const DevStep* __restrict__ step,
+                                                              Q4Matrix gate, Q4Matrix up,
+                                                              GemvInput in, float* __restrict__ act,
+                                                              const uint32_t* __restrict__ edits,
+                                                              int layer) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int kNeurons = 2 * kWaves;
+  constexpr int X4 = kNormMaxCols / 4 / kThreads;
+  float* parts = smem;
+  float* red = parts + 2 * kNeurons * 33;
+  float* xs = red + kRedFloats;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31;
+  const int local = wave * 2 + (lane >> 5);
+  const int n = blockIdx.x * kNeurons + local;
+  const int rows[2] = {n < gate.rows ? n : -1, n < gate.rows ? n : -1};
+  const int slots[2] = {2 * local, 2 * local + 1};
+  const Q4Matrix mats[2] = {gate, up};
+  Prologue<X4> pro;
+  prologue_load<MODE, X4>(pro, in, step, gate.cols);
+  LaneWork<2, MAXI> L;
+  lane_work<2, MAXI>(L, mats, rows, slots, r);
+  prologue_finish<MODE, X4>(xs, red, pro, in, gate.cols);
+  __syncthreads();
+  lane_chains<2, MAXI>(L, xs, parts);
+  __syncthreads();
+  if (threadIdx.x < kNeurons) {
+    const int nn = blockIdx.x * kNeurons + threadIdx.x;
+    if (nn < gate.rows) {
+      const float g = row_total(parts + (2 * threadIdx.x) * 33);
+      const float u = row_total(parts + (2 * threadIdx.x + 1) * 33);
+      float v = gelu_tanh(g) * u;
+      if (edits) v = apply_pins(edits, layer, (uint32_t)nn, step->position, v);
+      act[nn] = v;
+    }
+  }
+}
+
+int max_items(int cols, int rh) {
+  const int groups = cols / 32;
+  int most = 0;
+  for (int r = 0; r < kRanges; ++r) {
+    int n = 0;
+    for (int j = 0; j < rh; ++j) {
+      const int rr = (r + j) & 31;
+      n += (rr + 1) * groups / kRanges - rr * groups / kRanges;
+    }
+    most = n > most ? n : most;
+  }
+  return most;
+}
+
+// Workgroups a product launches at most: beyond this, workgroups loop over
+// tiles (the 262,144-row head), staging their input row once.
+constexpr int kMaxWorkgroups = 4096;
+
+template <int RH, int MAXI, int MODE>
+hipError_t launch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w, const GemvInput& in,
+                        float* y) {
+  constexpr int kRows = 2 * RH * kWaves;
+  const size_t lds = (size_t)(kRows * 33 + kRedFloats + (w.cols / 32) * kXStride) * 4;
+  const int tiles = (w.rows + kRows - 1) / kRows;
+  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE>),
+                     dim3(tiles < kMaxWorkgroups ? tiles : kMaxWorkgroups), dim3(kThreads), lds,
+                     s, step, w, in, y);
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+                          const GemvInput& in, float* y) {
+  const int items1 = max_items(w.cols, 1);
+  const int items2 = max_items(w.cols, 2);
+  // Many rows: two rows a half-wave, ranges rotated, where that balances.
+  if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536) return launch_write<2, 3, MODE>(s, step, w, in, y);
+  if (items1 <= 1) return launch_write<1, 1, MODE>(s, step, w, in, y);
+  if (items1 <= 2) return launch_write<1, 2, MODE>(s, step, w, in, y);
+  if (items1 <= 4) return launch_write<1, 4, MODE>(s, step, w, in, y);
+  if (items1 <= 8) return launch_write<1, 8, MODE>(s, step, w, in, y);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+                              const GemvInput& in, int mode, float* y) {
+  if (w.cols % 32 != 0 || w.rows <= 0 || w.cols > 8 * 1024) return hipErrorInvalidValue;
+  if (mode != 0 && w.cols > kNormMaxCols) return hipErrorInvalidValue;
+  switch (mode) {
+    case 0: return dispatch_write<0>(s, step, w, in, y);
+    case 1: return dispatch_write<1>(s, step, w, in, y);
+    case 2: return dispatch_write<2>(s, step, w, in, y);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
+                               const Q4Matrix& up, const GemvInput& in, int mode, float* act,
+                               const uint32_t* edits, int layer) {
+  // Gate and up rows together: two rows' ranges, at most 4 items below K = 2,048.
+  if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
+      gate.cols > kNormMaxCols) {
+    return hipErrorInvalidValue;
+  }
+  constexpr int kNeurons = 2 * kWaves;
+  const int items = max_items(gate.cols, 2);
+  const size_t lds = (size_t)(2 * kNeurons * 33 + kRedFloats + (gate.cols / 32) * kXStride) * 4;
+  const dim3 grid((gate.rows + kNeurons - 1) / kNeurons);
+  if (mode != 0 && mode != 1) return hipErrorInvalidValue;
+  if (items <= 3) {
+    if (mode == 0)
+      hipLaunchKernelGGL((gemv_gated_kernel<3, 0>), grid, dim3(kThreads), lds, s, step, gate, up,
+                         in, act, edits, layer);
+    else
+      hipLaunchKernelGGL((gemv_gated_kernel<3, 1>), grid, dim3(kThreads), lds, s, step, gate, up,
+                         in, act, edits, layer);
+  } else if (items <= 4) {
+    if (mode == 0)
+      hipLaunchKernelGGL((gemv_gated_kernel<4, 0>), grid, dim3(kThreads), lds, s, step, gate, up,
+                         in, act, edits, layer);
+    else
+      hipLaunchKernelGGL((gemv_gated_kernel<4, 1>), grid, dim3(kThreads), lds, s, step, gate, up,
+                         in, act, edits, layer);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace frz

@@ -58,6 +58,31 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
                         Q4Matrix up, const float* x, float* act,
                         int max_tokens, const uint32_t* edits, int layer);
 
+// The input row of a decode product, made in the product's prologue.
+// mode 0: x as given. mode 1: hidden + post-norm(output) (written to
+// hidden_out by the first workgroup when not null), then RMSNorm with gain.
+// mode 2: the step's token's embedding row times scale (written to
+// hidden_out likewise), then RMSNorm with gain.
+struct GemvInput {
+  const float* x;
+  const float* hidden;
+  const float* output;
+  const float* post_gain;
+  const float* gain;
+  float* hidden_out;
+  Q4Matrix table;
+  const uint32_t* sampled;
+  float scale;
+  float epsilon;
+};
+hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+                              const GemvInput& in, int mode, float* y);
+// The gated decode product (prologue mode 0 or 1): act = gelu(gate) * up,
+// then layer `layer`'s pins.
+hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
+                               const Q4Matrix& up, const GemvInput& in, int mode, float* act,
+                               const uint32_t* edits, int layer);
+
 // ---- per-row kernels ---------------------------------------------------
 struct NormArgs {
   const float* gain;
@@ -110,6 +135,31 @@ struct AttentionArgs {
 };
 hipError_t launch_attention(hipStream_t s, const DevStep* step,
                             const AttentionArgs& a, int max_tokens);
+
+// One decode token's QK-norm, rope and KV append fused with its attention:
+// one workgroup a chunk; the last to finish folds them into `out`.
+struct DecodeAttentionArgs {
+  const float* qkv;           // the token's q (query_heads * d), k, v
+  const float* turns;
+  const float* query_gain;
+  const float* key_gain;
+  uint16_t* key_cache;
+  uint16_t* value_cache;
+  float* out;                 // query_heads * d
+  float* partials;            // [max_chunks][query_heads][d]
+  float* stats;               // [max_chunks][query_heads][4]
+  uint32_t* counter;          // zero between launches; the kernel leaves it zero
+  int slots;
+  int window;
+  int head_dim;
+  int query_heads;
+  int kv_heads;
+  int max_chunks;
+  float epsilon;
+  float scale_log2e;
+};
+hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
+                                   const DecodeAttentionArgs& a);
 
 hipError_t launch_gather(hipStream_t s, const DevStep* step, Q4Matrix table,
                          const uint32_t* sampled, float* hidden, float scale,

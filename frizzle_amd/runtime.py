@@ -214,6 +214,9 @@ class Model:
     def synthesize(self, seed):
         check(self.lib.frz_model_synthesize(self.handle, seed))
 
+    def set_graphs(self, enabled):
+        check(self.lib.frz_model_set_graphs(self.handle, int(enabled)))
+
     def set_edits(self, table):
         t = np.ascontiguousarray(table, dtype=np.uint32)
         check(self.lib.frz_model_set_edits(self.handle, t.ctypes.data, t.size))

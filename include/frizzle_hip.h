@@ -113,6 +113,15 @@ int frz_op_attention(frz_device* dev, const float* query, int q_stride,
                      float* out, int slots, int window, int head_dim,
                      int query_heads, int kv_heads, float scale,
                      uint32_t position, uint32_t tokens);
+/* One decode token's QK-norm, rope and F16 KV append fused with its attention
+ * (rope.wgsl + rope_cache.wgsl + attention.wgsl, one launch): qkv holds the
+ * token's 4 x 256 query, 256 key and 256 value floats; head_dim 256, 4 query
+ * heads on 1 key-value head. */
+int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
+                          const float* query_gain, const float* key_gain,
+                          uint16_t* key_cache, uint16_t* value_cache, float* out,
+                          int slots, int window, float epsilon, float scale,
+                          uint32_t position);
 /* Embedding rows times scale (kernels/gather/gather.wgsl:25-48). */
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales,
                   int rows, int cols, const uint32_t* ids, uint32_t tokens,
@@ -270,6 +279,11 @@ int frz_model_synthesize(frz_model* model, uint64_t seed);
  * position, end position] per edit), used by every later step. */
 int frz_model_set_edits(frz_model* model, const uint32_t* table,
                         uint32_t words);
+
+/* Whether fed decode steps replay one captured HIP graph (1, the default)
+ * or launch their kernels one by one (0: the same kernels, for tools that
+ * trace launches). */
+int frz_model_set_graphs(frz_model* model, int enabled);
 
 /* One step of `tokens` (1 .. 512) token ids from `position`
  * (kernels::Step, src/core/kernels/interface.h:163-188). With logits, the

@@ -304,3 +304,39 @@ def test_draw_matches_oracle(device, temperature, top_k, top_p, min_p):
         want = orc.draw(cand_bits, cand_ids, top_k, temperature, top_p, min_p,
                         counter=101 + trial, seed=seed)
         assert np.array_equal(dr.numpy(), want), (trial, dr.numpy(), want)
+
+
+@pytest.mark.parametrize("position,window,slots,base", [
+    (0, 512, 5120, 1e4), (63, 512, 5120, 1e4), (64, 512, 5120, 1e4), (700, 512, 640, 1e4),
+    (5000, 512, 5120, 1e4), (4100, 8192, 8192, 1e6), (1000, 64, 640, 1e4)])
+def test_rope_attention_decode_bit_exact(device, position, window, slots, base):
+    # The decode kernel fuses QK-norm, rope, the KV append and attention; its
+    # query, cache slot and output are the separate kernels' bits.
+    rng = np.random.default_rng(position + window)
+    qh, d = 4, 256
+    qkv = rng.normal(0, 2, 6 * d).astype(np.float32)
+    qg = (1 + 0.1 * rng.normal(0, 1, d)).astype(np.float32)
+    kg = (1 + 0.1 * rng.normal(0, 1, d)).astype(np.float32)
+    kc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16).view(np.uint16)
+    vc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16).view(np.uint16)
+    turns = fz.rope_turns(base, d)
+    dqkv, dk, dv = device.array(qkv), device.array(kc), device.array(vc)
+    dt, dqg, dkg = device.array(turns), device.array(qg), device.array(kg)
+    do = device.empty((qh * d,), np.float32)
+    fz._lib.check(fz.load().frz_op_rope_attention(
+        device.handle, dqkv.ptr, dt.ptr, dqg.ptr, dkg.ptr, dk.ptr, dv.ptr, do.ptr, slots,
+        window, 1e-6, 0.0625, position))
+    q = qkv[:qh * d].copy()
+    k = qkv[qh * d:(qh + 1) * d].copy()
+    v = qkv[(qh + 1) * d:].copy()
+    want_k, want_v = kc.copy(), vc.copy()
+    orc.lib().orc_rope_row(position, slots, d, qh, 1, 1e-6, turns.ctypes.data, qg.ctypes.data,
+                           kg.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                           want_k.ctypes.data, want_v.ctypes.data)
+    assert np.array_equal(dk.numpy(), want_k)
+    assert np.array_equal(dv.numpy(), want_v)
+    want = np.empty(qh * d, dtype=np.float32)
+    scale_log2e = np.float32(np.float64(np.float32(0.0625)) * 1.4426950408889634)
+    orc.lib().orc_attention_row(position, window, slots, d, qh, 1, scale_log2e, q.ctypes.data,
+                                want_k.ctypes.data, want_v.ctypes.data, want.ctypes.data)
+    assert_same_bits(do.numpy(), want, "decode attention")

@@ -105,6 +105,9 @@ def test_greedy_decode_token_identical(device, split):
         rest, _ = model.decode(len(prompt), steps - 1)
         got = np.concatenate([[first], rest]).astype(np.uint32)
     assert np.array_equal(got, want), (got, want)
+    # The logits the last token was drawn from, bit for bit.
+    lg = oracle.token(int(want[-2]), len(prompt) + steps - 2)
+    assert_same_bits(model.logits(), lg, "last decode logits")
     model.close()
 
 
@@ -119,14 +122,23 @@ def test_steered_and_original_token_identical(device):
                                 rng.uniform(-10, 10, 8))]
     edits = list({(e.layer, e.neuron): e for e in edits}.values())
     edits.append(fz.Edit(0, 5, fz.EditKind.SCALE, 3.0, 4, 9))
-    original, steered = model.paired(prompt, edits, max_tokens=steps)
+    original = model.generate(prompt, (), max_tokens=steps)
+    cand_o = model.candidates()
+    steered = model.generate(prompt, edits, max_tokens=steps)
+    cand_s = model.candidates()
     want_o, _ = oracle_run(oracle, prompt, steps, cfg,
                            np.zeros(2 * cfg.layers, dtype=np.uint32))
     oracle2 = orc.OracleModel(cfg.as_dict(), oracle.tensors)
     want_s, _ = oracle_run(oracle2, prompt, steps, cfg, placed(cfg, edits, len(prompt) - 1))
     assert np.array_equal(original, want_o)
     assert np.array_equal(steered, want_s)
-    assert not np.array_equal(original, steered)
+    # The pins act: the last step's candidate logits differ (a random-init
+    # model may keep its argmax, so the tokens alone need not).
+    assert not np.array_equal(cand_o[0::2], cand_s[0::2])
+    # And the original reply again, after the steered run, from the cached
+    # prompt: the same tokens (the cache is rewound where the edits act).
+    again = model.generate(prompt, (), max_tokens=steps)
+    assert np.array_equal(again, original)
     model.close()
 
 
