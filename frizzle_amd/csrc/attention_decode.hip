@@ -1,6 +1,9 @@
 // The decode attention kernel: one token's QK-norm, rope and KV append
-// fused with its attention over the cache (the chunk arithmetic is in
-// attention_common.h).
+// (rope.wgsl:51-138) fused with its attention over the cache; a workgroup
+// per (chunk, head). Only the chunk holding the token's own position needs
+// its key and value: that chunk's workgroups compute them (all four heads
+// redundantly, head 0 also appends them to the cache). The chunk states are
+// folded by the next launch (the O product's prologue, or the fold kernel).
 
 #include "attention_common.h"
 
@@ -8,83 +11,70 @@ namespace frz {
 namespace {
 using namespace attn;
 
-// ---- decode: rope + append + chunk + fold ------------------------------------
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
     const DevStep* __restrict__ step, DecodeAttentionArgs a) {
   __shared__ ChunkShared S;
   __shared__ float cosines[D / 2], sines[D / 2];
-  __shared__ float red[256];
-  __shared__ __align__(16) uint16_t knew[D];
-  __shared__ __align__(16) uint16_t vnew[D];
-  __shared__ int is_last;
   const int p = (int)step->position;
   const ChunkRange r = chunk_range(p, a.window, blockIdx.x);
   if ((int)blockIdx.x >= r.count) return;
+  const int h = blockIdx.y;
   const bool holds_p = r.c == p / kChunkKeys;
   const int own = holds_p ? p : -1;
   const int t = threadIdx.x;
-  // Heads: 4 query heads, then the key head, then the value head; 32 lanes
-  // each (rope.wgsl:97-118). Key and value only where this chunk holds p.
-  // Their loads go first, the cached rows' after, so the rope waits only for
-  // the former while the latter are in flight.
-  const int h = t >> 5, lane = t & 31;
-  const bool active = t < 192 && (h < QH || holds_p);
+  // Rope lanes, 32 a head: the query head h, then the key and the value
+  // (only where this chunk holds p). Their loads go first, the cached rows'
+  // after, so the rope waits only for the former.
+  const int role = t >> 5, lane = t & 31;
+  const bool active = role == 0 || (holds_p && role <= 2);
   float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
   if (active) {
-    const float* src = a.qkv + h * D;  // q heads, then k at 4 D, v at 5 D
+    const float* src = a.qkv + (role == 0 ? h : QH + role - 1) * D;
     va = ld4f(src + 4 * lane);
     vb = ld4f(src + D / 2 + 4 * lane);
   }
-  StageRegs R;
-  stage_load(R, a.key_cache, a.value_cache, a.slots, r, own);
+  uint4 kr[kKeyLoads], vr[kValueLoads];
+  key_load(kr, a.key_cache, a.slots, r, own);
+  value_load(vr, a.value_cache, a.slots, r, own);
   rope_angles(a.turns, (uint32_t)p, D / 2, cosines, sines, t, kThreads);
-  if (t < 256) red[t] = rope_lane_squares(va, vb);
+  // The head's sum of squares: the halving tree over its 32 lanes.
+  float sum = rope_lane_squares(va, vb);
+#pragma unroll
+  for (int stride = 16; stride > 0; stride >>= 1) sum = sum + __shfl_down(sum, stride, 32);
+  sum = __shfl(sum, 0, 32);
   __syncthreads();
-  for (int stride = 16; stride > 0; stride >>= 1) {
-    if (active && lane < stride) red[t] = red[t] + red[t + stride];
-    __syncthreads();
-  }
-  stage_store(S, R, r, own);
   if (active) {
-    if (h <= QH) {
-      rope_norm_rotate(va, vb, red[t - lane], D, a.epsilon, h < QH ? a.query_gain : a.key_gain,
-                       lane, cosines, sines);
+    if (role <= 1) {
+      rope_norm_rotate(va, vb, sum, D, a.epsilon, role == 0 ? a.query_gain : a.key_gain, lane,
+                       cosines, sines);
     }
-    if (h < QH) {
-      float* q = S.q + h * D;
+    if (role == 0) {
       const float sc = a.scale_log2e;
-      q[4 * lane] = va.x * sc; q[4 * lane + 1] = va.y * sc;
-      q[4 * lane + 2] = va.z * sc; q[4 * lane + 3] = va.w * sc;
-      q[D / 2 + 4 * lane] = vb.x * sc; q[D / 2 + 4 * lane + 1] = vb.y * sc;
-      q[D / 2 + 4 * lane + 2] = vb.z * sc; q[D / 2 + 4 * lane + 3] = vb.w * sc;
+      *reinterpret_cast<float4*>(S.q + 4 * lane) =
+          make_float4(va.x * sc, va.y * sc, va.z * sc, va.w * sc);
+      *reinterpret_cast<float4*>(S.q + D / 2 + 4 * lane) =
+          make_float4(vb.x * sc, vb.y * sc, vb.z * sc, vb.w * sc);
     } else {
-      uint16_t* dst = h == QH ? knew : vnew;
       const ushort4 pa = pack4_f16(va), pb = pack4_f16(vb);
-      *reinterpret_cast<ushort4*>(dst + 4 * lane) = pa;
-      *reinterpret_cast<ushort4*>(dst + D / 2 + 4 * lane) = pb;
-      uint16_t* cache = (h == QH ? a.key_cache : a.value_cache) + (size_t)(p % a.slots) * D;
-      *reinterpret_cast<ushort4*>(cache + 4 * lane) = pa;
-      *reinterpret_cast<ushort4*>(cache + D / 2 + 4 * lane) = pb;
+      uint16_t* row = role == 1 ? S.knew : S.v + (p - r.k_begin) * D;
+      *reinterpret_cast<ushort4*>(row + 4 * lane) = pa;
+      *reinterpret_cast<ushort4*>(row + D / 2 + 4 * lane) = pb;
+      if (h == 0) {
+        uint16_t* cache = (role == 1 ? a.key_cache : a.value_cache) + (size_t)(p % a.slots) * D;
+        *reinterpret_cast<ushort4*>(cache + 4 * lane) = pa;
+        *reinterpret_cast<ushort4*>(cache + D / 2 + 4 * lane) = pb;
+      }
     }
   }
+  value_store(S, vr, r, own);
   __syncthreads();
-  if (holds_p && t < D / 8) stage_put(S, p - r.k_begin, t, *reinterpret_cast<const uint4*>(knew + 8 * t),
-                                      *reinterpret_cast<const uint4*>(vnew + 8 * t));
-  __syncthreads();
-  chunk_state<true>(S, p, a.window, r, a.partials + (size_t)blockIdx.x * QH * D,
-                    a.stats + (size_t)blockIdx.x * QH * 4);
-  // Arrival: this thread's coherent stores complete, then one count.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t == 0) {
-    const uint32_t before =
-        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = before == (uint32_t)(r.count - 1);
+  if (r.k_begin + (t >> 2) == own) {
+    const uint4* src = reinterpret_cast<const uint4*>(S.knew + 64 * (t & 3));
+#pragma unroll
+    for (int m = 0; m < kKeyLoads; ++m) kr[m] = src[m];
   }
-  __syncthreads();
-  if (!is_last) return;
-  a.out[t] = fold_chunks<true>(a.partials, a.stats, r.count);
-  if (t == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const size_t slot = (size_t)blockIdx.x * QH + h;
+  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
 }
 
 }  // namespace
@@ -92,7 +82,8 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
                                    const DecodeAttentionArgs& a) {
   if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.max_chunks), dim3(kThreads), 0, s, step, a);
+  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.max_chunks, QH), dim3(kThreads), 0, s, step,
+                     a);
   return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
-// The prefill attention kernels: chunk states for every row of a step,
-// then each row's in-order fold (the chunk arithmetic is in
-// attention_common.h).
+// The step's chunk states for every row (a workgroup per chunk, row and
+// head), and the fold of each row's chunk states in chunk order
+// (attention.wgsl:403-438), which also serves the decode path when a row has
+// more chunks than the O product's prologue folds.
 
 #include "attention_common.h"
 
@@ -8,7 +9,6 @@ namespace frz {
 namespace {
 using namespace attn;
 
-// ---- prefill: chunk states, then the fold per row ------------------------------
 __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
     const DevStep* __restrict__ step, AttentionArgs a) {
   __shared__ ChunkShared S;
@@ -17,41 +17,152 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
   const int p = (int)step->position + row;
   const ChunkRange r = chunk_range(p, a.window, blockIdx.x);
   if ((int)blockIdx.x >= r.count) return;
-  const int t = threadIdx.x;
-  StageRegs R;
-  stage_load(R, a.key_cache, a.value_cache, a.slots, r, -1);
-  {
-    const float* q = a.query + (size_t)row * a.q_stride;
-    S.q[t] = q[t] * a.scale_log2e;  // kThreads == QH * D
+  const int h = blockIdx.z, t = threadIdx.x;
+  uint4 kr[kKeyLoads], vr[kValueLoads];
+  float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t < D / 4) q = ld4f(a.query + (size_t)row * a.q_stride + h * D + 4 * t);
+  key_load(kr, a.key_cache, a.slots, r, -1);
+  value_load(vr, a.value_cache, a.slots, r, -1);
+  if (t < D / 4) {
+    const float sc = a.scale_log2e;
+    *reinterpret_cast<float4*>(S.q + 4 * t) = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
   }
-  stage_store(S, R, r, -1);
+  value_store(S, vr, r, -1);
   __syncthreads();
-  const size_t slot = (size_t)row * a.max_chunks + blockIdx.x;
-  chunk_state<false>(S, p, a.window, r, a.partials + slot * QH * D, a.stats + slot * QH * 4);
+  const size_t slot = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
+  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
 }
 
-__global__ __launch_bounds__(kThreads) void attention_combine_kernel(
-    const DevStep* __restrict__ step, AttentionArgs a) {
-  const int row = blockIdx.x;
+// ---- fold ------------------------------------------------------------------
+// A workgroup folds one row's chunks for 64 dimensions of one head. The
+// chunk states are staged into LDS; each chunk's factors (a, b) follow from
+// the running maximum and liveness before it, found by a prefix scan (a
+// running maximum is a max while no chunk maximum is NaN; with one, lane 0
+// replays the recursion itself); then each dimension's chain
+// o = o a + po b, and l's, run in chunk order.
+constexpr int kFoldDims = 64;
+constexpr int kFoldBatch = 8;  // staging loads a thread keeps in flight
+
+__global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep* __restrict__ step,
+                                                                  FoldArgs f) {
+  extern __shared__ __align__(16) float fold_smem[];
+  const int row = blockIdx.y;
   if (row >= (int)step->tokens) return;
   const int p = (int)step->position + row;
-  const ChunkRange r = chunk_range(p, a.window, 0);
-  const size_t slot = (size_t)row * a.max_chunks;
-  a.out[(size_t)row * QH * D + threadIdx.x] =
-      fold_chunks<false>(a.partials + slot * QH * D, a.stats + slot * QH * 4, r.count);
+  const int count = chunk_range(p, f.window, 0).count;
+  const int h = blockIdx.x / (D / kFoldDims), dim0 = (blockIdx.x % (D / kFoldDims)) * kFoldDims;
+  const int t = threadIdx.x;
+  float* po = fold_smem;                                      // [count][64]
+  float4* st = reinterpret_cast<float4*>(po + f.max_chunks * kFoldDims);  // [count]
+  float* fa = reinterpret_cast<float*>(st + f.max_chunks);    // [count]
+  float* fb = fa + f.max_chunks;
+  float* mb = fb + f.max_chunks;                              // m before chunk c
+  int* lb = reinterpret_cast<int*>(mb + f.max_chunks);        // live before chunk c
+  const float* part = f.partials + (size_t)row * f.max_chunks * QH * D;
+  const float* stats = f.stats + (size_t)row * f.max_chunks * QH * 4;
+  // Stage: uint4 i of the head's block is chunk i / 16, dims 4 (i % 16).
+  const int vec4s = count * (kFoldDims / 4);
+  for (int base = 0; base < vec4s; base += kFoldBatch * kThreads) {
+    float4 v[kFoldBatch];
+#pragma unroll
+    for (int n = 0; n < kFoldBatch; ++n) {
+      const int i = base + t + n * kThreads;
+      if (i < vec4s) v[n] = ld4f(part + ((size_t)(i >> 4) * QH + h) * D + dim0 + 4 * (i & 15));
+    }
+#pragma unroll
+    for (int n = 0; n < kFoldBatch; ++n) {
+      const int i = base + t + n * kThreads;
+      if (i < vec4s) reinterpret_cast<float4*>(po)[i] = v[n];
+    }
+  }
+  for (int c = t; c < count; c += kThreads) st[c] = ld4f(stats + ((size_t)c * QH + h) * 4);
+  __syncthreads();
+  if (t < 64) {
+    bool carry_live = false, nan = false;
+    float carry_m = 0.0f;
+    for (int base = 0; base < count; base += 64) {
+      const int c = base + t;
+      const float4 s4 = c < count ? st[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool cl = c < count && s4.z != 0.0f;
+      nan = nan || (cl && s4.x != s4.x);
+      float v = cl ? s4.x : -__builtin_inff();
+      int lv = cl ? 1 : 0;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_up(v, off, 64);
+        const int ol = __shfl_up(lv, off, 64);
+        if (t >= off) {
+          v = __builtin_fmaxf(v, ov);
+          lv |= ol;
+        }
+      }
+      float ev = __shfl_up(v, 1, 64);
+      int el = __shfl_up(lv, 1, 64);
+      if (t == 0) {
+        ev = -__builtin_inff();
+        el = 0;
+      }
+      if (c < count) {
+        lb[c] = carry_live || el;
+        mb[c] = carry_live ? (el ? __builtin_fmaxf(carry_m, ev) : carry_m) : ev;
+      }
+      const float last_v = __shfl(v, 63, 64);
+      const int last_l = __shfl(lv, 63, 64);
+      carry_m = carry_live ? (last_l ? __builtin_fmaxf(carry_m, last_v) : carry_m) : last_v;
+      carry_live = carry_live || last_l;
+    }
+    if (__any(nan) && t == 0) {
+      bool live = false;
+      float m = 0.0f;
+      for (int c = 0; c < count; ++c) {
+        lb[c] = live;
+        mb[c] = m;
+        const Fold g = fold_factors(live, m, st[c].z != 0.0f, st[c].x);
+        m = g.m;
+        live = live || st[c].z != 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  for (int c = t; c < count; c += kThreads) {
+    const Fold g = fold_factors(lb[c] != 0, mb[c], st[c].z != 0.0f, st[c].x);
+    fa[c] = g.a;
+    fb[c] = g.b;
+  }
+  __syncthreads();
+  if (t < kFoldDims) {
+    bool live = false;
+    float l = 0.0f, o = 0.0f;
+    for (int c = 0; c < count; ++c) {
+      const float a = fa[c], b = fb[c];
+      l = l * a + st[c].y * b;
+      o = o * a + po[c * kFoldDims + t] * b;
+      live = live || st[c].z != 0.0f;
+    }
+    f.out[(size_t)row * QH * D + h * D + dim0 + t] = live ? o / l : 0.0f;
+  }
 }
 
 }  // namespace
 
+hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
+                                 int max_tokens) {
+  const size_t lds = (size_t)f.max_chunks * (kFoldDims * 4 + 16 + 4 * 4);
+  if (f.max_chunks <= 0 || f.max_chunks > kMaxFoldChunks) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_fold_kernel, dim3(QH * (D / kFoldDims), max_tokens), dim3(kThreads),
+                     lds, s, step, f);
+  return hipGetLastError();
+}
+
 hipError_t launch_attention(hipStream_t s, const DevStep* step, const AttentionArgs& a,
                             int max_tokens) {
   if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_chunk_kernel, dim3(a.max_chunks, max_tokens), dim3(kThreads), 0,
+  hipLaunchKernelGGL(attention_chunk_kernel, dim3(a.max_chunks, max_tokens, QH), dim3(kThreads), 0,
                      s, step, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attention_combine_kernel, dim3(max_tokens), dim3(kThreads), 0, s, step, a);
-  return hipGetLastError();
+  return launch_attention_fold(s, step, FoldArgs{a.partials, a.stats, a.out, a.window, a.max_chunks},
+                               max_tokens);
 }
 
 }  // namespace frz

@@ -297,24 +297,25 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
   const int max_chunks = attention_max_chunks(window, slots);
   const size_t part_floats = (size_t)max_chunks * 4 * 256;
   float* partials = nullptr;
-  uint32_t* counter = nullptr;
   if (int rc = check_hip(hipMalloc(&partials, (part_floats + part_floats / 64) * sizeof(float)),
                          "hipMalloc(partials)"))
     return rc;
-  int rc = check_hip(hipMalloc(&counter, 4), "hipMalloc(counter)");
-  if (rc == FRZ_OK) rc = check_hip(hipMemsetAsync(counter, 0, 4, dev->stream), "hipMemsetAsync");
-  if (rc == FRZ_OK) rc = device_put_step(dev, host_step(position, 1));
+  int rc = device_put_step(dev, host_step(position, 1));
   if (rc == FRZ_OK) {
     const float scale_log2e = (float)((double)scale * 1.4426950408889634);
-    DecodeAttentionArgs a{qkv,        turns,      query_gain, key_gain,   key_cache,
-                          value_cache, out,       partials,   partials + part_floats,
-                          counter,    slots,      window,     256,        4,
-                          1,          max_chunks, epsilon,    scale_log2e};
-    rc = device_finish(dev, launch_attention_decode(dev->stream, dev->step, a),
-                       "frz_op_rope_attention");
+    DecodeAttentionArgs a{qkv,        turns,    query_gain,            key_gain, key_cache,
+                          value_cache, partials, partials + part_floats, slots,   window,
+                          256,        4,        1,                     max_chunks, epsilon,
+                          scale_log2e};
+    hipError_t e = launch_attention_decode(dev->stream, dev->step, a);
+    if (e == hipSuccess) {
+      e = launch_attention_fold(dev->stream, dev->step,
+                                FoldArgs{partials, partials + part_floats, out, window, max_chunks},
+                                1);
+    }
+    rc = device_finish(dev, e, "frz_op_rope_attention");
   }
   (void)hipFree(partials);
-  if (counter) (void)hipFree(counter);
   return rc;
 }
 

@@ -102,7 +102,6 @@ struct frz_model {
         *stats = nullptr;
   uint32_t *topk_scratch = nullptr, *candidates = nullptr, *sampled = nullptr,
            *token_log = nullptr, *edits = nullptr;
-  uint32_t* counters = nullptr;  // a layer's decode-attention arrivals, zero between steps
   uint32_t token_log_capacity = 0;
   size_t partial_floats = 0;
   DevStep* step = nullptr;       // device
@@ -252,17 +251,28 @@ int enqueue_decode(frz_model* m, bool logits) {
     in.epsilon = c.epsilon;
     e = launch_gemv_decode(s, m->step, L.qkv, in, l == 0 ? 2 : 1, m->qkv);
     if (e == hipSuccess) {
-      DecodeAttentionArgs d{m->qkv,      L.turns,      L.gains[1], L.gains[2],
-                            L.kcache,    L.vcache,     m->attn,    m->partials,
-                            m->partials + m->partial_floats, m->counters + l, L.slots,
-                            L.window,    c.head_dim,   c.query_heads, c.kv_heads,
-                            L.max_chunks, c.epsilon,   scale_log2e};
+      DecodeAttentionArgs d{m->qkv,      L.turns,  L.gains[1],  L.gains[2], L.kcache,
+                            L.vcache,    m->partials, m->partials + m->partial_floats, L.slots,
+                            L.window,    c.head_dim, c.query_heads, c.kv_heads, L.max_chunks,
+                            c.epsilon,   scale_log2e};
       e = launch_attention_decode(s, m->step, d);
     }
+    // O: local layers fold their few chunks in the product's prologue.
     if (e == hipSuccess) {
       GemvInput x{};
-      x.x = m->attn;
-      e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+      if (L.max_chunks <= kFoldPrologueChunks) {
+        x.partials = m->partials;
+        x.stats = m->partials + m->partial_floats;
+        x.window = L.window;
+        e = launch_gemv_decode(s, m->step, L.o, x, 3, m->output);
+      } else {
+        e = launch_attention_fold(
+            s, m->step,
+            FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window, L.max_chunks},
+            1);
+        x.x = m->attn;
+        if (e == hipSuccess) e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+      }
     }
     if (e == hipSuccess) {
       GemvInput g{};
@@ -446,10 +456,13 @@ int frz_synth_tensor(const frz_model_config* config, uint64_t seed, int layer, i
 int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model** out) {
   if (!dev || !config || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_create: null argument");
   const frz_model_config& c = *config;
-  if (c.head_dim != 256 || c.query_heads != 4 * c.kv_heads || c.hidden % 32 != 0 ||
+  // The kernels are built for Gemma-3's attention shape (d = 256, four query
+  // heads on one key-value head), rows the norm prologues take (hidden at most
+  // 2,048) and contexts whose chunk states the fold stages at once.
+  if (c.head_dim != 256 || c.query_heads != 4 || c.kv_heads != 1 || c.hidden % 32 != 0 ||
       c.ffn % 32 != 0 || c.vocab < kCandidates || c.layers <= 0 || c.pattern <= 0 ||
       c.window <= 0 || c.context < kPrefillBlock || c.local_slots < c.window + kPrefillBlock ||
-      c.hidden > 4096) {
+      c.hidden > 2048 || attention_max_chunks(c.context, c.context) > kMaxFoldChunks) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_create: unsupported shape");
   }
   (void)hipSetDevice(dev->ordinal);
@@ -502,8 +515,6 @@ int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model*
   if (int rc = alloc(m, &m->act, B * c.ffn * 4)) return bail(rc);
   if (int rc = alloc(m, &m->logits, (size_t)c.vocab * 4)) return bail(rc);
   if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->counters, (size_t)c.layers * 4)) return bail(rc);
-  (void)hipMemsetAsync(m->counters, 0, (size_t)c.layers * 4, dev->stream);
   const int tiles = (c.vocab + kSelectionTile - 1) / kSelectionTile;
   const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
   if (int rc = alloc(m, &m->topk_scratch, (size_t)2 * kCandidates * (tiles + second) * 4))

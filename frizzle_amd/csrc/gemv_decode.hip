@@ -19,6 +19,7 @@
 // then makes the input row while the weights are in flight (loads return in
 // issue order, so the input row waits only for its own loads).
 
+#include "attention_common.h"
 #include "kernels.h"
 #include "numerics.h"
 
@@ -32,6 +33,13 @@ constexpr int kNormLanes = 256;  // the norm's reduction width
 constexpr int kLanesPer = kNormLanes / kThreads;  // norm lanes a thread holds
 constexpr int kRedFloats = 260;  // the tree's sums, its total at [256], padding to 16 B
 constexpr int kNormMaxCols = 2 * 4 * kNormLanes;  // two vec4s a norm lane
+constexpr int kFoldWidth = attn::QH * attn::D;    // the attention output a fold makes
+constexpr int kFoldVec4s = kFoldWidth / 4 / kThreads;
+
+// Chunks of 64 keys a position's window reaches (attention.wgsl:95-120).
+__device__ __forceinline__ int window_chunks(const DevStep* __restrict__ step, int window) {
+  return attn::chunk_range((int)step->position, window, 0).count;
+}
 
 __device__ __forceinline__ float half_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -125,6 +133,8 @@ struct Prologue {
   float4 g[2 * kLanesPer];   // the norm gain
   uint32_t word[2 * kLanesPer];
   uint16_t d[2 * kLanesPer];
+  float4 st;                                 // MODE 3: a chunk state's (m, l, live, 0)
+  float4 po[kFoldPrologueChunks][kFoldVec4s];  // MODE 3: the chunks' outputs
 };
 
 __device__ __forceinline__ int norm_vec4(int k, int m) {
@@ -142,6 +152,20 @@ __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& 
     for (int j = 0; j < X4; ++j) {
       const int q = (int)threadIdx.x + j * kThreads;
       if (q < vec4s) P.plain[j] = ld4(in.x + 4 * q);
+    }
+    return;
+  }
+  if (MODE == 3) {
+    const int count = window_chunks(step, in.window);
+    if ((int)threadIdx.x < count * attn::QH) P.st = ld4(in.stats + 4 * threadIdx.x);
+#pragma unroll
+    for (int c = 0; c < kFoldPrologueChunks; ++c) {
+      if (c < count) {
+#pragma unroll
+        for (int j = 0; j < kFoldVec4s; ++j) {
+          P.po[c][j] = ld4(in.partials + c * kFoldWidth + 4 * ((int)threadIdx.x + j * kThreads));
+        }
+      }
     }
     return;
   }
@@ -174,10 +198,65 @@ __device__ __forceinline__ float squares4(float4 a) {
   return dot4(a.x, a.y, a.z, a.w, a.x, a.y, a.z, a.w);
 }
 
+// The attention output from its chunk states (attention.wgsl:403-438): the
+// factors of chunk c for head h follow from the running maximum and
+// liveness before it, which thread (c, h) replays; each thread then folds
+// its vec4s' chains o = o a + po b (and the head's l) in chunk order, and
+// stages o / l.
+template <int X4>
+__device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prologue<X4>& P,
+                                              int count) {
+  constexpr int QH = attn::QH;
+  static_assert(6 * kFoldPrologueChunks * QH <= kRedFloats, "fold tables exceed the tree's LDS");
+  float4* st = reinterpret_cast<float4*>(red);  // [count][QH]
+  float* fa = red + 4 * kFoldPrologueChunks * QH;
+  float* fb = fa + kFoldPrologueChunks * QH;
+  const int t = threadIdx.x;
+  if (t < count * QH) st[t] = P.st;
+  __syncthreads();
+  if (t < count * QH) {
+    const int c = t / QH, h = t % QH;
+    bool live = false;
+    float m = 0.0f;
+    for (int b = 0; b < c; ++b) {
+      const float4 s = st[b * QH + h];
+      m = attn::fold_factors(live, m, s.z != 0.0f, s.x).m;
+      live = live || s.z != 0.0f;
+    }
+    const attn::Fold f = attn::fold_factors(live, m, P.st.z != 0.0f, P.st.x);
+    fa[t] = f.a;
+    fb[t] = f.b;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kFoldVec4s; ++j) {
+    const int q = t + j * kThreads, h = q / (attn::D / 4);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float l = 0.0f;
+    bool live = false;
+#pragma unroll
+    for (int c = 0; c < kFoldPrologueChunks; ++c) {
+      if (c < count) {
+        const float a = fa[c * QH + h], b = fb[c * QH + h];
+        const float4 s = st[c * QH + h], po = P.po[c][j];
+        l = l * a + s.y * b;
+        o.x = o.x * a + po.x * b;
+        o.y = o.y * a + po.y * b;
+        o.z = o.z * a + po.z * b;
+        o.w = o.w * a + po.w * b;
+        live = live || s.z != 0.0f;
+      }
+    }
+    stage4(xs, q, live ? make_float4(o.x / l, o.y / l, o.z / l, o.w / l)
+                       : make_float4(0.f, 0.f, 0.f, 0.f));
+  }
+}
+
 // Makes the input row from the loads and stages it into xs.
 template <int MODE, int X4>
 __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<X4>& P,
-                                                const GemvInput& in, int width) {
+                                                const GemvInput& in,
+                                                const DevStep* __restrict__ step, int width) {
   const int vec4s = width >> 2;
   if (MODE == 0) {
 #pragma unroll
@@ -185,6 +264,10 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
       const int q = (int)threadIdx.x + j * kThreads;
       if (q < vec4s) stage4(xs, q, P.plain[j]);
     }
+    return;
+  }
+  if (MODE == 3) {
+    fold_prologue(xs, red, P, window_chunks(step, in.window));
     return;
   }
   const float n = (float)width;
@@ -414,7 +497,7 @@ __global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __r
   prologue_load<MODE, X4>(pro, in, step, w.cols);
   LaneWork<RH, MAXI> cur;
   work_of(cur, tile);
-  prologue_finish<MODE, X4>(xs, red, pro, in, w.cols);
+  prologue_finish<MODE, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
   for (;;) {
     const int next = tile + gridDim.x;
@@ -458,7 +541,7 @@ __global__ __launch_bounds__(kThreads) void gemv_gated_kernel(const DevStep* __r
   prologue_load<MODE, X4>(pro, in, step, gate.cols);
   LaneWork<2, MAXI> L;
   lane_work<2, MAXI>(L, mats, rows, slots, r);
-  prologue_finish<MODE, X4>(xs, red, pro, in, gate.cols);
+  prologue_finish<MODE, X4>(xs, red, pro, in, step, gate.cols);
   __syncthreads();
   lane_chains<2, MAXI>(L, xs, parts);
   __syncthreads();
@@ -528,6 +611,9 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
     case 0: return dispatch_write<0>(s, step, w, in, y);
     case 1: return dispatch_write<1>(s, step, w, in, y);
     case 2: return dispatch_write<2>(s, step, w, in, y);
+    case 3:
+      if (w.cols != kFoldWidth || max_items(w.cols, 1) != 1) return hipErrorInvalidValue;
+      return launch_write<1, 1, 3>(s, step, w, in, y);
     default: return hipErrorInvalidValue;
   }
 }

@@ -62,7 +62,9 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
 // mode 0: x as given. mode 1: hidden + post-norm(output) (written to
 // hidden_out by the first workgroup when not null), then RMSNorm with gain.
 // mode 2: the step's token's embedding row times scale (written to
-// hidden_out likewise), then RMSNorm with gain.
+// hidden_out likewise), then RMSNorm with gain. mode 3: the attention
+// output, folded from the decode attention's chunk states (partials, stats;
+// at most kFoldPrologueChunks chunks at this window).
 struct GemvInput {
   const float* x;
   const float* hidden;
@@ -74,7 +76,11 @@ struct GemvInput {
   const uint32_t* sampled;
   float scale;
   float epsilon;
+  const float* partials;
+  const float* stats;
+  int window;
 };
+constexpr int kFoldPrologueChunks = 10;
 hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
                               const GemvInput& in, int mode, float* y);
 // The gated decode product (prologue mode 0 or 1): act = gelu(gate) * up,
@@ -137,7 +143,7 @@ hipError_t launch_attention(hipStream_t s, const DevStep* step,
                             const AttentionArgs& a, int max_tokens);
 
 // One decode token's QK-norm, rope and KV append fused with its attention:
-// one workgroup a chunk; the last to finish folds them into `out`.
+// one workgroup a (chunk, head), each writing its chunk state.
 struct DecodeAttentionArgs {
   const float* qkv;           // the token's q (query_heads * d), k, v
   const float* turns;
@@ -145,10 +151,8 @@ struct DecodeAttentionArgs {
   const float* key_gain;
   uint16_t* key_cache;
   uint16_t* value_cache;
-  float* out;                 // query_heads * d
   float* partials;            // [max_chunks][query_heads][d]
   float* stats;               // [max_chunks][query_heads][4]
-  uint32_t* counter;          // zero between launches; the kernel leaves it zero
   int slots;
   int window;
   int head_dim;
@@ -160,6 +164,18 @@ struct DecodeAttentionArgs {
 };
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
                                    const DecodeAttentionArgs& a);
+
+// Each row's chunk states folded in chunk order into out[row][heads * d].
+struct FoldArgs {
+  const float* partials;      // [tokens][max_chunks][query_heads][d]
+  const float* stats;         // [tokens][max_chunks][query_heads][4]
+  float* out;
+  int window;
+  int max_chunks;
+};
+hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
+                                 int max_tokens);
+constexpr int kMaxFoldChunks = 224;  // chunk states a fold stages in LDS: 14,272 keys
 
 hipError_t launch_gather(hipStream_t s, const DevStep* step, Q4Matrix table,
                          const uint32_t* sampled, float* hidden, float scale,
