@@ -37,7 +37,7 @@ struct ChunkShared {
   alignas(16) float q[D];              // the head's query, roped, times scale * log2(e)
   alignas(16) uint16_t v[kChunkKeys * D];  // value rows as stored
   alignas(16) uint16_t knew[D];        // the step's own key row, when the chunk holds it
-  float e[kChunkKeys];                 // weights
+  alignas(16) float e[kChunkKeys];     // weights
   float tile_top[kTiles];
   int tile_seen[kTiles];
   float tile_a[kTiles];
@@ -74,40 +74,55 @@ __device__ __forceinline__ ChunkRange chunk_range(int p, int window, int cs) {
   return r;
 }
 
-// Lane t's part of a key row: key k_begin + t / 4, halves 64 (t % 4) ..
-// +63. Rows at or past k_end, and the row `own` (supplied later), load
-// nothing.
+// The cache slot of the chunk's key k_begin + jj, from k_begin's slot `base`
+// (slots is at least a chunk).
+__device__ __forceinline__ int chunk_slot(int base, int jj, int slots) {
+  const int s = base + jj;
+  return s < slots ? s : s - slots;
+}
+
+// Loads are issued for every lane, whatever its row (rows at or past k_end
+// and the row `own`, supplied later, read row k_begin instead), and nothing
+// overwrites their registers until they are used: the code stays
+// straight-line, and a wait for earlier loads does not wait for these.
+
+// Lane t's part of a key row: key k_begin + t / 4, halves 64 (t % 4) .. +63.
+// A row past k_end only feeds scores that are never used.
 __device__ __forceinline__ void key_load(uint4 (&k)[kKeyLoads], const uint16_t* __restrict__ kc,
                                          int slots, const ChunkRange& r, int own) {
   const int jj = threadIdx.x >> 2, u = threadIdx.x & 3, j = r.k_begin + jj;
-  const bool load = jj < r.n_tiles * kTileKeys && j < r.k_end && j != own;
-  const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)(j % slots) * D + 64 * u);
+  const bool keep = jj < r.n_tiles * kTileKeys && j < r.k_end && j != own;
+  const int base = r.k_begin % slots;
+  const uint4* src = reinterpret_cast<const uint4*>(
+      kc + (size_t)(keep ? chunk_slot(base, jj, slots) : base) * D + 64 * u);
 #pragma unroll
-  for (int m = 0; m < kKeyLoads; ++m) k[m] = load ? src[m] : make_uint4(0, 0, 0, 0);
+  for (int m = 0; m < kKeyLoads; ++m) k[m] = src[m];
 }
 
 // Thread t's share of the value rows: uint4 i = t + 256 n of the chunk is
-// row i / 32, halves 8 (i % 32) .. +7; same exclusions.
+// row i / 32, halves 8 (i % 32) .. +7.
 __device__ __forceinline__ void value_load(uint4 (&v)[kValueLoads], const uint16_t* __restrict__ vc,
                                            int slots, const ChunkRange& r, int own) {
+  const int base = r.k_begin % slots;
 #pragma unroll
   for (int n = 0; n < kValueLoads; ++n) {
     const int i = threadIdx.x + n * kThreads;
     const int jj = i / (D / 8), w8 = i % (D / 8), j = r.k_begin + jj;
-    v[n] = make_uint4(0, 0, 0, 0);
-    if (jj < r.n_tiles * kTileKeys && j < r.k_end && j != own) {
-      v[n] = *reinterpret_cast<const uint4*>(vc + (size_t)(j % slots) * D + 8 * w8);
-    }
+    const bool keep = jj < r.n_tiles * kTileKeys && j < r.k_end && j != own;
+    v[n] = *reinterpret_cast<const uint4*>(
+        vc + (size_t)(keep ? chunk_slot(base, jj, slots) : base) * D + 8 * w8);
   }
 }
+// Stages the value rows into LDS: rows past k_end as zeros, every row but
+// `own`.
 __device__ __forceinline__ void value_store(ChunkShared& S, const uint4 (&v)[kValueLoads],
                                             const ChunkRange& r, int own) {
 #pragma unroll
   for (int n = 0; n < kValueLoads; ++n) {
     const int i = threadIdx.x + n * kThreads;
-    const int jj = i / (D / 8), w8 = i % (D / 8);
-    if (jj < r.n_tiles * kTileKeys && r.k_begin + jj != own) {
-      *reinterpret_cast<uint4*>(S.v + jj * D + 8 * w8) = v[n];
+    const int jj = i / (D / 8), w8 = i % (D / 8), j = r.k_begin + jj;
+    if (jj < r.n_tiles * kTileKeys && j != own) {
+      *reinterpret_cast<uint4*>(S.v + jj * D + 8 * w8) = j < r.k_end ? v[n] : make_uint4(0, 0, 0, 0);
     }
   }
 }
@@ -168,8 +183,9 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   const int tile = jj >> 3;
   bool chunk_live = false;
   float cm = 0.0f, my_old = 0.0f, my_top = 0.0f;
-  for (int tt = 0; tt < r.n_tiles; ++tt) {
-    if (S.tile_seen[tt]) {
+#pragma unroll
+  for (int tt = 0; tt < kTiles; ++tt) {
+    if (tt < r.n_tiles && S.tile_seen[tt]) {
       const float top_tile = S.tile_top[tt];
       const float old = chunk_live ? cm : top_tile;
       chunk_live = true;
@@ -213,11 +229,10 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   float o = 0.0f;
   for (int tt = 0; tt < r.n_tiles; ++tt) {
     o = o * S.tile_a[tt];
+    const float4 ea = ld4f(S.e + tt * kTileKeys), eb = ld4f(S.e + tt * kTileKeys + 4);
+    const float e[kTileKeys] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
 #pragma unroll
-    for (int b = 0; b < kTileKeys; ++b) {
-      const int key = tt * kTileKeys + b;
-      o = o + S.e[key] * h2f(S.v[key * D + t]);
-    }
+    for (int b = 0; b < kTileKeys; ++b) o = o + e[b] * h2f(S.v[(tt * kTileKeys + b) * D + t]);
   }
   partial[t] = o;
 }

@@ -15,28 +15,29 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
     const DevStep* __restrict__ step, DecodeAttentionArgs a) {
   __shared__ ChunkShared S;
   __shared__ float cosines[D / 2], sines[D / 2];
+  const int h = blockIdx.y, t = threadIdx.x;
+  // Rope lanes, 32 a head: the query head h, then the key and the value.
+  // Their loads and the turns go first (none depends on the position), the
+  // cached rows' after, so the rope waits only for the former.
+  const int role = t >> 5, lane = t & 31;
+  const float turn = a.turns[t & (D / 2 - 1)];
+  const float* src = a.qkv + (role == 0 || role > 2 ? h : QH + role - 1) * D;
+  float4 va = ld4f(src + 4 * lane), vb = ld4f(src + D / 2 + 4 * lane);
+  const float* gain = role == 1 ? a.key_gain : a.query_gain;
+  const float4 ga = ld4f(gain + 4 * lane), gb = ld4f(gain + D / 2 + 4 * lane);
+  __asm__ volatile("" ::: "memory");  // keep these loads ahead of the position's
   const int p = (int)step->position;
   const ChunkRange r = chunk_range(p, a.window, blockIdx.x);
   if ((int)blockIdx.x >= r.count) return;
-  const int h = blockIdx.y;
+  // Key and value are needed only where this chunk holds p.
   const bool holds_p = r.c == p / kChunkKeys;
   const int own = holds_p ? p : -1;
-  const int t = threadIdx.x;
-  // Rope lanes, 32 a head: the query head h, then the key and the value
-  // (only where this chunk holds p). Their loads go first, the cached rows'
-  // after, so the rope waits only for the former.
-  const int role = t >> 5, lane = t & 31;
   const bool active = role == 0 || (holds_p && role <= 2);
-  float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
-  if (active) {
-    const float* src = a.qkv + (role == 0 ? h : QH + role - 1) * D;
-    va = ld4f(src + 4 * lane);
-    vb = ld4f(src + D / 2 + 4 * lane);
-  }
   uint4 kr[kKeyLoads], vr[kValueLoads];
   key_load(kr, a.key_cache, a.slots, r, own);
   value_load(vr, a.value_cache, a.slots, r, own);
-  rope_angles(a.turns, (uint32_t)p, D / 2, cosines, sines, t, kThreads);
+  if (t < D / 2) rope_angle(turn, (uint32_t)p, &sines[t], &cosines[t]);
+  if (!active) va = vb = make_float4(0.f, 0.f, 0.f, 0.f);
   // The head's sum of squares: the halving tree over its 32 lanes.
   float sum = rope_lane_squares(va, vb);
 #pragma unroll
@@ -45,8 +46,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
   __syncthreads();
   if (active) {
     if (role <= 1) {
-      rope_norm_rotate(va, vb, sum, D, a.epsilon, role == 0 ? a.query_gain : a.key_gain, lane,
-                       cosines, sines);
+      rope_norm_rotate(va, vb, sum, D, a.epsilon, ga, gb, lane, cosines, sines);
     }
     if (role == 0) {
       const float sc = a.scale_log2e;

@@ -142,7 +142,10 @@ __device__ __forceinline__ int norm_vec4(int k, int m) {
 }
 
 // Issues the input row's loads: MODE 0 a plain row x; 1 hidden, output and
-// the gains; 2 the embedding of the step's token (gather.wgsl:25-48).
+// the gains; 2 the embedding of the step's token (gather.wgsl:25-48); 3 the
+// chunk states. Every load is issued unconditionally (out-of-range indexes
+// clamped, their values unused), so the code is straight-line and waiting
+// for these loads does not wait for the weights issued after them.
 template <int MODE, int X4>
 __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& in,
                                               const DevStep* __restrict__ step, int width) {
@@ -150,21 +153,20 @@ __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& 
   if (MODE == 0) {
 #pragma unroll
     for (int j = 0; j < X4; ++j) {
-      const int q = (int)threadIdx.x + j * kThreads;
-      if (q < vec4s) P.plain[j] = ld4(in.x + 4 * q);
+      const int q = min((int)threadIdx.x + j * kThreads, vec4s - 1);
+      P.plain[j] = ld4(in.x + 4 * q);
     }
     return;
   }
   if (MODE == 3) {
     const int count = window_chunks(step, in.window);
-    if ((int)threadIdx.x < count * attn::QH) P.st = ld4(in.stats + 4 * threadIdx.x);
+    P.st = ld4(in.stats + 4 * min((int)threadIdx.x, count * attn::QH - 1));
 #pragma unroll
     for (int c = 0; c < kFoldPrologueChunks; ++c) {
-      if (c < count) {
+      const int cc = min(c, count - 1);
 #pragma unroll
-        for (int j = 0; j < kFoldVec4s; ++j) {
-          P.po[c][j] = ld4(in.partials + c * kFoldWidth + 4 * ((int)threadIdx.x + j * kThreads));
-        }
+      for (int j = 0; j < kFoldVec4s; ++j) {
+        P.po[c][j] = ld4(in.partials + cc * kFoldWidth + 4 * ((int)threadIdx.x + j * kThreads));
       }
     }
     return;
@@ -176,20 +178,18 @@ __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& 
   for (int k = 0; k < kLanesPer; ++k) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const int q = norm_vec4(k, m), s = 2 * k + m;
-      if (q < vec4s) {
-        if (MODE == 1) {
-          P.v[s] = ld4(in.hidden + 4 * q);
-          P.y[s] = ld4(in.output + 4 * q);
-          P.pg[s] = ld4(in.post_gain + 4 * q);
-        } else {
-          const size_t blk = (size_t)token * groups + (q >> 3);
-          const int j = (4 * q) & 31;
-          P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
-          P.d[s] = in.table.scales[blk];
-        }
-        P.g[s] = ld4(in.gain + 4 * q);
+      const int q = min(norm_vec4(k, m), vec4s - 1), s = 2 * k + m;
+      if (MODE == 1) {
+        P.v[s] = ld4(in.hidden + 4 * q);
+        P.y[s] = ld4(in.output + 4 * q);
+        P.pg[s] = ld4(in.post_gain + 4 * q);
+      } else {
+        const size_t blk = (size_t)token * groups + (q >> 3);
+        const int j = (4 * q) & 31;
+        P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
+        P.d[s] = in.table.scales[blk];
       }
+      P.g[s] = ld4(in.gain + 4 * q);
     }
   }
 }
@@ -387,13 +387,11 @@ __device__ __forceinline__ void lane_work(LaneWork<RH, MAXI>& L, const Q4Matrix 
     }
     L.xoff[it] = g < 0 ? -1 : g * kXStride;
     L.dest[it] = g >= 0 && g == last ? dest : -1;
-    L.codes[it] = make_uint4(0, 0, 0, 0);
-    L.scale[it] = 0;
-    if (g >= 0 && row >= 0) {
-      const size_t blk = (size_t)row * groups + g;
-      L.codes[it] = reinterpret_cast<const uint4*>(codes)[blk];
-      L.scale[it] = scales[blk];
-    }
+    // Loaded unconditionally (block 0 for no item or a row past the end,
+    // whose sums are never written), keeping the loads straight-line.
+    const int blk = g >= 0 && row >= 0 ? row * groups + g : 0;
+    L.codes[it] = reinterpret_cast<const uint4*>(codes)[blk];
+    L.scale[it] = scales[blk];
   }
 }
 
@@ -459,10 +457,13 @@ constexpr int plain_vec4s() {
 }
 
 // Write products: a tile is 2 RH kWaves rows, each wave two half-waves of RH
-// rows. A workgroup stages its input row once and takes tiles blockIdx.x,
-// blockIdx.x + gridDim.x, ..., loading the next tile's weights before it
-// computes the current one.
-template <int RH, int MAXI, int MODE>
+// rows. A workgroup stages its input row once and takes TPW tiles,
+// blockIdx.x + k gridDim.x (clamped to the last tile, which a workgroup past
+// the end then recomputes with the same bits), loading each tile's weights
+// before it computes the one before. The tiles are unrolled into
+// straight-line code over two register buffers, so every wait is for the
+// oldest loads only.
+template <int RH, int MAXI, int MODE, int TPW>
 __global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __restrict__ step,
                                                               Q4Matrix w, GemvInput in,
                                                               float* __restrict__ y) {
@@ -483,6 +484,7 @@ __global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __r
     slots[j] = slot0 + j;
     mats[j] = w;
   }
+  auto tile_of = [&](int k) { return min((int)blockIdx.x + k * (int)gridDim.x, tiles - 1); };
   auto work_of = [&](LaneWork<RH, MAXI>& L, int tile) {
     int rows[RH];
 #pragma unroll
@@ -492,27 +494,22 @@ __global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __r
     }
     lane_work<RH, MAXI>(L, mats, rows, slots, r);
   };
-  int tile = blockIdx.x;
   Prologue<X4> pro;
   prologue_load<MODE, X4>(pro, in, step, w.cols);
-  LaneWork<RH, MAXI> cur;
-  work_of(cur, tile);
+  LaneWork<RH, MAXI> buf[2];
+  work_of(buf[0], tile_of(0));
   prologue_finish<MODE, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
-  for (;;) {
-    const int next = tile + gridDim.x;
-    LaneWork<RH, MAXI> nxt;
-    if (next < tiles) work_of(nxt, next);
-    lane_chains<RH, MAXI>(cur, xs, parts);
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    if (k + 1 < TPW) work_of(buf[(k + 1) & 1], tile_of(k + 1));
+    lane_chains<RH, MAXI>(buf[k & 1], xs, parts);
     __syncthreads();
     if (threadIdx.x < kRows) {
-      const int row = tile * kRows + threadIdx.x;
+      const int row = tile_of(k) * kRows + threadIdx.x;
       if (row < w.rows) y[row] = row_total(parts + threadIdx.x * 33);
     }
-    if (next >= tiles) break;
-    __syncthreads();
-    cur = nxt;
-    tile = next;
+    if (k + 1 < TPW) __syncthreads();
   }
 }
 
@@ -571,19 +568,18 @@ int max_items(int cols, int rh) {
   return most;
 }
 
-// Workgroups a product launches at most: beyond this, workgroups loop over
-// tiles (the 262,144-row head), staging their input row once.
-constexpr int kMaxWorkgroups = 4096;
+// Tiles a workgroup of the many-row product (the 262,144-row head) takes:
+// its input row is staged once for all of them.
+constexpr int kHeadTilesPerGroup = 8;
 
-template <int RH, int MAXI, int MODE>
+template <int RH, int MAXI, int MODE, int TPW>
 hipError_t launch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w, const GemvInput& in,
                         float* y) {
   constexpr int kRows = 2 * RH * kWaves;
   const size_t lds = (size_t)(kRows * 33 + kRedFloats + (w.cols / 32) * kXStride) * 4;
   const int tiles = (w.rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE>),
-                     dim3(tiles < kMaxWorkgroups ? tiles : kMaxWorkgroups), dim3(kThreads), lds,
-                     s, step, w, in, y);
+  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE, TPW>), dim3((tiles + TPW - 1) / TPW),
+                     dim3(kThreads), lds, s, step, w, in, y);
   return hipGetLastError();
 }
 
@@ -593,11 +589,12 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
   const int items1 = max_items(w.cols, 1);
   const int items2 = max_items(w.cols, 2);
   // Many rows: two rows a half-wave, ranges rotated, where that balances.
-  if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536) return launch_write<2, 3, MODE>(s, step, w, in, y);
-  if (items1 <= 1) return launch_write<1, 1, MODE>(s, step, w, in, y);
-  if (items1 <= 2) return launch_write<1, 2, MODE>(s, step, w, in, y);
-  if (items1 <= 4) return launch_write<1, 4, MODE>(s, step, w, in, y);
-  if (items1 <= 8) return launch_write<1, 8, MODE>(s, step, w, in, y);
+  if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536)
+    return launch_write<2, 3, MODE, kHeadTilesPerGroup>(s, step, w, in, y);
+  if (items1 <= 1) return launch_write<1, 1, MODE, 1>(s, step, w, in, y);
+  if (items1 <= 2) return launch_write<1, 2, MODE, 1>(s, step, w, in, y);
+  if (items1 <= 4) return launch_write<1, 4, MODE, 1>(s, step, w, in, y);
+  if (items1 <= 8) return launch_write<1, 8, MODE, 1>(s, step, w, in, y);
   return hipErrorInvalidValue;
 }
 
@@ -605,7 +602,10 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
 
 hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
                               const GemvInput& in, int mode, float* y) {
-  if (w.cols % 32 != 0 || w.rows <= 0 || w.cols > 8 * 1024) return hipErrorInvalidValue;
+  if (w.cols % 32 != 0 || w.rows <= 0 || w.cols > 8 * 1024 ||
+      (long long)w.rows * (w.cols / 32) >= (1ll << 31)) {
+    return hipErrorInvalidValue;
+  }
   if (mode != 0 && w.cols > kNormMaxCols) return hipErrorInvalidValue;
   switch (mode) {
     case 0: return dispatch_write<0>(s, step, w, in, y);
@@ -613,7 +613,7 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
     case 2: return dispatch_write<2>(s, step, w, in, y);
     case 3:
       if (w.cols != kFoldWidth || max_items(w.cols, 1) != 1) return hipErrorInvalidValue;
-      return launch_write<1, 1, 3>(s, step, w, in, y);
+      return launch_write<1, 1, 3, 1>(s, step, w, in, y);
     default: return hipErrorInvalidValue;
   }
 }
@@ -623,7 +623,7 @@ hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matri
                                const uint32_t* edits, int layer) {
   // Gate and up rows together: two rows' ranges, at most 4 items below K = 2,048.
   if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
-      gate.cols > kNormMaxCols) {
+      gate.cols > kNormMaxCols || (long long)gate.rows * (gate.cols / 32) >= (1ll << 31)) {
     return hipErrorInvalidValue;
   }
   constexpr int kNeurons = 2 * kWaves;

@@ -9,14 +9,16 @@ namespace frz {
 
 // Each pair's cos and sin at position p into LDS tables (rope.wgsl:122-129):
 // t = f32(p) * turns_k, angle = 2 pi (t - round(t)).
+__device__ __forceinline__ void rope_angle(float turn, uint32_t p, float* sine, float* cosine) {
+  const float tt = (float)p * turn;
+  const float angle = 6.283185307179586f * (tt - rint_(tt));
+  sincos_fixed(angle, sine, cosine);
+}
+
 __device__ __forceinline__ void rope_angles(const float* __restrict__ turns, uint32_t p,
                                             int half, float* cosines, float* sines,
                                             int t, int threads) {
-  for (int k = t; k < half; k += threads) {
-    const float tt = (float)p * turns[k];
-    const float angle = 6.283185307179586f * (tt - rint_(tt));
-    sincos_fixed(angle, &sines[k], &cosines[k]);
-  }
+  for (int k = t; k < half; k += threads) rope_angle(turns[k], p, &sines[k], &cosines[k]);
 }
 
 __device__ __forceinline__ float4 ld4f(const float* p) {
@@ -34,13 +36,11 @@ __device__ __forceinline__ float rope_lane_squares(float4 a, float4 b) {
 
 // Normalize by r = 1/sqrt(sum / d + eps), times the gain, then turn each pair
 // (k, k + d/2) by its angle: x' = x c - y s, y' = x s + y c.
+// The gain's values for the lane: ga at 4 lane, gb at d/2 + 4 lane.
 __device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum, int head_dim,
-                                                 float epsilon, const float* __restrict__ gain,
-                                                 int lane, const float* cosines,
-                                                 const float* sines) {
-  const int half = head_dim / 2;
+                                                 float epsilon, float4 ga, float4 gb, int lane,
+                                                 const float* cosines, const float* sines) {
   const float r = inverse_sqrt(sum / (float)head_dim + epsilon);
-  const float4 ga = ld4f(gain + 4 * lane), gb = ld4f(gain + half + 4 * lane);
   a.x = (a.x * r) * ga.x; a.y = (a.y * r) * ga.y;
   a.z = (a.z * r) * ga.z; a.w = (a.w * r) * ga.w;
   b.x = (b.x * r) * gb.x; b.y = (b.y * r) * gb.y;
@@ -54,6 +54,15 @@ __device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum
                                 a.z * s2 + b.z * c2, a.w * s3 + b.w * c3);
   a = ra;
   b = rb;
+}
+
+__device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum, int head_dim,
+                                                 float epsilon, const float* __restrict__ gain,
+                                                 int lane, const float* cosines,
+                                                 const float* sines) {
+  const int half = head_dim / 2;
+  rope_norm_rotate(a, b, sum, head_dim, epsilon, ld4f(gain + 4 * lane),
+                   ld4f(gain + half + 4 * lane), lane, cosines, sines);
 }
 
 __device__ __forceinline__ ushort4 pack4_f16(float4 v) {
