@@ -346,11 +346,8 @@ int frz_op_edit(frz_device* dev, const uint32_t* edits_dev, int layer, float* ac
 
 int frz_op_topk(frz_device* dev, const float* logits, int count, uint32_t* candidates_dev) {
   if (count < kCandidates) return fail(FRZ_ERR_ARGUMENT, "frz_op_topk: fewer than 64 logits");
-  const int tiles = (count + kSelectionTile - 1) / kSelectionTile;
-  const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
   uint32_t* scratch = nullptr;
-  if (int rc = check_hip(hipMalloc(&scratch, (size_t)2 * kCandidates * (tiles + second) * 4),
-                         "hipMalloc(topk)"))
+  if (int rc = check_hip(hipMalloc(&scratch, topk_scratch_words(count) * 4), "hipMalloc(topk)"))
     return rc;
   const int rc =
       device_finish(dev, launch_topk(dev->stream, logits, count, scratch, candidates_dev),

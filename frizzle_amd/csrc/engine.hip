@@ -158,12 +158,15 @@ int upload_q4(frz_model* m, const Q4Matrix& w, int row0, int rows, const void* d
 
 // The head, the selection and the draw, after the final norm wrote the step's
 // last row into `normed`.
-hipError_t enqueue_output(frz_model* m, int max_tokens) {
+// A fed decode step also advances the step parameters at its end.
+hipError_t enqueue_output(frz_model* m, int max_tokens, bool advance) {
   hipStream_t s = m->dev->stream;
   hipError_t e = launch_gemv(s, m->step, m->embedding, m->normed, m->c.hidden, m->logits,
                              m->c.vocab, max_tokens, true);
-  if (e == hipSuccess) e = launch_topk(s, m->logits, m->c.vocab, m->topk_scratch, m->candidates);
-  if (e == hipSuccess) e = launch_draw(s, m->step, m->candidates, m->sampled, m->token_log);
+  if (e == hipSuccess) {
+    e = launch_select(s, m->step, m->logits, m->c.vocab, m->topk_scratch, m->candidates,
+                      m->sampled, m->token_log, advance);
+  }
   return e;
 }
 
@@ -222,7 +225,7 @@ int enqueue_prefill(frz_model* m, int max_tokens, bool logits) {
                         c.epsilon, H, true};
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
-  if (logits && e == hipSuccess) e = enqueue_output(m, max_tokens);
+  if (logits && e == hipSuccess) e = enqueue_output(m, max_tokens, false);
   return check_hip(e, "enqueue_prefill");
 }
 
@@ -230,7 +233,7 @@ int enqueue_prefill(frz_model* m, int max_tokens, bool logits) {
 // that reads it. The hidden row alternates between two buffers: Q/K/V's
 // prologue reads hidden_b (layer 0: the embedding) and writes hidden;
 // gate-up's reads hidden and writes hidden_b.
-int enqueue_decode(frz_model* m, bool logits) {
+int enqueue_decode(frz_model* m, bool logits, bool advance) {
   const frz_model_config& c = m->c;
   hipStream_t s = m->dev->stream;
   const int H = c.hidden, qw = c.query_heads * c.head_dim;
@@ -296,12 +299,15 @@ int enqueue_decode(frz_model* m, bool logits) {
                         c.epsilon, H, true};
     e = launch_norm(s, m->step, final_norm, 1);
   }
-  if (logits && e == hipSuccess) e = enqueue_output(m, 1);
+  if (logits && e == hipSuccess) e = enqueue_output(m, 1, advance);
   return check_hip(e, "enqueue_decode");
 }
 
-int enqueue_step(frz_model* m, int max_tokens, bool logits) {
-  return max_tokens == 1 ? enqueue_decode(m, logits) : enqueue_prefill(m, max_tokens, logits);
+// `advance`: a fed decode step (logits drawn), whose last kernel advances
+// the step parameters for the next.
+int enqueue_step(frz_model* m, int max_tokens, bool logits, bool advance = false) {
+  return max_tokens == 1 ? enqueue_decode(m, logits, advance)
+                         : enqueue_prefill(m, max_tokens, logits);
 }
 
 int build_decode_graph(frz_model* m) {
@@ -310,8 +316,7 @@ int build_decode_graph(frz_model* m) {
   if (int rc = check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal),
                          "hipStreamBeginCapture"))
     return rc;
-  int rc = enqueue_step(m, 1, true);
-  if (rc == FRZ_OK) rc = check_hip(launch_advance(s, m->step), "advance");
+  int rc = enqueue_step(m, 1, true, true);
   hipGraph_t graph = nullptr;
   const int end_rc = check_hip(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
   if (rc != FRZ_OK) return rc;
@@ -326,8 +331,7 @@ int launch_decode_step(frz_model* m) {
   if (m->use_graphs) {
     return check_hip(hipGraphLaunch(m->decode_exec, m->dev->stream), "hipGraphLaunch");
   }
-  if (int rc = enqueue_step(m, 1, true)) return rc;
-  return check_hip(launch_advance(m->dev->stream, m->step), "advance");
+  return enqueue_step(m, 1, true, true);
 }
 
 int put_step(frz_model* m) {
@@ -515,10 +519,7 @@ int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model*
   if (int rc = alloc(m, &m->act, B * c.ffn * 4)) return bail(rc);
   if (int rc = alloc(m, &m->logits, (size_t)c.vocab * 4)) return bail(rc);
   if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
-  const int tiles = (c.vocab + kSelectionTile - 1) / kSelectionTile;
-  const int second = (tiles * kCandidates + kSelectionTile - 1) / kSelectionTile;
-  if (int rc = alloc(m, &m->topk_scratch, (size_t)2 * kCandidates * (tiles + second) * 4))
-    return bail(rc);
+  if (int rc = alloc(m, &m->topk_scratch, topk_scratch_words(c.vocab) * 4)) return bail(rc);
   if (int rc = alloc(m, &m->candidates, 2 * kCandidates * 4)) return bail(rc);
   if (int rc = alloc(m, &m->sampled, 4 * 4)) return bail(rc);
   m->token_log_capacity = 1u << 16;

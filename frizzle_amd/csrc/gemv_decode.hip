@@ -1,6 +1,7 @@
-// Decode (one token) Q4_0 products with their input's RMSNorm fused in
-// front, so each layer runs its norms inside the products that read them:
+// Decode (one token) Q4_0 products with their input row made in a prologue,
+// so each layer runs its norms inside the products that read them:
 //   the attention norm (and layer 0's embedding gather) before Q/K/V,
+//   the attention fold (local layers) before O,
 //   the feed-forward norm before gate/up (GELU and the pins after it).
 // Every workgroup computes its input row itself, redundantly, with the
 // reference's 256-invocation reduction tree (norm.wgsl:75-198), so every
@@ -13,11 +14,17 @@
 // products chained by fma from zero; the 32 range sums add in order to a
 // total from zero. Lane r of a half-wave takes range (r + j) mod 32 of the
 // half-wave's row j: the rotation spreads each row's longer ranges over
-// different lanes (at K = 1,152, four ranges of 32 hold two groups).
+// different lanes (at K = 1,152, four ranges of 32 hold two groups). A lane's
+// plan (which groups, where each range sum goes) is fixed for the kernel;
+// a tile only moves it by whole rows.
 //
-// Latency: a workgroup issues its input loads, then all its weight loads,
-// then makes the input row while the weights are in flight (loads return in
-// issue order, so the input row waits only for its own loads).
+// Latency: a workgroup issues its input loads, then its weight loads, then
+// makes the input row while the weights are in flight. Loads return in issue
+// order, so every load is issued unconditionally (out-of-range indexes
+// clamped, values unused) and the code stays straight-line: a wait for the
+// input row is then a wait for its own loads only. After the input row is
+// staged, each half-wave works alone: it writes its range sums to LDS and
+// totals its own rows, with no workgroup barrier.
 
 #include "attention_common.h"
 #include "kernels.h"
@@ -26,15 +33,12 @@
 namespace frz {
 namespace {
 
-constexpr int kWaves = 2;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kXStride = 36;     // a staged group of x: 32 floats + 4 of padding
+constexpr int kPartStride = 33;  // a row's 32 range sums + 1 of padding
 constexpr int kNormLanes = 256;  // the norm's reduction width
-constexpr int kLanesPer = kNormLanes / kThreads;  // norm lanes a thread holds
 constexpr int kRedFloats = 260;  // the tree's sums, its total at [256], padding to 16 B
 constexpr int kNormMaxCols = 2 * 4 * kNormLanes;  // two vec4s a norm lane
 constexpr int kFoldWidth = attn::QH * attn::D;    // the attention output a fold makes
-constexpr int kFoldVec4s = kFoldWidth / 4 / kThreads;
 
 // Chunks of 64 keys a position's window reaches (attention.wgsl:95-120).
 __device__ __forceinline__ int window_chunks(const DevStep* __restrict__ step, int window) {
@@ -47,6 +51,14 @@ __device__ __forceinline__ float half_to_float(uint16_t h) {
 
 __device__ __forceinline__ float4 ld4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
+}
+
+// Orders a wave's LDS accesses around it (a wave's LDS instructions execute
+// in program order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -85,31 +97,46 @@ __device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits,
   return acc;
 }
 
-// The norm's halving tree over its 256 lane sums (norm.wgsl:75-85). Thread t
-// holds lanes t + k kThreads; the levels above kThreads add in registers, the
-// next in LDS, the last six across wave 0. Every thread gets the total.
-__device__ __forceinline__ float tree_total(float* red, const float (&lanes)[kLanesPer]) {
+// ---- the input row ------------------------------------------------------------
+// T threads (128 or 256): norm lane t + k T (k < 256 / T) belongs to thread t
+// and holds vec4s lane and lane + 256, in slot 2 k + m.
+template <int T>
+struct Shape {
+  static_assert(T == 128 || T == 256, "workgroups of two or four waves");
+  static constexpr int kLanesPer = kNormLanes / T;
+  static constexpr int kFoldVec4s = kFoldWidth / 4 / T;
+};
+
+template <int T>
+__device__ __forceinline__ int norm_vec4(int k, int m) {
+  return (int)threadIdx.x + k * T + m * kNormLanes;
+}
+
+// The norm's halving tree over its 256 lane sums (norm.wgsl:75-85): the
+// levels above T add in registers, the next in LDS, the last six across
+// wave 0. Every thread gets the total.
+template <int T>
+__device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Shape<T>::kLanesPer]) {
+  constexpr int LP = Shape<T>::kLanesPer;
   const int t = threadIdx.x;
-  float v[kLanesPer];
+  float v[LP];
 #pragma unroll
-  for (int k = 0; k < kLanesPer; ++k) v[k] = lanes[k];
+  for (int k = 0; k < LP; ++k) v[k] = lanes[k];
 #pragma unroll
-  for (int width = kLanesPer; width > 1; width >>= 1) {
+  for (int width = LP; width > 1; width >>= 1) {
 #pragma unroll
     for (int k = 0; k < width / 2; ++k) v[k] = v[k] + v[k + width / 2];
   }
   float s = v[0];
-  if (kThreads > 64) {
-    red[t] = s;
-    __syncthreads();
+  red[t] = s;
+  __syncthreads();
 #pragma unroll
-    for (int stride = kThreads / 2; stride > 64; stride >>= 1) {
-      if (t < stride) red[t] = red[t] + red[t + stride];
-      __syncthreads();
-    }
-    if (t < 64) s = red[t] + red[t + 64];
+  for (int stride = T / 2; stride > 64; stride >>= 1) {
+    if (t < stride) red[t] = red[t] + red[t + stride];
+    __syncthreads();
   }
   if (t < 64) {
+    s = red[t] + red[t + 64];
 #pragma unroll
     for (int stride = 32; stride > 0; stride >>= 1) s = s + __shfl_down(s, stride, 64);
     if (t == 0) red[kNormLanes] = s;
@@ -122,40 +149,30 @@ __device__ __forceinline__ void stage4(float* xs, int q, float4 v) {
   *reinterpret_cast<float4*>(xs + (q >> 3) * kXStride + 4 * (q & 7)) = v;
 }
 
-// A prologue's loads. Plain rows: vec4s t + j kThreads. Norm rows: lane
-// t + k kThreads holds vec4s lane and lane + 256, in slot 2 k + m.
-template <int X4>
+template <int T, int X4>
 struct Prologue {
-  float4 plain[X4];
-  float4 v[2 * kLanesPer];   // hidden (MODE 1) or the embedding row (MODE 2)
-  float4 y[2 * kLanesPer];   // the block output (MODE 1)
-  float4 pg[2 * kLanesPer];  // its post-norm gain
-  float4 g[2 * kLanesPer];   // the norm gain
-  uint32_t word[2 * kLanesPer];
-  uint16_t d[2 * kLanesPer];
-  float4 st;                                 // MODE 3: a chunk state's (m, l, live, 0)
-  float4 po[kFoldPrologueChunks][kFoldVec4s];  // MODE 3: the chunks' outputs
+  static constexpr int S = 2 * Shape<T>::kLanesPer;
+  float4 plain[X4];  // MODE 0: vec4s t + j T of x
+  float4 v[S];       // hidden (MODE 1) or the embedding row (MODE 2)
+  float4 y[S];       // the block output (MODE 1)
+  float4 pg[S];      // its post-norm gain
+  float4 g[S];       // the norm gain
+  uint32_t word[S];
+  uint16_t d[S];
+  float4 st;                                                // MODE 3: a chunk state
+  float4 po[kFoldPrologueChunks][Shape<T>::kFoldVec4s];     // MODE 3: the chunks' outputs
 };
-
-__device__ __forceinline__ int norm_vec4(int k, int m) {
-  return (int)threadIdx.x + k * kThreads + m * kNormLanes;
-}
 
 // Issues the input row's loads: MODE 0 a plain row x; 1 hidden, output and
 // the gains; 2 the embedding of the step's token (gather.wgsl:25-48); 3 the
-// chunk states. Every load is issued unconditionally (out-of-range indexes
-// clamped, their values unused), so the code is straight-line and waiting
-// for these loads does not wait for the weights issued after them.
-template <int MODE, int X4>
-__device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& in,
+// chunk states.
+template <int MODE, int T, int X4>
+__device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInput& in,
                                               const DevStep* __restrict__ step, int width) {
   const int vec4s = width >> 2;
   if (MODE == 0) {
 #pragma unroll
-    for (int j = 0; j < X4; ++j) {
-      const int q = min((int)threadIdx.x + j * kThreads, vec4s - 1);
-      P.plain[j] = ld4(in.x + 4 * q);
-    }
+    for (int j = 0; j < X4; ++j) P.plain[j] = ld4(in.x + 4 * min((int)threadIdx.x + j * T, vec4s - 1));
     return;
   }
   if (MODE == 3) {
@@ -165,8 +182,8 @@ __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& 
     for (int c = 0; c < kFoldPrologueChunks; ++c) {
       const int cc = min(c, count - 1);
 #pragma unroll
-      for (int j = 0; j < kFoldVec4s; ++j) {
-        P.po[c][j] = ld4(in.partials + cc * kFoldWidth + 4 * ((int)threadIdx.x + j * kThreads));
+      for (int j = 0; j < Shape<T>::kFoldVec4s; ++j) {
+        P.po[c][j] = ld4(in.partials + cc * kFoldWidth + 4 * ((int)threadIdx.x + j * T));
       }
     }
     return;
@@ -175,22 +192,19 @@ __device__ __forceinline__ void prologue_load(Prologue<X4>& P, const GemvInput& 
   if (MODE == 2) token = step->fed ? in.sampled[0] : step->ids[0];
   const int groups = width >> 5;
 #pragma unroll
-  for (int k = 0; k < kLanesPer; ++k) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int q = min(norm_vec4(k, m), vec4s - 1), s = 2 * k + m;
-      if (MODE == 1) {
-        P.v[s] = ld4(in.hidden + 4 * q);
-        P.y[s] = ld4(in.output + 4 * q);
-        P.pg[s] = ld4(in.post_gain + 4 * q);
-      } else {
-        const size_t blk = (size_t)token * groups + (q >> 3);
-        const int j = (4 * q) & 31;
-        P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
-        P.d[s] = in.table.scales[blk];
-      }
-      P.g[s] = ld4(in.gain + 4 * q);
+  for (int s = 0; s < Prologue<T, X4>::S; ++s) {
+    const int q = min(norm_vec4<T>(s >> 1, s & 1), vec4s - 1);
+    if (MODE == 1) {
+      P.v[s] = ld4(in.hidden + 4 * q);
+      P.y[s] = ld4(in.output + 4 * q);
+      P.pg[s] = ld4(in.post_gain + 4 * q);
+    } else {
+      const size_t blk = (size_t)token * groups + (q >> 3);
+      const int j = (4 * q) & 31;
+      P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
+      P.d[s] = in.table.scales[blk];
     }
+    P.g[s] = ld4(in.gain + 4 * q);
   }
 }
 
@@ -203,8 +217,8 @@ __device__ __forceinline__ float squares4(float4 a) {
 // liveness before it, which thread (c, h) replays; each thread then folds
 // its vec4s' chains o = o a + po b (and the head's l) in chunk order, and
 // stages o / l.
-template <int X4>
-__device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prologue<X4>& P,
+template <int T, int X4>
+__device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prologue<T, X4>& P,
                                               int count) {
   constexpr int QH = attn::QH;
   static_assert(6 * kFoldPrologueChunks * QH <= kRedFloats, "fold tables exceed the tree's LDS");
@@ -229,8 +243,8 @@ __device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prolo
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kFoldVec4s; ++j) {
-    const int q = t + j * kThreads, h = q / (attn::D / 4);
+  for (int j = 0; j < Shape<T>::kFoldVec4s; ++j) {
+    const int q = t + j * T, h = q / (attn::D / 4);
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     float l = 0.0f;
     bool live = false;
@@ -253,39 +267,40 @@ __device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prolo
 }
 
 // Makes the input row from the loads and stages it into xs.
-template <int MODE, int X4>
-__device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<X4>& P,
+template <int MODE, int T, int X4>
+__device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<T, X4>& P,
                                                 const GemvInput& in,
                                                 const DevStep* __restrict__ step, int width) {
+  constexpr int LP = Shape<T>::kLanesPer, S = Prologue<T, X4>::S;
   const int vec4s = width >> 2;
   if (MODE == 0) {
 #pragma unroll
     for (int j = 0; j < X4; ++j) {
-      const int q = (int)threadIdx.x + j * kThreads;
+      const int q = (int)threadIdx.x + j * T;
       if (q < vec4s) stage4(xs, q, P.plain[j]);
     }
     return;
   }
   if (MODE == 3) {
-    fold_prologue(xs, red, P, window_chunks(step, in.window));
+    fold_prologue<T, X4>(xs, red, P, window_chunks(step, in.window));
     return;
   }
   const float n = (float)width;
-  float lanes[kLanesPer];
+  float lanes[LP];
   if (MODE == 1) {
     // hidden + post-normed block output (norm.wgsl:120-160)
 #pragma unroll
-    for (int k = 0; k < kLanesPer; ++k) {
+    for (int k = 0; k < LP; ++k) {
       lanes[k] = 0.0f;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        if (norm_vec4(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.y[2 * k + m]);
+        if (norm_vec4<T>(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.y[2 * k + m]);
       }
     }
-    const float ry = inverse_sqrt(tree_total(red, lanes) / n + in.epsilon);
+    const float ry = inverse_sqrt(tree_total<T>(red, lanes) / n + in.epsilon);
 #pragma unroll
-    for (int s = 0; s < 2 * kLanesPer; ++s) {
-      if (norm_vec4(s >> 1, s & 1) < vec4s) {
+    for (int s = 0; s < S; ++s) {
+      if (norm_vec4<T>(s >> 1, s & 1) < vec4s) {
         float4& x = P.v[s];
         const float4 y = P.y[s], g = P.pg[s];
         x.x = x.x + ((y.x * ry) * g.x) * 1.0f;
@@ -297,8 +312,8 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
   } else {
     // weight j of the token's group, times the scale
 #pragma unroll
-    for (int s = 0; s < 2 * kLanesPer; ++s) {
-      const int q = norm_vec4(s >> 1, s & 1);
+    for (int s = 0; s < S; ++s) {
+      const int q = norm_vec4<T>(s >> 1, s & 1);
       if (q < vec4s) {
         const int shift = ((4 * q) & 31) < 16 ? 0 : 4;
         const float d = half_to_float(P.d[s]);
@@ -314,23 +329,23 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
   }
   if (blockIdx.x == 0 && in.hidden_out) {
 #pragma unroll
-    for (int s = 0; s < 2 * kLanesPer; ++s) {
-      const int q = norm_vec4(s >> 1, s & 1);
+    for (int s = 0; s < S; ++s) {
+      const int q = norm_vec4<T>(s >> 1, s & 1);
       if (q < vec4s) *reinterpret_cast<float4*>(in.hidden_out + 4 * q) = P.v[s];
     }
   }
 #pragma unroll
-  for (int k = 0; k < kLanesPer; ++k) {
+  for (int k = 0; k < LP; ++k) {
     lanes[k] = 0.0f;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      if (norm_vec4(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.v[2 * k + m]);
+      if (norm_vec4<T>(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.v[2 * k + m]);
     }
   }
-  const float r = inverse_sqrt(tree_total(red, lanes) / n + in.epsilon);
+  const float r = inverse_sqrt(tree_total<T>(red, lanes) / n + in.epsilon);
 #pragma unroll
-  for (int s = 0; s < 2 * kLanesPer; ++s) {
-    const int q = norm_vec4(s >> 1, s & 1);
+  for (int s = 0; s < S; ++s) {
+    const int q = norm_vec4<T>(s >> 1, s & 1);
     if (q < vec4s) {
       const float4 x = P.v[s], g = P.g[s];
       stage4(xs, q, make_float4((x.x * r) * g.x, (x.y * r) * g.y, (x.z * r) * g.z,
@@ -339,77 +354,105 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
   }
 }
 
-// A lane's work: up to MAXI (row, group) items over its RH rows, ranges
-// rotated, their weights loaded up front. xoff is the item's group offset
-// in xs (-1: no item); dest the parts index its range's sum goes to when the
-// item closes the range (-1: it does not).
+// ---- a lane's plan and weights ------------------------------------------------
+// Item it of lane r is group off[it] of the half-wave's row jrow[it] (ranges
+// rotated); xoff its offset in xs (-1: no item); dest the parts index its
+// range's sum goes to when the item closes the range (-1: it does not).
 template <int RH, int MAXI>
-struct LaneWork {
-  uint4 codes[MAXI];
-  uint16_t scale[MAXI];
+struct LanePlan {
+  int off[MAXI];
+  int jrow[MAXI];
   int xoff[MAXI];
   int dest[MAXI];
   int empty_dest[RH];  // parts index of an empty range's zero (-1: none)
 };
 
 template <int RH, int MAXI>
-__device__ __forceinline__ void lane_work(LaneWork<RH, MAXI>& L, const Q4Matrix (&mats)[RH],
-                                          const int (&rows)[RH], const int (&slots)[RH], int r) {
-  const int groups = mats[0].cols >> 5;
+__device__ __forceinline__ void lane_plan(LanePlan<RH, MAXI>& P, int groups, int slot0, int r) {
   int lo[RH], len[RH];
 #pragma unroll
   for (int j = 0; j < RH; ++j) {
     const int rr = (r + j) & 31;
     lo[j] = rr * groups / kRanges;
     len[j] = (rr + 1) * groups / kRanges - lo[j];
-    L.empty_dest[j] = len[j] == 0 ? slots[j] * 33 + rr : -1;
+    P.empty_dest[j] = len[j] == 0 ? (slot0 + j) * kPartStride + rr : -1;
   }
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
     // Item it is the k-th group of the first row j whose ranges it reaches.
-    int k = it, g = -1, last = -1, row = -1, dest = -1;
-    const uint8_t* codes = mats[0].codes;
-    const uint16_t* scales = mats[0].scales;
+    int k = it, g = -1, last = -1, jsel = 0, dest = -1;
 #pragma unroll
     for (int j = 0; j < RH; ++j) {
       if (g < 0) {
         if (k < len[j]) {
           g = lo[j] + k;
           last = lo[j] + len[j] - 1;
-          row = rows[j];
-          dest = slots[j] * 33 + ((r + j) & 31);
-          codes = mats[j].codes;
-          scales = mats[j].scales;
+          jsel = j;
+          dest = (slot0 + j) * kPartStride + ((r + j) & 31);
         } else {
           k -= len[j];
         }
       }
     }
-    L.xoff[it] = g < 0 ? -1 : g * kXStride;
-    L.dest[it] = g >= 0 && g == last ? dest : -1;
-    // Loaded unconditionally (block 0 for no item or a row past the end,
-    // whose sums are never written), keeping the loads straight-line.
-    const int blk = g >= 0 && row >= 0 ? row * groups + g : 0;
-    L.codes[it] = reinterpret_cast<const uint4*>(codes)[blk];
-    L.scale[it] = scales[blk];
+    P.off[it] = g;
+    P.jrow[it] = jsel;
+    P.xoff[it] = g < 0 ? -1 : g * kXStride;
+    P.dest[it] = g >= 0 && g == last ? dest : -1;
+  }
+}
+
+template <int MAXI>
+struct LaneWeights {
+  uint4 codes[MAXI];
+  uint16_t scale[MAXI];
+};
+
+// Item it's block: row row0 + jrow of m (write products). Loaded
+// unconditionally (block 0 for no item or a row past the end, whose sums are
+// never written).
+template <int RH, int MAXI>
+__device__ __forceinline__ void load_rows(LaneWeights<MAXI>& W, const LanePlan<RH, MAXI>& P,
+                                          const Q4Matrix& m, int row0) {
+  const int groups = m.cols >> 5;
+#pragma unroll
+  for (int it = 0; it < MAXI; ++it) {
+    const int row = row0 + P.jrow[it];
+    const int blk = P.off[it] >= 0 && row < m.rows ? row * groups + P.off[it] : 0;
+    W.codes[it] = reinterpret_cast<const uint4*>(m.codes)[blk];
+    W.scale[it] = m.scales[blk];
+  }
+}
+
+// Item it's block: row n of gate (jrow 0) or up (jrow 1).
+template <int MAXI>
+__device__ __forceinline__ void load_neuron(LaneWeights<MAXI>& W, const LanePlan<2, MAXI>& P,
+                                            const Q4Matrix& gate, const Q4Matrix& up, int n) {
+  const int groups = gate.cols >> 5;
+#pragma unroll
+  for (int it = 0; it < MAXI; ++it) {
+    const int blk = P.off[it] >= 0 && n < gate.rows ? n * groups + P.off[it] : 0;
+    const uint4* codes = reinterpret_cast<const uint4*>(P.jrow[it] ? up.codes : gate.codes);
+    const uint16_t* scales = P.jrow[it] ? up.scales : gate.scales;
+    W.codes[it] = codes[blk];
+    W.scale[it] = scales[blk];
   }
 }
 
 // The lane's chains; each range's sum goes to its parts entry.
 template <int RH, int MAXI>
-__device__ __forceinline__ void lane_chains(const LaneWork<RH, MAXI>& L, const float* xs,
-                                            float* parts) {
+__device__ __forceinline__ void lane_chains(const LaneWeights<MAXI>& W, const LanePlan<RH, MAXI>& P,
+                                            const float* xs, float* parts) {
 #pragma unroll
   for (int j = 0; j < RH; ++j) {
-    if (L.empty_dest[j] >= 0) parts[L.empty_dest[j]] = 0.0f;
+    if (P.empty_dest[j] >= 0) parts[P.empty_dest[j]] = 0.0f;
   }
   float acc = 0.0f;
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
-    if (L.xoff[it] >= 0) {
-      acc = chain_group(acc, L.codes[it], L.scale[it], xs + L.xoff[it]);
-      if (L.dest[it] >= 0) {
-        parts[L.dest[it]] = acc;
+    if (P.xoff[it] >= 0) {
+      acc = chain_group(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
+      if (P.dest[it] >= 0) {
+        parts[P.dest[it]] = acc;
         acc = 0.0f;
       }
     }
@@ -451,106 +494,91 @@ __device__ __forceinline__ float apply_pins(const uint32_t* __restrict__ t, int 
 
 // A plain row's vec4s a thread loads: RH = 1 products take K up to 1,024
 // MAXI; RH = 2 ones (items of two rows' ranges at most 3) K below 1,536.
-template <int RH, int MAXI>
+template <int RH, int MAXI, int T>
 constexpr int plain_vec4s() {
-  return RH == 1 ? (1024 * MAXI / 4 + kThreads - 1) / kThreads : (1536 / 4 + kThreads - 1) / kThreads;
+  return RH == 1 ? (1024 * MAXI / 4 + T - 1) / T : (1536 / 4 + T - 1) / T;
 }
 
-// Write products: a tile is 2 RH kWaves rows, each wave two half-waves of RH
+// ---- kernels ------------------------------------------------------------------
+// Write products: a tile is 2 RH WAVES rows, each wave two half-waves of RH
 // rows. A workgroup stages its input row once and takes TPW tiles,
 // blockIdx.x + k gridDim.x (clamped to the last tile, which a workgroup past
 // the end then recomputes with the same bits), loading each tile's weights
 // before it computes the one before. The tiles are unrolled into
 // straight-line code over two register buffers, so every wait is for the
 // oldest loads only.
-template <int RH, int MAXI, int MODE, int TPW>
-__global__ __launch_bounds__(kThreads) void gemv_write_kernel(const DevStep* __restrict__ step,
-                                                              Q4Matrix w, GemvInput in,
-                                                              float* __restrict__ y) {
+template <int RH, int MAXI, int MODE, int TPW, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* __restrict__ step,
+                                                                Q4Matrix w, GemvInput in,
+                                                                float* __restrict__ y) {
   extern __shared__ __align__(16) float smem[];
-  constexpr int kRows = 2 * RH * kWaves;
-  constexpr int X4 = plain_vec4s<RH, MAXI>();
+  constexpr int T = 64 * WAVES;
+  constexpr int kRows = 2 * RH * WAVES;
+  constexpr int X4 = plain_vec4s<RH, MAXI, T>();
   float* parts = smem;
-  float* red = parts + kRows * 33;
+  float* red = parts + kRows * kPartStride;
   float* xs = red + kRedFloats;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31;
   const int slot0 = (wave * 2 + (lane >> 5)) * RH;
   const int tiles = (w.rows + kRows - 1) / kRows;
-  int slots[RH];
-  Q4Matrix mats[RH];
-#pragma unroll
-  for (int j = 0; j < RH; ++j) {
-    slots[j] = slot0 + j;
-    mats[j] = w;
-  }
   auto tile_of = [&](int k) { return min((int)blockIdx.x + k * (int)gridDim.x, tiles - 1); };
-  auto work_of = [&](LaneWork<RH, MAXI>& L, int tile) {
-    int rows[RH];
-#pragma unroll
-    for (int j = 0; j < RH; ++j) {
-      const int row = tile * kRows + slot0 + j;
-      rows[j] = row < w.rows ? row : -1;
-    }
-    lane_work<RH, MAXI>(L, mats, rows, slots, r);
-  };
-  Prologue<X4> pro;
-  prologue_load<MODE, X4>(pro, in, step, w.cols);
-  LaneWork<RH, MAXI> buf[2];
-  work_of(buf[0], tile_of(0));
-  prologue_finish<MODE, X4>(xs, red, pro, in, step, w.cols);
+  LanePlan<RH, MAXI> plan;
+  lane_plan<RH, MAXI>(plan, w.cols >> 5, slot0, r);
+  Prologue<T, X4> pro;
+  prologue_load<MODE, T, X4>(pro, in, step, w.cols);
+  LaneWeights<MAXI> buf[2];
+  load_rows<RH, MAXI>(buf[0], plan, w, tile_of(0) * kRows + slot0);
+  prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < TPW; ++k) {
-    if (k + 1 < TPW) work_of(buf[(k + 1) & 1], tile_of(k + 1));
-    lane_chains<RH, MAXI>(buf[k & 1], xs, parts);
-    __syncthreads();
-    if (threadIdx.x < kRows) {
-      const int row = tile_of(k) * kRows + threadIdx.x;
-      if (row < w.rows) y[row] = row_total(parts + threadIdx.x * 33);
+    if (k + 1 < TPW) load_rows<RH, MAXI>(buf[(k + 1) & 1], plan, w, tile_of(k + 1) * kRows + slot0);
+    lane_chains<RH, MAXI>(buf[k & 1], plan, xs, parts);
+    wave_sync();
+    if (r < RH) {
+      const int row = tile_of(k) * kRows + slot0 + r;
+      if (row < w.rows) y[row] = row_total(parts + (slot0 + r) * kPartStride);
     }
-    if (k + 1 < TPW) __syncthreads();
+    wave_sync();
   }
 }
 
 // Gated product: each half-wave one neuron n, its gate row and its up row
 // (rotated ranges), then gelu_tanh(gate) * up and the layer's pins.
-template <int MAXI, int MODE>
-__global__ __launch_bounds__(kThreads) void gemv_gated_kernel(const DevStep* __restrict__ step,
-                                                              Q4Matrix gate, Q4Matrix up,
-                                                              GemvInput in, float* __restrict__ act,
-                                                              const uint32_t* __restrict__ edits,
-                                                              int layer) {
+template <int MAXI, int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* __restrict__ step,
+                                                                Q4Matrix gate, Q4Matrix up,
+                                                                GemvInput in, float* __restrict__ act,
+                                                                const uint32_t* __restrict__ edits,
+                                                                int layer) {
   extern __shared__ __align__(16) float smem[];
-  constexpr int kNeurons = 2 * kWaves;
-  constexpr int X4 = kNormMaxCols / 4 / kThreads;
+  constexpr int T = 64 * WAVES;
+  constexpr int kNeurons = 2 * WAVES;
+  constexpr int X4 = kNormMaxCols / 4 / T;
   float* parts = smem;
-  float* red = parts + 2 * kNeurons * 33;
+  float* red = parts + 2 * kNeurons * kPartStride;
   float* xs = red + kRedFloats;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 31;
   const int local = wave * 2 + (lane >> 5);
   const int n = blockIdx.x * kNeurons + local;
-  const int rows[2] = {n < gate.rows ? n : -1, n < gate.rows ? n : -1};
-  const int slots[2] = {2 * local, 2 * local + 1};
-  const Q4Matrix mats[2] = {gate, up};
-  Prologue<X4> pro;
-  prologue_load<MODE, X4>(pro, in, step, gate.cols);
-  LaneWork<2, MAXI> L;
-  lane_work<2, MAXI>(L, mats, rows, slots, r);
-  prologue_finish<MODE, X4>(xs, red, pro, in, step, gate.cols);
+  LanePlan<2, MAXI> plan;
+  lane_plan<2, MAXI>(plan, gate.cols >> 5, 2 * local, r);
+  Prologue<T, X4> pro;
+  prologue_load<MODE, T, X4>(pro, in, step, gate.cols);
+  LaneWeights<MAXI> W;
+  load_neuron<MAXI>(W, plan, gate, up, n);
+  prologue_finish<MODE, T, X4>(xs, red, pro, in, step, gate.cols);
   __syncthreads();
-  lane_chains<2, MAXI>(L, xs, parts);
-  __syncthreads();
-  if (threadIdx.x < kNeurons) {
-    const int nn = blockIdx.x * kNeurons + threadIdx.x;
-    if (nn < gate.rows) {
-      const float g = row_total(parts + (2 * threadIdx.x) * 33);
-      const float u = row_total(parts + (2 * threadIdx.x + 1) * 33);
-      float v = gelu_tanh(g) * u;
-      if (edits) v = apply_pins(edits, layer, (uint32_t)nn, step->position, v);
-      act[nn] = v;
-    }
+  lane_chains<2, MAXI>(W, plan, xs, parts);
+  wave_sync();
+  if (r == 0 && n < gate.rows) {
+    const float g = row_total(parts + (2 * local) * kPartStride);
+    const float u = row_total(parts + (2 * local + 1) * kPartStride);
+    float v = gelu_tanh(g) * u;
+    if (edits) v = apply_pins(edits, layer, (uint32_t)n, step->position, v);
+    act[n] = v;
   }
 }
 
@@ -572,14 +600,14 @@ int max_items(int cols, int rh) {
 // its input row is staged once for all of them.
 constexpr int kHeadTilesPerGroup = 8;
 
-template <int RH, int MAXI, int MODE, int TPW>
+template <int RH, int MAXI, int MODE, int TPW, int WAVES>
 hipError_t launch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w, const GemvInput& in,
                         float* y) {
-  constexpr int kRows = 2 * RH * kWaves;
-  const size_t lds = (size_t)(kRows * 33 + kRedFloats + (w.cols / 32) * kXStride) * 4;
+  constexpr int kRows = 2 * RH * WAVES;
+  const size_t lds = (size_t)(kRows * kPartStride + kRedFloats + (w.cols / 32) * kXStride) * 4;
   const int tiles = (w.rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE, TPW>), dim3((tiles + TPW - 1) / TPW),
-                     dim3(kThreads), lds, s, step, w, in, y);
+  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE, TPW, WAVES>), dim3((tiles + TPW - 1) / TPW),
+                     dim3(64 * WAVES), lds, s, step, w, in, y);
   return hipGetLastError();
 }
 
@@ -590,12 +618,26 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
   const int items2 = max_items(w.cols, 2);
   // Many rows: two rows a half-wave, ranges rotated, where that balances.
   if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536)
-    return launch_write<2, 3, MODE, kHeadTilesPerGroup>(s, step, w, in, y);
-  if (items1 <= 1) return launch_write<1, 1, MODE, 1>(s, step, w, in, y);
-  if (items1 <= 2) return launch_write<1, 2, MODE, 1>(s, step, w, in, y);
-  if (items1 <= 4) return launch_write<1, 4, MODE, 1>(s, step, w, in, y);
-  if (items1 <= 8) return launch_write<1, 8, MODE, 1>(s, step, w, in, y);
+    return launch_write<2, 3, MODE, kHeadTilesPerGroup, 2>(s, step, w, in, y);
+  if (items1 <= 1) return launch_write<1, 1, MODE, 1, 2>(s, step, w, in, y);
+  if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2>(s, step, w, in, y);
+  if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2>(s, step, w, in, y);
+  if (items1 <= 8) return launch_write<1, 8, MODE, 1, 2>(s, step, w, in, y);
   return hipErrorInvalidValue;
+}
+
+template <int MAXI, int MODE>
+hipError_t launch_gated(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
+                        const Q4Matrix& up, const GemvInput& in, float* act,
+                        const uint32_t* edits, int layer) {
+  // Four waves: half as many workgroups making the input row.
+  constexpr int kWaves = 4, kNeurons = 2 * kWaves;
+  const size_t lds =
+      (size_t)(2 * kNeurons * kPartStride + kRedFloats + (gate.cols / 32) * kXStride) * 4;
+  hipLaunchKernelGGL((gemv_gated_kernel<MAXI, MODE, kWaves>),
+                     dim3((gate.rows + kNeurons - 1) / kNeurons), dim3(64 * kWaves), lds, s, step,
+                     gate, up, in, act, edits, layer);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -613,7 +655,7 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
     case 2: return dispatch_write<2>(s, step, w, in, y);
     case 3:
       if (w.cols != kFoldWidth || max_items(w.cols, 1) != 1) return hipErrorInvalidValue;
-      return launch_write<1, 1, 3, 1>(s, step, w, in, y);
+      return launch_write<1, 1, 3, 1, 2>(s, step, w, in, y);
     default: return hipErrorInvalidValue;
   }
 }
@@ -621,34 +663,22 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
 hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
                                const Q4Matrix& up, const GemvInput& in, int mode, float* act,
                                const uint32_t* edits, int layer) {
-  // Gate and up rows together: two rows' ranges, at most 4 items below K = 2,048.
+  // Gate and up rows together: two rows' ranges, at most 4 items to K = 2,048.
   if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
-      gate.cols > kNormMaxCols || (long long)gate.rows * (gate.cols / 32) >= (1ll << 31)) {
+      gate.cols > kNormMaxCols || (long long)gate.rows * (gate.cols / 32) >= (1ll << 31) ||
+      (mode != 0 && mode != 1)) {
     return hipErrorInvalidValue;
   }
-  constexpr int kNeurons = 2 * kWaves;
   const int items = max_items(gate.cols, 2);
-  const size_t lds = (size_t)(2 * kNeurons * 33 + kRedFloats + (gate.cols / 32) * kXStride) * 4;
-  const dim3 grid((gate.rows + kNeurons - 1) / kNeurons);
-  if (mode != 0 && mode != 1) return hipErrorInvalidValue;
   if (items <= 3) {
-    if (mode == 0)
-      hipLaunchKernelGGL((gemv_gated_kernel<3, 0>), grid, dim3(kThreads), lds, s, step, gate, up,
-                         in, act, edits, layer);
-    else
-      hipLaunchKernelGGL((gemv_gated_kernel<3, 1>), grid, dim3(kThreads), lds, s, step, gate, up,
-                         in, act, edits, layer);
-  } else if (items <= 4) {
-    if (mode == 0)
-      hipLaunchKernelGGL((gemv_gated_kernel<4, 0>), grid, dim3(kThreads), lds, s, step, gate, up,
-                         in, act, edits, layer);
-    else
-      hipLaunchKernelGGL((gemv_gated_kernel<4, 1>), grid, dim3(kThreads), lds, s, step, gate, up,
-                         in, act, edits, layer);
-  } else {
-    return hipErrorInvalidValue;
+    return mode == 0 ? launch_gated<3, 0>(s, step, gate, up, in, act, edits, layer)
+                     : launch_gated<3, 1>(s, step, gate, up, in, act, edits, layer);
   }
-  return hipGetLastError();
+  if (items <= 4) {
+    return mode == 0 ? launch_gated<4, 0>(s, step, gate, up, in, act, edits, layer)
+                     : launch_gated<4, 1>(s, step, gate, up, in, act, edits, layer);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace frz

@@ -185,10 +185,17 @@ hipError_t launch_edit(hipStream_t s, const DevStep* step,
                        int width, int max_tokens);
 
 // ---- output ------------------------------------------------------------
-// Top-64 of `count` logits into candidates (64 x {bits, token}); `scratch`
-// holds 2 * 64 * ceil(count / 1024) + 2 * 64 * ceil(that / 1024) words.
+// Top-64 of `count` logits into candidates (64 x {bits, token}), sorted;
+// `scratch` holds topk_scratch_words(count) words.
+size_t topk_scratch_words(int count);
 hipError_t launch_topk(hipStream_t s, const float* logits, int count,
                        uint32_t* scratch, uint32_t* candidates);
+// The top-64 as above, then the draw (as launch_draw) and, when `advance`,
+// the fed step's advance (as launch_advance), the last two in the final
+// selection kernel.
+hipError_t launch_select(hipStream_t s, DevStep* step, const float* logits, int count,
+                         uint32_t* scratch, uint32_t* candidates, uint32_t* sampled,
+                         uint32_t* token_log, bool advance);
 // The draw: record {token, failed, u bits, 0} into sampled; also appends
 // the token to token_log[step.drawn] when token_log is not null.
 hipError_t launch_draw(hipStream_t s, const DevStep* step,

@@ -8,62 +8,129 @@
 namespace frz {
 namespace {
 
-constexpr int kTopkThreads = 256;
+// Entries are ordered by the order-preserving key of their bits (larger
+// first) and, on equal keys, by the lower token (topk.wgsl:57-61); packed as
+// key << 32 | ~token, that order is the descending order of one 64-bit
+// integer. Slots past the input, and padding (token 0xFFFFFFFF), pack to 0
+// and sort last (topk.wgsl:138-166). The top 64 are found by sorted lists
+// of 64 held one entry a lane: a wave sorts 64 entries with a bitonic
+// network over its lanes, and merges two sorted lists into the top 64 of
+// both (the larger half of a bitonic merge), all through lane shuffles.
+constexpr int kTileThreads = kSelectionTile / 4;  // four entries a thread
+constexpr int kMergeWaves = 4;                    // lists merged by a workgroup: 4 waves x 4
+constexpr int kListsPerMerge = 16;
 
-// One pass: each workgroup keeps the top 64 of its tile of 1,024 entries,
-// sorted, as (logit bits, token) pairs. Entries are ordered by the
-// order-preserving key of their bits (larger first) and, on equal keys, by
-// the lower token (topk.wgsl:57-61); packed as key << 32 | ~token, that
-// order is the descending order of one 64-bit integer, sorted here by a
-// bitonic network. Slots past the input, and slots a pass before padded
-// (token 0xFFFFFFFF), pack to 0 and sort last (topk.wgsl:138-166).
-template <bool FIRST>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const uint32_t* __restrict__ in,
-                                                            int count,
-                                                            uint32_t* __restrict__ out) {
-  __shared__ uint64_t keys[kSelectionTile];
-  const int t = threadIdx.x;
-  for (int part = 0; part < 4; ++part) {
-    const int s = t + part * kTopkThreads;
-    const int e = blockIdx.x * kSelectionTile + s;
-    uint64_t packed = 0;
-    if (e < count) {
-      uint32_t bits, id;
-      if (FIRST) {
-        bits = in[e];
-        id = (uint32_t)e;
-      } else {
-        bits = in[2 * e];
-        id = in[2 * e + 1];
-      }
-      if (id != 0xFFFFFFFFu) packed = ((uint64_t)topk_key(bits) << 32) | (uint32_t)~id;
-    }
-    keys[s] = packed;
-  }
-  __syncthreads();
-  for (int k = 2; k <= kSelectionTile; k <<= 1) {
+__device__ __forceinline__ uint64_t pack_entry(uint32_t bits, uint32_t id) {
+  return id == 0xFFFFFFFFu ? 0ull : ((uint64_t)topk_key(bits) << 32) | (uint32_t)~id;
+}
+
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, mask, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), mask, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// The wave's 64 entries (one a lane) sorted descending over the lanes.
+__device__ __forceinline__ uint64_t wave_sort(uint64_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int part = 0; part < 2; ++part) {
-        const int i = t + part * kTopkThreads;  // one of 512 pairs
-        const int i1 = (i / j) * 2 * j + (i % j);
-        const int i2 = i1 + j;
-        const bool descending = (i1 & k) == 0;
-        const uint64_t x = keys[i1], y = keys[i2];
-        if ((x < y) == descending) {
-          keys[i1] = y;
-          keys[i2] = x;
-        }
-      }
-      __syncthreads();
+      const uint64_t o = shfl_xor64(v, j);
+      const bool keep_max = ((lane & j) == 0) == ((lane & k) == 0);
+      v = keep_max ? (v > o ? v : o) : (v < o ? v : o);
     }
   }
-  if (t < kCandidates) {
-    const uint64_t packed = keys[t];
-    const uint32_t key = (uint32_t)(packed >> 32);
-    const uint32_t id = ~(uint32_t)packed;
-    out[2 * (blockIdx.x * kCandidates + t)] = topk_bits(key);
-    out[2 * (blockIdx.x * kCandidates + t) + 1] = id;
+  return v;
+}
+
+// The top 64 of two descending lists, descending: the larger of a[i] and
+// b[63 - i] is a bitonic list holding them, which half-cleaners sort.
+__device__ __forceinline__ uint64_t wave_merge(uint64_t a, uint64_t b) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t br = shfl64(b, 63 - lane);
+  uint64_t v = a > br ? a : br;
+#pragma unroll
+  for (int j = 32; j > 0; j >>= 1) {
+    const uint64_t o = shfl_xor64(v, j);
+    v = (lane & j) == 0 ? (v > o ? v : o) : (v < o ? v : o);
   }
+  return v;
+}
+
+__device__ __forceinline__ void store_entry(uint32_t* out, int i, uint64_t v) {
+  out[2 * i] = topk_bits((uint32_t)(v >> 32));
+  out[2 * i + 1] = ~(uint32_t)v;
+}
+
+// The workgroup's waves' lists merged into wave 0's (a tree over LDS).
+template <int WAVES>
+__device__ __forceinline__ uint64_t merge_waves(uint64_t top, uint64_t (*lists)[64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int width = WAVES / 2; width >= 1; width >>= 1) {
+    if (wave >= width && wave < 2 * width) lists[wave][lane] = top;
+    __syncthreads();
+    if (wave < width) top = wave_merge(top, lists[wave + width][lane]);
+    __syncthreads();
+  }
+  return top;
+}
+
+// Pass one: the top 64 of each tile of 1,024 logits, sorted.
+__global__ __launch_bounds__(kTileThreads) void topk_tile_kernel(const uint32_t* __restrict__ in,
+                                                                 int count,
+                                                                 uint32_t* __restrict__ out) {
+  __shared__ uint64_t lists[kTileThreads / 64][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int base = blockIdx.x * kSelectionTile + wave * 4 * 64 + lane;
+  uint64_t v[4];
+#pragma unroll
+  for (int part = 0; part < 4; ++part) {
+    const int e = base + part * 64;
+    v[part] = e < count ? pack_entry(in[e], (uint32_t)e) : 0ull;
+  }
+  uint64_t top = wave_sort(v[0]);
+#pragma unroll
+  for (int part = 1; part < 4; ++part) top = wave_merge(top, wave_sort(v[part]));
+  top = merge_waves<kTileThreads / 64>(top, lists);
+  if (wave == 0) store_entry(out, blockIdx.x * kCandidates + lane, top);
+}
+
+// Merges sorted lists of 64 (bits, token) pairs, kListsPerMerge a
+// workgroup, into one sorted list each.
+__device__ __forceinline__ uint64_t merge_lists(const uint32_t* __restrict__ in, int lists,
+                                                uint64_t (*shared)[64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t v[kListsPerMerge / kMergeWaves];
+#pragma unroll
+  for (int u = 0; u < kListsPerMerge / kMergeWaves; ++u) {
+    const int l = blockIdx.x * kListsPerMerge + wave + u * kMergeWaves;
+    v[u] = 0ull;
+    if (l < lists) {
+      const int i = l * kCandidates + lane;
+      v[u] = pack_entry(in[2 * i], in[2 * i + 1]);
+    }
+  }
+  uint64_t top = v[0];
+#pragma unroll
+  for (int u = 1; u < kListsPerMerge / kMergeWaves; ++u) top = wave_merge(top, v[u]);
+  return merge_waves<kMergeWaves>(top, shared);
+}
+
+__global__ __launch_bounds__(64 * kMergeWaves) void topk_merge_kernel(const uint32_t* __restrict__ in,
+                                                                      int lists,
+                                                                      uint32_t* __restrict__ out) {
+  __shared__ uint64_t shared[kMergeWaves][64];
+  const uint64_t top = merge_lists(in, lists, shared);
+  if (threadIdx.x < 64) store_entry(out, blockIdx.x * kCandidates + threadIdx.x, top);
 }
 
 // The high word of a * b from 16-bit halves (draw.wgsl:34-45).
@@ -77,11 +144,8 @@ __device__ __forceinline__ uint32_t mulhi16(uint32_t a, uint32_t b) {
 // The draw (draw.wgsl:77-170), by one lane: every sum the reference takes
 // runs in candidate order on one invocation there too, and the per-candidate
 // exponentials are independent, so one lane gives the same bits.
-__global__ __launch_bounds__(64) void draw_kernel(const DevStep* __restrict__ step,
-                                                  const uint32_t* __restrict__ cand,
-                                                  uint32_t* __restrict__ sampled,
-                                                  uint32_t* __restrict__ token_log) {
-  if (threadIdx.x != 0) return;
+__device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __restrict__ sampled,
+                         uint32_t* __restrict__ token_log) {
   const uint32_t k = min(step->top_k, (uint32_t)kCandidates);
   const bool use_top_p = step->top_p < 1.0f;
   const float temperature = step->temperature;
@@ -158,8 +222,8 @@ __global__ __launch_bounds__(64) void draw_kernel(const DevStep* __restrict__ st
   }
 }
 
-__global__ void advance_kernel(DevStep* step) {
-  if (threadIdx.x != 0) return;
+// A fed step's advance of the step parameters.
+__device__ void advance_one(DevStep* step) {
   step->position += step->tokens;
   step->tokens = 1;
   step->fed = 1;
@@ -167,29 +231,83 @@ __global__ void advance_kernel(DevStep* step) {
   step->drawn += 1;
 }
 
+__global__ __launch_bounds__(64) void draw_kernel(const DevStep* __restrict__ step,
+                                                  const uint32_t* __restrict__ cand,
+                                                  uint32_t* __restrict__ sampled,
+                                                  uint32_t* __restrict__ token_log) {
+  if (threadIdx.x == 0) draw_one(step, cand, sampled, token_log);
+}
+
+__global__ void advance_kernel(DevStep* step) {
+  if (threadIdx.x == 0) advance_one(step);
+}
+
+// The last merge (at most kListsPerMerge lists), the draw from its list and,
+// for a fed decode step, the advance.
+__global__ __launch_bounds__(64 * kMergeWaves) void topk_draw_kernel(
+    const uint32_t* __restrict__ in, int lists, uint32_t* __restrict__ cand, DevStep* step,
+    uint32_t* __restrict__ sampled, uint32_t* __restrict__ token_log, int advance) {
+  __shared__ uint64_t shared[kMergeWaves][64];
+  __shared__ uint32_t final_list[2 * kCandidates];
+  const uint64_t top = merge_lists(in, lists, shared);
+  if (threadIdx.x < 64) {
+    store_entry(cand, threadIdx.x, top);
+    store_entry(final_list, threadIdx.x, top);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    draw_one(step, final_list, sampled, token_log);
+    if (advance) advance_one(step);
+  }
+}
+
+// Pass one into scratch, then merges of kListsPerMerge lists a workgroup
+// until one list is left; `last` launches the final merge.
+template <typename Last>
+hipError_t select_passes(hipStream_t s, const float* logits, int count, uint32_t* scratch,
+                         Last last) {
+  if (count < kCandidates) return hipErrorInvalidValue;
+  int lists = (count + kSelectionTile - 1) / kSelectionTile;
+  uint32_t* bufs[2] = {scratch, scratch + 2 * kCandidates * lists};
+  hipLaunchKernelGGL(topk_tile_kernel, dim3(lists), dim3(kTileThreads), 0, s,
+                     reinterpret_cast<const uint32_t*>(logits), count, bufs[0]);
+  hipError_t e = hipGetLastError();
+  int at = 0;
+  while (e == hipSuccess && lists > kListsPerMerge) {
+    const int groups = (lists + kListsPerMerge - 1) / kListsPerMerge;
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(groups), dim3(64 * kMergeWaves), 0, s, bufs[at],
+                       lists, bufs[at ^ 1]);
+    e = hipGetLastError();
+    lists = groups;
+    at ^= 1;
+  }
+  return e == hipSuccess ? last(bufs[at], lists) : e;
+}
+
 }  // namespace
+
+size_t topk_scratch_words(int count) {
+  const int lists = (count + kSelectionTile - 1) / kSelectionTile;
+  return (size_t)2 * kCandidates * (lists + (lists + kListsPerMerge - 1) / kListsPerMerge);
+}
 
 hipError_t launch_topk(hipStream_t s, const float* logits, int count,
                        uint32_t* scratch, uint32_t* candidates) {
-  if (count < kCandidates) return hipErrorInvalidValue;
-  const uint32_t* in = reinterpret_cast<const uint32_t*>(logits);
-  int tiles = (count + kSelectionTile - 1) / kSelectionTile;
-  uint32_t* bufs[2] = {scratch, scratch + 2 * kCandidates * tiles};
-  uint32_t* out = tiles == 1 ? candidates : bufs[0];
-  hipLaunchKernelGGL(topk_kernel<true>, dim3(tiles), dim3(kTopkThreads), 0, s, in, count, out);
-  hipError_t e = hipGetLastError();
-  int pass = 1;
-  while (e == hipSuccess && tiles > 1) {
-    in = out;
-    count = tiles * kCandidates;
-    tiles = (count + kSelectionTile - 1) / kSelectionTile;
-    out = tiles == 1 ? candidates : bufs[pass % 2];
-    hipLaunchKernelGGL(topk_kernel<false>, dim3(tiles), dim3(kTopkThreads), 0, s, in, count,
-                       out);
-    e = hipGetLastError();
-    ++pass;
-  }
-  return e;
+  return select_passes(s, logits, count, scratch, [&](const uint32_t* in, int lists) {
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(64 * kMergeWaves), 0, s, in, lists,
+                       candidates);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_select(hipStream_t s, DevStep* step, const float* logits, int count,
+                         uint32_t* scratch, uint32_t* candidates, uint32_t* sampled,
+                         uint32_t* token_log, bool advance) {
+  return select_passes(s, logits, count, scratch, [&](const uint32_t* in, int lists) {
+    hipLaunchKernelGGL(topk_draw_kernel, dim3(1), dim3(64 * kMergeWaves), 0, s, in, lists,
+                       candidates, step, sampled, token_log, advance ? 1 : 0);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_draw(hipStream_t s, const DevStep* step, const uint32_t* candidates,

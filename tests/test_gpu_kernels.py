@@ -272,11 +272,26 @@ def test_edit_kernel_matches_apply(device):
     assert_same_bits(da.numpy()[:2], act[:2], "before the range")
 
 
-def test_topk_matches_oracle(device):
-    rng = np.random.default_rng(41)
-    logits = rng.normal(0, 3, 262144).astype(np.float32)
-    logits[[5, 70000, 262143]] = logits.max()  # ties: lower token first
-    logits[9] = np.float32(-0.0)
+@pytest.mark.parametrize("count,case", [
+    (262144, "normal"), (64, "normal"), (1000, "ties"), (1025, "specials"),
+    (16385, "normal"), (300000, "specials"), (50000, "ties")])
+def test_topk_matches_oracle(device, count, case):
+    # One tile, a ragged last tile, one merge level and two (300,000 logits
+    # make 293 lists, then 19, then 2); equal keys order by lower token.
+    rng = np.random.default_rng(41 + count)
+    logits = rng.normal(0, 3, count).astype(np.float32)
+    logits[[5 % count, (70000 % count), count - 1]] = logits.max()
+    logits[9 % count] = np.float32(-0.0)
+    if case == "ties":
+        logits = np.round(logits).astype(np.float32)  # a handful of values, many ties
+    if case == "specials":
+        specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, np.float32(3.4e38),
+                             -np.float32(3.4e38), np.float32(1e-45), -np.float32(1e-45)],
+                            dtype=np.float32)
+        where = rng.choice(count, 200, replace=False)
+        logits[where] = specials[rng.integers(0, specials.size, where.size)]
+        logits.view(np.uint32)[where[:5]] = np.array([0x7FC00001, 0xFFC00000, 0x7F800001,
+                                                      0xFF812345, 0x7FFFFFFF], dtype=np.uint32)
     dl = device.array(logits)
     dc = device.empty((128,), np.uint32)
     fz._lib.check(fz.load().frz_op_topk(device.handle, dl.ptr, logits.size, dc.ptr))
