@@ -24,6 +24,30 @@
  * tests; the exact bits of the reference's built-ins on its own GPUs are not
  * defined and stay "parity unpinned".
  *
+ * How each function is pinned (tests/test_oracle.py):
+ *   orc_q4_0_unpack   the reference's fixture valid.gguf; every code x every
+ *                     finite f16 scale against the exact product
+ *   orc_f16_*         all 65,536 halves; saturate + round-to-nearest-even
+ *                     against numpy's IEEE conversion, ties included
+ *   orc_gemv/gated    exact integer results; range boundaries and their order
+ *                     (2^24 + 1 + 1 constructions); fma chaining; the
+ *                     gamma(2K) bound against f64
+ *   orc_norm_row      f64 within 2^-18 (the reference's design margin)
+ *   orc_rope_turns    the f64 closed form, bit for bit
+ *   orc_rope_row      f64 rotation; the cache as numpy's f16 of the clamp
+ *   orc_attention_row f64 softmax attention; keys outside the window inert
+ *   orc_gather_row    the dequantized row times the scale
+ *   orc_edit_row      the edit kernel contract (edit_kernel_test.cpp:1-21)
+ *   orc_topk          brute-force stable sort in the total order
+ *   orc_philox        Random123 known answers; orc_mulhi against 64-bit
+ *   orc_draw          greedy and the uniform's closed form; the inverse
+ *                     transform against f64
+ *   orc_inverse_sqrt  bit for bit against numpy's correctly rounded ops
+ *   orc_dot4          order by a 2^24 + 1 + 1 construction
+ *   orc_exp2, orc_exp_nonpositive, orc_gelu_tanh, orc_cos, orc_sin
+ *                     accuracy against f64 only: their bits, as the
+ *                     reference's built-ins give them, are parity unpinned
+ *
  * Weights are Q4_0 blocks as GGUF stores them: 18 bytes, an fp16 scale d then
  * 16 code bytes; a matrix of N rows of K is N * K / 32 blocks, row-major.
  */
