@@ -8,10 +8,13 @@ seeded random-init Q4_0 weights, after a 4,096-token seeded random prompt
 (prefilled untimed). The timed region replays K captured decode steps.
 
 Also measured, for the JSON line:
-  roofline     the Q4_0 dequant-GEMV of 6,912 x 1,152 (the MLP gate's shape),
-               timed with HIP events on its launching stream over 64 distinct
-               weight copies in turn, so the weights stream from HBM;
-               algorithmic bytes W 4,478,976 + x 4,608 + y 27,648 a launch.
+  roofline     the Q4_0 dequant-GEMV of 6,912 x 1,152 (the MLP gate's shape):
+               64 launches over 64 distinct weight copies captured in a HIP
+               graph and replayed, timed with HIP events on the launching
+               stream, so the weights stream from HBM; algorithmic bytes
+               W 4,478,976 + x 4,608 + y 27,648 a launch. Its HBM traffic a
+               launch comes from the committed rocprofv3 counter summary
+               (profiles/q4_0_gemv_6912x1152_traffic.md), when present.
   cpu_baseline the CPU oracle (the reference's arithmetic restated in C++,
                OpenMP over output rows) decoding the same model on the host,
                a bounded sample of tokens after a 16-token prompt.
@@ -54,7 +57,35 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--eager", action="store_true",
                    help="launch decode kernels one by one instead of replaying a graph")
+    p.add_argument("--roofline-only", action="store_true",
+                   help="only the GEMV roofline and a 256 MiB device copy (for counter runs)")
+    p.add_argument("--gemv-stream", action="store_true",
+                   help="time the GEMV launches on the stream, not replayed from a graph")
     return p.parse_args()
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "q4_0_gemv_6912x1152_traffic.md"
+
+
+def committed_traffic():
+    """HBM bytes a GEMV launch moves, from the committed counter summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def calibration_copy(fz, dev, mib=256):
+    """A plain device copy of known size: the counters' scale."""
+    import ctypes
+    n = mib << 20
+    src, dst = dev.empty((n,), np.uint8), dev.empty((n,), np.uint8)
+    for _ in range(3):
+        fz._lib.check(fz.load().frz_copy(dev.handle, dst.ptr, src.ptr, ctypes.c_uint64(n)))
+    src.free()
+    dst.free()
 
 
 def synth_all(fz, cfg, seed):
@@ -67,7 +98,7 @@ def synth_all(fz, cfg, seed):
     return t
 
 
-def gemv_roofline(fz, dev, copies, iters, seed):
+def gemv_roofline(fz, dev, copies, iters, seed, graph=True):
     import ctypes
     rng = np.random.default_rng(seed + 1)
     blocks = GEMV_ROWS * GEMV_COLS // 32
@@ -82,7 +113,8 @@ def gemv_roofline(fz, dev, copies, iters, seed):
     sp = (ctypes.c_void_p * copies)(*[s.ptr for s in scales])
     us = ctypes.c_double()
     fz._lib.check(fz.load().frz_bench_gemv(dev.handle, cp, sp, copies, GEMV_ROWS, GEMV_COLS,
-                                          x.ptr, y.ptr, iters, ctypes.byref(us)))
+                                          x.ptr, y.ptr, iters, 1 if graph else 0,
+                                          ctypes.byref(us)))
     for a in codes + scales + [x, y]:
         a.free()
     return us.value
@@ -119,6 +151,16 @@ def main():
         sys.exit(2)
     import frizzle_amd as fz
     sys.path.insert(0, str(ROOT / "tests"))
+    if args.roofline_only:
+        dev = fz.Device(0)
+        us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
+                           not args.gemv_stream)
+        calibration_copy(fz, dev)
+        dev.close()
+        achieved = GEMV_BYTES / (us * 1e-6) / 1e9
+        print(json.dumps({"roofline_only": True, "us_per_launch": us, "achieved_gbs": achieved,
+                          "frac": achieved / HBM_PEAK_GBS}))
+        return
 
     context = 8192
     assert args.prompt + args.warmup + args.steps + 1 <= context
@@ -184,7 +226,8 @@ def main():
     log(f"decode {args.steps} steps: {ms_per_step * 1000:.1f} us/step wall, "
         f"{us_events:.1f} us/step events")
 
-    us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed)
+    us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
+                       not args.gemv_stream)
     achieved = GEMV_BYTES / (us * 1e-6) / 1e9
     log(f"gemv 6912x1152: {us:.3f} us/launch, {achieved:.0f} GB/s")
     model.close()
@@ -208,7 +251,8 @@ def main():
                    "prompt_tokens": args.prompt, "decode_tokens": args.steps,
                    "prefill_seconds": prefill_s, "us_per_step_hip_events": us_events},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": committed_traffic(),
                      "kernel": "Q4_0 decode GEMV 6912x1152 (gemv_decode<1>)",
                      "us_per_launch": us, "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,

@@ -65,6 +65,7 @@ _SIGS = {
     "frz_write": (c_int, [_P, _P, _P, c_uint64]),
     "frz_read": (c_int, [_P, _P, _P, c_uint64]),
     "frz_fill_zero": (c_int, [_P, _P, c_uint64]),
+    "frz_copy": (c_int, [_P, _P, _P, c_uint64]),
     "frz_q4_0_split": (c_int, [_P, c_uint64, _P, _P]),
     "frz_op_gemv": (c_int, [_P, _P, _P, c_int, c_int, _P, c_int, _P, c_int,
                             c_uint32, c_int]),
@@ -88,10 +89,10 @@ _SIGS = {
                             _P]),
     "frz_op_numerics": (c_int, [_P, c_int, _P, _P, c_int]),
     "frz_bench_gemv": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p), c_int,
-                               c_int, c_int, _P, _P, c_int, POINTER(c_double)]),
+                               c_int, c_int, _P, _P, c_int, c_int, POINTER(c_double)]),
     "frz_bench_gated": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p),
                                 POINTER(c_void_p), POINTER(c_void_p), c_int,
-                                c_int, c_int, _P, _P, c_int,
+                                c_int, c_int, _P, _P, c_int, c_int,
                                 POINTER(c_double)]),
     "frz_rope_turns": (None, [c_float, c_int, POINTER(c_float)]),
     "frz_edit_check": (c_int, [_P, c_uint32, c_uint32, c_uint32,

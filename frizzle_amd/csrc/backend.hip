@@ -376,66 +376,101 @@ int frz_op_numerics(frz_device* dev, int which, const float* in_dev, float* out_
   return device_finish(dev, hipGetLastError(), "frz_op_numerics");
 }
 
+}  // extern "C"
+
+namespace frz {
+// Times launches replayed from a graph of one launch per weight copy: the
+// captured launches run back to back, so the figure is the kernels' own
+// rate, with the weights streaming from HBM as the copies rotate.
+// Without `graph` the launches go to the stream one by one (for profilers
+// that do not follow graph launches).
+template <typename Launch>
+static int bench_graph(frz_device* dev, int copies, int iters, int graph_mode, Launch launch,
+                       const char* what, double* us_per_launch) {
+  hipStream_t s = dev->stream;
+  for (int i = 0; i < copies; ++i) {  // warm: every copy once
+    if (int rc = check_hip(launch(i), what)) return rc;
+  }
+  if (int rc = check_hip(hipStreamSynchronize(s), what)) return rc;
+  if (!graph_mode) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    int rc = check_hip(hipEventCreate(&start), what);
+    if (rc == FRZ_OK) rc = check_hip(hipEventCreate(&stop), what);
+    if (rc == FRZ_OK) rc = check_hip(hipEventRecord(start, s), what);
+    for (int i = 0; i < iters && rc == FRZ_OK; ++i) rc = check_hip(launch(i % copies), what);
+    if (rc == FRZ_OK) rc = check_hip(hipEventRecord(stop, s), what);
+    if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), what);
+    float ms = 0.0f;
+    if (rc == FRZ_OK) rc = check_hip(hipEventElapsedTime(&ms, start, stop), what);
+    if (start) (void)hipEventDestroy(start);
+    if (stop) (void)hipEventDestroy(stop);
+    *us_per_launch = (double)ms * 1000.0 / iters;
+    return rc;
+  }
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int rc = check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), what);
+  if (rc == FRZ_OK) {
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < copies && e == hipSuccess; ++i) e = launch(i);
+    const hipError_t end = hipStreamEndCapture(s, &graph);
+    rc = check_hip(e != hipSuccess ? e : end, what);
+  }
+  if (rc == FRZ_OK) rc = check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), what);
+  const int replays = (iters + copies - 1) / copies;
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (rc == FRZ_OK) rc = check_hip(hipGraphLaunch(exec, s), what);  // warm the graph
+  if (rc == FRZ_OK) rc = check_hip(hipEventCreate(&start), what);
+  if (rc == FRZ_OK) rc = check_hip(hipEventCreate(&stop), what);
+  if (rc == FRZ_OK) rc = check_hip(hipEventRecord(start, s), what);
+  for (int i = 0; i < replays && rc == FRZ_OK; ++i) rc = check_hip(hipGraphLaunch(exec, s), what);
+  if (rc == FRZ_OK) rc = check_hip(hipEventRecord(stop, s), what);
+  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), what);
+  float ms = 0.0f;
+  if (rc == FRZ_OK) rc = check_hip(hipEventElapsedTime(&ms, start, stop), what);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  *us_per_launch = (double)ms * 1000.0 / ((double)replays * copies);
+  return rc;
+}
+}  // namespace frz
+
+extern "C" {
+
 int frz_bench_gemv(frz_device* dev, const void* const* codes, const void* const* scales,
                    int copies, int rows, int cols, const float* x, float* y, int iters,
-                   double* us_per_launch) {
+                   int graph, double* us_per_launch) {
   if (!shape_ok(rows, cols) || copies <= 0 || iters <= 0 || !us_per_launch) {
     return fail(FRZ_ERR_ARGUMENT, "frz_bench_gemv: bad argument");
   }
   if (int rc = device_put_step(dev, host_step(0, 1))) return rc;
-  hipEvent_t start, stop;
-  (void)hipEventCreate(&start);
-  (void)hipEventCreate(&stop);
-  for (int i = 0; i < copies; ++i) {  // warm: every copy once
-    (void)launch_gemv(dev->stream, dev->step, q4(codes[i], scales[i], rows, cols), x, cols, y, rows, 1,
-                false);
-  }
-  (void)hipEventRecord(start, dev->stream);
-  hipError_t e = hipSuccess;
-  for (int i = 0; i < iters && e == hipSuccess; ++i) {
-    const int c = i % copies;
-    e = launch_gemv(dev->stream, dev->step, q4(codes[c], scales[c], rows, cols), x, cols, y,
-                    rows, 1, false);
-  }
-  (void)hipEventRecord(stop, dev->stream);
-  int rc = check_hip(e, "frz_bench_gemv launch");
-  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), "hipEventSynchronize");
-  float ms = 0.0f;
-  if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, start, stop);
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
-  *us_per_launch = (double)ms * 1000.0 / iters;
-  return rc;
+  return bench_graph(dev, copies, iters, graph, [&](int c) {
+    return launch_gemv(dev->stream, dev->step, q4(codes[c], scales[c], rows, cols), x, cols, y,
+                       rows, 1, false);
+  }, "frz_bench_gemv", us_per_launch);
 }
 
 int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
                     const void* const* gate_scales, const void* const* up_codes,
                     const void* const* up_scales, int copies, int rows, int cols,
-                    const float* x, float* act, int iters, double* us_per_launch) {
+                    const float* x, float* act, int iters, int graph, double* us_per_launch) {
   if (!shape_ok(rows, cols) || copies <= 0 || iters <= 0 || !us_per_launch) {
     return fail(FRZ_ERR_ARGUMENT, "frz_bench_gated: bad argument");
   }
   if (int rc = device_put_step(dev, host_step(0, 1))) return rc;
-  hipEvent_t start, stop;
-  (void)hipEventCreate(&start);
-  (void)hipEventCreate(&stop);
-  auto launch = [&](int c) {
+  return bench_graph(dev, copies, iters, graph, [&](int c) {
     return launch_gated(dev->stream, dev->step, q4(gate_codes[c], gate_scales[c], rows, cols),
                         q4(up_codes[c], up_scales[c], rows, cols), x, act, 1, nullptr, 0);
-  };
-  for (int i = 0; i < copies; ++i) (void)launch(i);
-  (void)hipEventRecord(start, dev->stream);
-  hipError_t e = hipSuccess;
-  for (int i = 0; i < iters && e == hipSuccess; ++i) e = launch(i % copies);
-  (void)hipEventRecord(stop, dev->stream);
-  int rc = check_hip(e, "frz_bench_gated launch");
-  if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(stop), "hipEventSynchronize");
-  float ms = 0.0f;
-  if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, start, stop);
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
-  *us_per_launch = (double)ms * 1000.0 / iters;
-  return rc;
+  }, "frz_bench_gated", us_per_launch);
+}
+
+int frz_copy(frz_device* dev, void* dev_dst, const void* dev_src, uint64_t bytes) {
+  if (!dev || (bytes && (!dev_dst || !dev_src))) return fail(FRZ_ERR_ARGUMENT, "frz_copy: null");
+  return device_finish(
+      dev, hipMemcpyAsync(dev_dst, dev_src, bytes, hipMemcpyDeviceToDevice, dev->stream),
+      "frz_copy");
 }
 
 void frz_rope_turns(float base, int head_dim, float* turns) {

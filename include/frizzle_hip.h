@@ -61,6 +61,8 @@ int frz_free(frz_device* dev, void* dev_ptr);
 int frz_write(frz_device* dev, void* dev_dst, const void* host_src, uint64_t bytes);
 int frz_read(frz_device* dev, void* host_dst, const void* dev_src, uint64_t bytes);
 int frz_fill_zero(frz_device* dev, void* dev_dst, uint64_t bytes);
+/* Device to device; waits for the copy. */
+int frz_copy(frz_device* dev, void* dev_dst, const void* dev_src, uint64_t bytes);
 
 /* The Q4_0 upload transform (replaces residency::PieceWriter,
  * src/core/residency/piece_writer.h:44-60, with the device layout of
@@ -157,18 +159,22 @@ int frz_op_draw(frz_device* dev, const uint32_t* candidates_dev,
 int frz_op_numerics(frz_device* dev, int which, const float* in_dev,
                     float* out_dev, int n);
 
-/* Times `iters` launches of the decode GEMV over `copies` distinct weight
- * copies in turn (so the weights stream from HBM, not a cache), with HIP
- * events on the launching stream; writes the mean microseconds a launch. */
+/* Times the decode GEMV over `copies` distinct weight copies in turn (so
+ * the weights stream from HBM, not a cache): with `graph`, one launch per
+ * copy captured in a HIP graph and replayed until `iters` launches; without,
+ * `iters` launches on the stream. Timed with HIP events on the launching
+ * stream; writes the mean microseconds a launch. No counterpart in the
+ * reference, which times nothing (measurement only). */
 int frz_bench_gemv(frz_device* dev, const void* const* codes,
                    const void* const* scales, int copies, int rows, int cols,
-                   const float* x, float* y, int iters, double* us_per_launch);
+                   const float* x, float* y, int iters, int graph,
+                   double* us_per_launch);
 /* The same for the gated product (gate and up copies in turn). */
 int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
                     const void* const* gate_scales,
                     const void* const* up_codes, const void* const* up_scales,
                     int copies, int rows, int cols, const float* x, float* act,
-                    int iters, double* us_per_launch);
+                    int iters, int graph, double* us_per_launch);
 
 /* Each pair's turns a position for a rotary base (src/core/kernels/rope/
  * rope.cpp:95-106): theta_k / 2 pi in f64, rounded once to f32. */
