@@ -36,7 +36,7 @@ namespace {
 constexpr int kXStride = 36;     // a staged group of x: 32 floats + 4 of padding
 constexpr int kPartStride = 33;  // a row's 32 range sums + 1 of padding
 constexpr int kNormLanes = 256;  // the norm's reduction width
-constexpr int kRedFloats = 260;  // the tree's sums, its total at [256], padding to 16 B
+constexpr int kRedFloats = 512;  // two trees' 256 sums
 constexpr int kNormMaxCols = 2 * 4 * kNormLanes;  // two vec4s a norm lane
 constexpr int kFoldWidth = attn::QH * attn::D;    // the attention output a fold makes
 
@@ -112,13 +112,15 @@ __device__ __forceinline__ int norm_vec4(int k, int m) {
   return (int)threadIdx.x + k * T + m * kNormLanes;
 }
 
-// The norm's halving tree over its 256 lane sums (norm.wgsl:75-85): the
-// levels above T add in registers, the next in LDS, the last six across
-// wave 0. Every thread gets the total.
+// The norm's halving tree over its 256 lane sums (norm.wgsl:75-85). The
+// levels above T add in registers; after one barrier every wave takes the
+// remaining levels itself from LDS (levels 128 and 64 in registers, the last
+// six across the wave), so every thread gets the total with no second
+// barrier. `red` is 256 floats the call owns: a second tree uses another.
 template <int T>
 __device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Shape<T>::kLanesPer]) {
   constexpr int LP = Shape<T>::kLanesPer;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
   float v[LP];
 #pragma unroll
   for (int k = 0; k < LP; ++k) v[k] = lanes[k];
@@ -127,22 +129,17 @@ __device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Sha
 #pragma unroll
     for (int k = 0; k < width / 2; ++k) v[k] = v[k] + v[k + width / 2];
   }
-  float s = v[0];
-  red[t] = s;
+  red[t] = v[0];  // the sum at level T (lane t's for T = 256)
   __syncthreads();
-#pragma unroll
-  for (int stride = T / 2; stride > 64; stride >>= 1) {
-    if (t < stride) red[t] = red[t] + red[t + stride];
-    __syncthreads();
+  float s;
+  if (T == 256) {
+    s = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
+  } else {
+    s = red[lane] + red[lane + 64];
   }
-  if (t < 64) {
-    s = red[t] + red[t + 64];
 #pragma unroll
-    for (int stride = 32; stride > 0; stride >>= 1) s = s + __shfl_down(s, stride, 64);
-    if (t == 0) red[kNormLanes] = s;
-  }
-  __syncthreads();
-  return red[kNormLanes];
+  for (int stride = 32; stride > 0; stride >>= 1) s = s + __shfl_down(s, stride, 64);
+  return __shfl(s, 0, 64);
 }
 
 __device__ __forceinline__ void stage4(float* xs, int q, float4 v) {
@@ -297,7 +294,7 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
         if (norm_vec4<T>(k, m) < vec4s) lanes[k] = lanes[k] + squares4(P.y[2 * k + m]);
       }
     }
-    const float ry = inverse_sqrt(tree_total<T>(red, lanes) / n + in.epsilon);
+    const float ry = inverse_sqrt(tree_total<T>(red + kNormLanes, lanes) / n + in.epsilon);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       if (norm_vec4<T>(s >> 1, s & 1) < vec4s) {
@@ -655,7 +652,8 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
     case 2: return dispatch_write<2>(s, step, w, in, y);
     case 3:
       if (w.cols != kFoldWidth || max_items(w.cols, 1) != 1) return hipErrorInvalidValue;
-      return launch_write<1, 1, 3, 1, 2>(s, step, w, in, y);
+      // Four waves: half as many workgroups folding the chunk states.
+      return launch_write<1, 1, 3, 1, 4>(s, step, w, in, y);
     default: return hipErrorInvalidValue;
   }
 }
