@@ -197,12 +197,12 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
       cm = next;
     }
   }
-  if (u == 0) {
-    S.e[jj] = live ? exp2f_fixed(s - my_top) : 0.0f;
-    if ((jj & 7) == 0 && tile < r.n_tiles) {
-      S.tile_a[tile] =
-          (S.tile_seen[tile] != 0 && my_old != my_top) ? exp2f_fixed(my_old - my_top) : 1.0f;
-    }
+  // The weight by lane 0 of the key, the tile's factor by lane 1 of its
+  // first key: the two exponentials run side by side.
+  if (u == 0) S.e[jj] = live ? exp2f_fixed(s - my_top) : 0.0f;
+  if (u == 1 && (jj & 7) == 0 && tile < r.n_tiles) {
+    S.tile_a[tile] =
+        (S.tile_seen[tile] != 0 && my_old != my_top) ? exp2f_fixed(my_old - my_top) : 1.0f;
   }
   __syncthreads();
   // Each tile's weights summed in order, then l = l a + sum over the seen
