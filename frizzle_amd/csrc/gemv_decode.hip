@@ -98,18 +98,27 @@ __device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits,
 }
 
 // ---- the input row ------------------------------------------------------------
-// T threads (128 or 256): norm lane t + k T (k < 256 / T) belongs to thread t
-// and holds vec4s lane and lane + 256, in slot 2 k + m.
+// T threads (128, 256 or 512). With N = min(T, 256) norm threads, norm lane
+// t + k N (k < 256 / N) belongs to thread t mod N and holds vec4s lane and
+// lane + 256, in slot 2 k + m. Past 256 threads, a thread repeats thread
+// t - 256's loads (so every load stays unconditional) and stages nothing.
 template <int T>
 struct Shape {
-  static_assert(T == 128 || T == 256, "workgroups of two or four waves");
-  static constexpr int kLanesPer = kNormLanes / T;
-  static constexpr int kFoldVec4s = kFoldWidth / 4 / T;
+  static_assert(T == 128 || T == 256 || T == 512, "workgroups of two, four or eight waves");
+  static constexpr int kNormThreads = T < kNormLanes ? T : kNormLanes;
+  static constexpr int kLanesPer = kNormLanes / kNormThreads;
+  static constexpr int kFoldVec4s = T <= kNormLanes ? kFoldWidth / 4 / T : 1;
 };
 
 template <int T>
 __device__ __forceinline__ int norm_vec4(int k, int m) {
-  return (int)threadIdx.x + k * T + m * kNormLanes;
+  constexpr int N = Shape<T>::kNormThreads;
+  return ((int)threadIdx.x & (N - 1)) + k * N + m * kNormLanes;
+}
+
+template <int T>
+__device__ __forceinline__ bool norm_thread() {
+  return (int)threadIdx.x < Shape<T>::kNormThreads;
 }
 
 // The norm's halving tree over its 256 lane sums (norm.wgsl:75-85). The
@@ -117,6 +126,25 @@ __device__ __forceinline__ int norm_vec4(int k, int m) {
 // remaining levels itself from LDS (levels 128 and 64 in registers, the last
 // six across the wave), so every thread gets the total with no second
 // barrier. `red` is 256 floats the call owns: a second tree uses another.
+// Lane l + N of the lane's 16-lane row (DPP row shift; out of the row: 0).
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x100 + N, 0xF, 0xF, true));
+}
+
+// The halving tree's last six levels over a wave's 64 sums: lane l adds
+// lane l + stride for strides 32 .. 1; lane 0's total, broadcast.
+__device__ __forceinline__ float wave_tree(float s) {
+  s = s + __shfl_down(s, 32, 64);
+  s = s + __shfl_down(s, 16, 64);
+  s = s + row_shl<8>(s);
+  s = s + row_shl<4>(s);
+  s = s + row_shl<2>(s);
+  s = s + row_shl<1>(s);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
+}
+
 template <int T>
 __device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Shape<T>::kLanesPer]) {
   constexpr int LP = Shape<T>::kLanesPer;
@@ -129,17 +157,15 @@ __device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Sha
 #pragma unroll
     for (int k = 0; k < width / 2; ++k) v[k] = v[k] + v[k + width / 2];
   }
-  red[t] = v[0];  // the sum at level T (lane t's for T = 256)
+  if (norm_thread<T>()) red[t] = v[0];  // the sum at level min(T, 256)
   __syncthreads();
   float s;
-  if (T == 256) {
+  if (T >= 256) {
     s = (red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]);
   } else {
     s = red[lane] + red[lane + 64];
   }
-#pragma unroll
-  for (int stride = 32; stride > 0; stride >>= 1) s = s + __shfl_down(s, stride, 64);
-  return __shfl(s, 0, 64);
+  return wave_tree(s);
 }
 
 __device__ __forceinline__ void stage4(float* xs, int q, float4 v) {
@@ -219,6 +245,7 @@ __device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prolo
                                               int count) {
   constexpr int QH = attn::QH;
   static_assert(6 * kFoldPrologueChunks * QH <= kRedFloats, "fold tables exceed the tree's LDS");
+  static_assert(T <= kNormLanes, "the fold takes up to four waves");
   float4* st = reinterpret_cast<float4*>(red);  // [count][QH]
   float* fa = red + 4 * kFoldPrologueChunks * QH;
   float* fb = fa + kFoldPrologueChunks * QH;
@@ -278,7 +305,7 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
     }
     return;
   }
-  if (MODE == 3) {
+  if constexpr (MODE == 3) {
     fold_prologue<T, X4>(xs, red, P, window_chunks(step, in.window));
     return;
   }
@@ -324,7 +351,7 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
       }
     }
   }
-  if (blockIdx.x == 0 && in.hidden_out) {
+  if (blockIdx.x == 0 && in.hidden_out && norm_thread<T>()) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int q = norm_vec4<T>(s >> 1, s & 1);
@@ -343,7 +370,7 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const int q = norm_vec4<T>(s >> 1, s & 1);
-    if (q < vec4s) {
+    if (q < vec4s && norm_thread<T>()) {
       const float4 x = P.v[s], g = P.g[s];
       stage4(xs, q, make_float4((x.x * r) * g.x, (x.y * r) * g.y, (x.z * r) * g.z,
                                 (x.w * r) * g.w));
@@ -466,10 +493,10 @@ __device__ __forceinline__ float row_total(const float* parts) {
 // A layer's pins on neuron n at `position` (edit.wgsl:55-76): the layer's
 // edits are sorted by neuron then first position (edit.cpp:20-31), so a
 // binary search finds the neuron's; its ranges never overlap.
-__device__ __forceinline__ float apply_pins(const uint32_t* __restrict__ t, int layer,
-                                            uint32_t n, uint32_t position, float value) {
-  const uint32_t first = t[2 * layer];
-  const uint32_t count = t[2 * layer + 1];
+// `first` and `count` are the layer's [first, count] words, read ahead.
+__device__ __forceinline__ float apply_pins(const uint32_t* __restrict__ t, uint32_t first,
+                                            uint32_t count, uint32_t n, uint32_t position,
+                                            float value) {
   uint32_t lo = 0, hi = count;
   while (lo < hi) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -560,6 +587,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   const int r = lane & 31;
   const int local = wave * 2 + (lane >> 5);
   const int n = blockIdx.x * kNeurons + local;
+  // The layer's pin words are read first, off the end's critical path.
+  uint32_t pin_first = 0, pin_count = 0;
+  if (edits) {
+    pin_first = edits[2 * layer];
+    pin_count = edits[2 * layer + 1];
+  }
   LanePlan<2, MAXI> plan;
   lane_plan<2, MAXI>(plan, gate.cols >> 5, 2 * local, r);
   Prologue<T, X4> pro;
@@ -570,11 +603,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   __syncthreads();
   lane_chains<2, MAXI>(W, plan, xs, parts);
   wave_sync();
+  // Lane 0 totals the gate row while lane 1 totals the up row.
+  const float total = r < 2 ? row_total(parts + (2 * local + r) * kPartStride) : 0.0f;
+  const float u = __shfl_down(total, 1, 64);
   if (r == 0 && n < gate.rows) {
-    const float g = row_total(parts + (2 * local) * kPartStride);
-    const float u = row_total(parts + (2 * local + 1) * kPartStride);
-    float v = gelu_tanh(g) * u;
-    if (edits) v = apply_pins(edits, layer, (uint32_t)n, step->position, v);
+    float v = gelu_tanh(total) * u;
+    if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)n, step->position, v);
     act[n] = v;
   }
 }
@@ -627,7 +661,7 @@ template <int MAXI, int MODE>
 hipError_t launch_gated(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
                         const Q4Matrix& up, const GemvInput& in, float* act,
                         const uint32_t* edits, int layer) {
-  // Four waves: half as many workgroups making the input row.
+  // Four waves: half as many workgroups making the input row as with two.
   constexpr int kWaves = 4, kNeurons = 2 * kWaves;
   const size_t lds =
       (size_t)(2 * kNeurons * kPartStride + kRedFloats + (gate.cols / 32) * kXStride) * 4;
