@@ -98,13 +98,12 @@ __device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits,
 }
 
 // ---- the input row ------------------------------------------------------------
-// T threads (128, 256 or 512). With N = min(T, 256) norm threads, norm lane
-// t + k N (k < 256 / N) belongs to thread t mod N and holds vec4s lane and
-// lane + 256, in slot 2 k + m. Past 256 threads, a thread repeats thread
-// t - 256's loads (so every load stays unconditional) and stages nothing.
+// T threads (128 to 1,024). With N = min(T, 256) norm threads, norm lane
+// t + k N (k < 256 / N) belongs to thread t and holds vec4s lane and
+// lane + 256, in slot 2 k + m. Threads past 256 hold no norm lane.
 template <int T>
 struct Shape {
-  static_assert(T == 128 || T == 256 || T == 512, "workgroups of two, four or eight waves");
+  static_assert(T == 128 || T == 256 || T == 512 || T == 1024, "two to sixteen waves");
   static constexpr int kNormThreads = T < kNormLanes ? T : kNormLanes;
   static constexpr int kLanesPer = kNormLanes / kNormThreads;
   static constexpr int kFoldVec4s = T <= kNormLanes ? kFoldWidth / 4 / T : 1;
@@ -113,7 +112,7 @@ struct Shape {
 template <int T>
 __device__ __forceinline__ int norm_vec4(int k, int m) {
   constexpr int N = Shape<T>::kNormThreads;
-  return ((int)threadIdx.x & (N - 1)) + k * N + m * kNormLanes;
+  return (int)threadIdx.x + k * N + m * kNormLanes;
 }
 
 template <int T>
@@ -211,6 +210,10 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
     }
     return;
   }
+  // Past 256 threads, whole waves hold no norm lane and load nothing: the
+  // loads skipped come before every other load, so no later wait counts
+  // them.
+  if (!norm_thread<T>()) return;
   uint32_t token = 0;
   if (MODE == 2) token = step->fed ? in.sampled[0] : step->ids[0];
   const int groups = width >> 5;
@@ -579,7 +582,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   extern __shared__ __align__(16) float smem[];
   constexpr int T = 64 * WAVES;
   constexpr int kNeurons = 2 * WAVES;
-  constexpr int X4 = kNormMaxCols / 4 / T;
+  constexpr int X4 = (kNormMaxCols / 4 + T - 1) / T;
   float* parts = smem;
   float* red = parts + 2 * kNeurons * kPartStride;
   float* xs = red + kRedFloats;
@@ -657,12 +660,15 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
   return hipErrorInvalidValue;
 }
 
-template <int MAXI, int MODE>
+// Gated workgroups of kGatedWaves waves: the fewer workgroups, the less
+// redundant input-row work and L2 traffic for it.
+constexpr int kGatedWaves = 4;
+
+template <int MAXI, int MODE, int kWaves = kGatedWaves>
 hipError_t launch_gated(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
                         const Q4Matrix& up, const GemvInput& in, float* act,
                         const uint32_t* edits, int layer) {
-  // Four waves: half as many workgroups making the input row as with two.
-  constexpr int kWaves = 4, kNeurons = 2 * kWaves;
+  constexpr int kNeurons = 2 * kWaves;
   const size_t lds =
       (size_t)(2 * kNeurons * kPartStride + kRedFloats + (gate.cols / 32) * kXStride) * 4;
   hipLaunchKernelGGL((gemv_gated_kernel<MAXI, MODE, kWaves>),
