@@ -149,6 +149,12 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
                                             float* __restrict__ stats) {
   const int t = threadIdx.x, jj = t >> 2, u = t & 3, j = r.k_begin + jj;
   const bool live = jj < r.n_tiles * kTileKeys && j < r.k_end && j <= p && j + window > p;
+  // Dimension t of every staged value row, read now so the reads complete
+  // under the scores and the softmax and the output chain finds them in
+  // registers (rows past the chunk's tiles read as staged; their weight is 0).
+  uint16_t vt[kChunkKeys];
+#pragma unroll
+  for (int key = 0; key < kChunkKeys; ++key) vt[key] = S.v[key * D + t];
   // Scores (attention.wgsl:277-297).
   float d[2 * kKeyLoads];
 #pragma unroll
@@ -227,12 +233,15 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   }
   // O = O a + sum_b e_b v_b per tile: thread t is dimension t.
   float o = 0.0f;
-  for (int tt = 0; tt < r.n_tiles; ++tt) {
-    o = o * S.tile_a[tt];
-    const float4 ea = ld4f(S.e + tt * kTileKeys), eb = ld4f(S.e + tt * kTileKeys + 4);
-    const float e[kTileKeys] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
 #pragma unroll
-    for (int b = 0; b < kTileKeys; ++b) o = o + e[b] * h2f(S.v[(tt * kTileKeys + b) * D + t]);
+  for (int tt = 0; tt < kTiles; ++tt) {
+    if (tt < r.n_tiles) {
+      o = o * S.tile_a[tt];
+      const float4 ea = ld4f(S.e + tt * kTileKeys), eb = ld4f(S.e + tt * kTileKeys + 4);
+      const float e[kTileKeys] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+#pragma unroll
+      for (int b = 0; b < kTileKeys; ++b) o = o + e[b] * h2f(vt[tt * kTileKeys + b]);
+    }
   }
   partial[t] = o;
 }
