@@ -10,14 +10,13 @@
 // (q4_0.wgsl:71-83) as fma(code, d, -8 d): code * d and 8 d are exact, and
 // so is their difference, so the fma's one rounding changes nothing.
 
+#include <algorithm>
+
 #include "kernels.h"
 #include "numerics.h"
 
 namespace frz {
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kXStride = 36;  // a staged group of x: 32 floats + 4 of padding
 
 __device__ __forceinline__ float half_to_float(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -50,139 +49,435 @@ __device__ __forceinline__ float apply_edits(const uint32_t* __restrict__ t,
   return value;
 }
 
-// ---- tiled form ----------------------------------------------------------
-// A workgroup computes a tile of 64 rows x 32 tokens. Per group of K: the 64
-// rows' weights are decoded into LDS and the 32 tokens' inputs staged; lane
-// (slot s = t % 64, token octet t / 64) chains its 8 tokens' products for row
-// s. Each range's sums start from zero and are added to the totals at the
-// range's end: the order above (matmul.wgsl:320-405).
-constexpr int kTileRows = 64;
-constexpr int kTileTokens = 32;
-constexpr int kWStride = 33;
+// ---- prefill form: matrix cores ------------------------------------------
+// The fp32 matrix-core instructions with one k per step,
+// v_mfma_f32_32x32x1_2b_f32 and v_mfma_f32_16x16x1_4b_f32, update NB
+// independent blocks of D x D accumulators (NB = 2, D = 32 or NB = 4,
+// D = 16) with one fma per element: C = fma(a_i, b_j, C), one rounding, the
+// fma of the reference's chain. A run of them in k order is that chain.
+//
+// A wave owns a tile of D rows x D tokens and gives each block its own
+// K-range of that same tile: at pass p, block b chains range NB p + b. When
+// the pass's ranges are done, their sums join the totals in range order
+// (matmul.wgsl:320-405), and the blocks start the next NB ranges. Ranges of
+// one pass may differ in length by a group; a block whose range is done
+// meanwhile multiplies zero inputs, which adds a zero to a range sum whose
+// sign can then differ only for a zero sum - and the totals, which start at
+// +0 and so are never -0, are the same either way.
+//
+// Lane l is row l % D and token l % D of block l / D: it decodes its row's
+// weights for its block's group, in-register and exactly, and reads its
+// token's inputs for that group. So every lane does distinct work and a pass
+// keeps NB chains in flight. The inputs of a step (NB groups x D tokens = 64
+// lines of 32 floats) are loaded whole-line into LDS and read back one line
+// per lane. A gated wave holds the gate and up tiles of the same neurons,
+// sharing the inputs.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
-// Row slot s of the tile: for a gated tile, slots 0..31 are gate rows and
-// 32..63 the same up rows.
+constexpr int kTileWaves = 4;  // waves per workgroup; each its own tokens
+
+template <int NB>
+struct Mfma;
+
+// Element (i, j) of block b: lane j + 32 ((i / 4) % 2), register
+// 16 b + 4 (i / 8) + i % 4. Output slot o of lane L (o < 16) is
+// row 8 (o / 4) + 4 ((L / 32) % 2) + o % 4, token L % 32; block b's value
+// is register 16 b + o.
+template <>
+struct Mfma<2> {
+  static constexpr int kDim = 32;
+  static constexpr int kSlots = 16;
+  typedef v32f Acc;
+  __device__ static Acc op(float a, float b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static int slot_row(int lane, int o) {
+    return 8 * (o >> 2) + 4 * ((lane >> 5) & 1) + (o & 3);
+  }
+};
+
+// Element (i, j) of block b: lane j + 16 (i / 4), register i % 4 + 4 b.
+// Output slot o of lane L (o < 4) is row 4 (L / 16) + o, token L % 16;
+// block b's value is register 4 b + o.
+template <>
+struct Mfma<4> {
+  static constexpr int kDim = 16;
+  static constexpr int kSlots = 4;
+  typedef v16f Acc;
+  __device__ static Acc op(float a, float b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+  }
+  __device__ static int slot_row(int lane, int o) { return 4 * (lane >> 4) + o; }
+};
+
+// A group's 32 weights in k order (q4_0.wgsl:71-83). Weight k < 16 is the
+// low nibble of byte k, weight 16 + k its high nibble. A bitfield insert puts
+// a low nibble q under the exponent of 1024 (f16 0x6400) to make 1024 + q,
+// and a high nibble in place to make 1024 + 16 q; then
+//   fma(1024 + q, d, -1032 d) = (q - 8) d  and
+//   fma(1024 + 16 q, d / 16, -72 d) = (q - 8) d,
+// both exact: every operand and the result fit in 24 bits.
+__device__ __forceinline__ void decode_group(uint4 c, uint16_t dbits, float (&wk)[32]) {
+  const float d = half_to_float(dbits);
+  const float lo_bias = -1032.0f * d;
+  const float d16 = 0.0625f * d;
+  const float hi_bias = -72.0f * d;
+  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+  // The exponent comes from a register the compiler cannot see into, so that
+  // (s & mask) | (exp & ~mask) stays one bitfield insert.
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+  constexpr uint32_t kLo = 0x000F000Fu, kHi = 0x00F000F0u;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t s = words[w], t = words[w] >> 8;
+    // even: bytes 0 and 2 of the word; odd: bytes 1 and 3.
+    const half2v le = __builtin_bit_cast(half2v, (s & kLo) | (kExp & ~kLo));
+    const half2v lo = __builtin_bit_cast(half2v, (t & kLo) | (kExp & ~kLo));
+    const half2v he = __builtin_bit_cast(half2v, (s & kHi) | (kExp & ~kHi));
+    const half2v ho = __builtin_bit_cast(half2v, (t & kHi) | (kExp & ~kHi));
+    wk[4 * w + 0] = __builtin_fmaf((float)le.x, d, lo_bias);
+    wk[4 * w + 1] = __builtin_fmaf((float)lo.x, d, lo_bias);
+    wk[4 * w + 2] = __builtin_fmaf((float)le.y, d, lo_bias);
+    wk[4 * w + 3] = __builtin_fmaf((float)lo.y, d, lo_bias);
+    wk[16 + 4 * w + 0] = __builtin_fmaf((float)he.x, d16, hi_bias);
+    wk[16 + 4 * w + 1] = __builtin_fmaf((float)ho.x, d16, hi_bias);
+    wk[16 + 4 * w + 2] = __builtin_fmaf((float)he.y, d16, hi_bias);
+    wk[16 + 4 * w + 3] = __builtin_fmaf((float)ho.y, d16, hi_bias);
+  }
+}
+
+// Orders a wave's LDS accesses around it (a wave's LDS instructions execute
+// in program order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The order of a wave's steps, the same for every tile of a product: at step
+// t, block b reads group g (16 bits: g, and bit 15 when b's range is
+// already done and its inputs are zeros). Step flags: kOpens (first step of
+// a pass: the blocks start from zero), kCloses (last step: the pass's sums
+// join the totals), kPads (some block's inputs are zeros). Built on the host.
+constexpr int kMaxSteps = 256;
+constexpr uint32_t kOpens = 1, kCloses = 2, kPads = 4;
+
+template <int NB>
+struct Schedule {
+  static constexpr int kWords = NB / 2;  // two blocks per word
+  int steps;
+  uint32_t flags[kMaxSteps / 8];  // 4 bits per step
+  uint32_t word[kMaxSteps * kWords];
+};
+
+// One step's schedule words, read ahead into scalar registers.
+template <int NB>
+struct StepInfo {
+  uint32_t word[Schedule<NB>::kWords];
+  uint32_t flags;
+  __device__ uint32_t entry(int b) const { return (word[b / 2] >> (16 * (b & 1))) & 0xFFFFu; }
+};
+
+template <int NB>
+__device__ __forceinline__ StepInfo<NB> step_info(const Schedule<NB>& S, int t) {
+  t = min(t, S.steps - 1);
+  StepInfo<NB> I;
+#pragma unroll
+  for (int i = 0; i < Schedule<NB>::kWords; ++i) I.word[i] = S.word[t * Schedule<NB>::kWords + i];
+  I.flags = (S.flags[t >> 3] >> (4 * (t & 7))) & 0xFu;
+  return I;
+}
+
+// Loads through a buffer resource over [base, base + bytes), with the
+// per-lane part of the offset in a VGPR and the uniform part in an SGPR, so
+// that no per-lane address arithmetic is needed; loads past the end read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// A step's inputs pass through LDS: 64 lines (line L = block L / D,
+// token L % D) of 32 floats, stored 9 float4s apart so that the lanes' line
+// reads fall in distinct banks. Lane l loads float4 l % 8 of lines 8 i + l / 8.
+constexpr int kXLine = 9;
+constexpr int kXBuf = 64 * kXLine;
+
+template <int NB, bool GATED>
+struct Tile {
+  static constexpr int D = Mfma<NB>::kDim;
+  static constexpr int kTokenRows = 8 / NB;  // distinct tokens a lane loads
+  static constexpr int kMats = GATED ? 2 : 1;
+  __amdgpu_buffer_rsrc_t x, codes[kMats], scales[kMats];
+  uint32_t x_off[kTokenRows];  // byte offset of float4 lane % 8 of each token it loads
+  uint32_t row_group0;         // this lane's row times the row's groups
+  float4* x_put[2];            // its load slots, per buffer (+ 8 kXLine i)
+  const float4* x_get[2];      // its own line, per buffer
+  int block;                   // lane / D
+};
+
+// Step t's inputs: instruction i is lines 8 i .. 8 i + 7, block
+// i / (8 / NB). A finished block's lines are loaded (from a valid group)
+// and zeroed when staged.
+template <int NB, bool GATED>
+__device__ __forceinline__ void load_inputs(const Tile<NB, GATED>& T, const StepInfo<NB>& I,
+                                            float4 (&G)[8]) {
+  constexpr int kPer = Tile<NB, GATED>::kTokenRows;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t g = I.entry(i / kPer) & 0x7FFFu;
+    G[i] = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(T.x, T.x_off[i % kPer], 128 * g, 0));
+  }
+}
+
+template <int NB, bool GATED>
+__device__ __forceinline__ void stage_inputs(const Tile<NB, GATED>& T, const StepInfo<NB>& I,
+                                             int buf, float4 (&G)[8]) {
+  constexpr int kPer = Tile<NB, GATED>::kTokenRows;
+  if (I.flags & kPads) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (I.entry(i / kPer) & 0x8000u) G[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) T.x_put[buf][8 * kXLine * i] = G[i];
+}
+
 template <bool GATED>
-__global__ __launch_bounds__(kThreads) void gemm_tiled(
-    const DevStep* __restrict__ step, Q4Matrix w, Q4Matrix up,
-    const float* __restrict__ x, int x_stride, float* __restrict__ y,
-    int y_stride, const uint32_t* __restrict__ edits, int layer) {
-  __shared__ float ws[kTileRows * kWStride];
-  __shared__ float xs[32 * kTileTokens];
-  const int tokens = (int)step->tokens;
-  const int token0 = blockIdx.y * kTileTokens;
-  if (token0 >= tokens) return;
-  const int groups = w.cols >> 5;
-  const int t = threadIdx.x;
-  const int slot = t & 63, octet = t >> 6;
-  // Staging roles: thread t decodes word t % 4 of row t / 4's block.
-  const int srow = t >> 2, sword = t & 3;
-  int stage_row;
-  const uint8_t* src_codes = w.codes;
-  const uint16_t* src_scales = w.scales;
-  if (GATED) {
-    const int n = blockIdx.x * 32 + (srow & 31);
-    if (srow >= 32) {
-      src_codes = up.codes;
-      src_scales = up.scales;
-    }
-    stage_row = n < w.rows ? n : -1;
-  } else {
-    const int n = blockIdx.x * kTileRows + srow;
-    stage_row = n < w.rows ? n : -1;
-  }
-  // x staging: thread t loads floats 4 (t % 8) .. +3 of token t / 8.
-  const int xtok = t >> 3, xpart = t & 7;
-  const bool xlive = token0 + xtok < tokens;
-  const float* xrow = x + (size_t)(token0 + xtok) * x_stride;
+struct Weights {
+  uint4 c[GATED ? 2 : 1];
+  uint16_t d[GATED ? 2 : 1];
+};
 
-  float s[8], total[8];
+template <int NB, bool GATED>
+__device__ __forceinline__ void load_weights(const Tile<NB, GATED>& T, const StepInfo<NB>& I,
+                                             Weights<GATED>& W) {
+  // this lane's block's group
+  uint32_t g = I.entry(0);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) total[i] = 0.0f;
-  for (int r = 0; r < kRanges; ++r) {
+  for (int b = 1; b < NB; ++b) g = T.block == b ? I.entry(b) : g;
+  const uint32_t blk = T.row_group0 + (g & 0x7FFFu);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = 0.0f;
-    const int lo = r * groups / kRanges, hi = (r + 1) * groups / kRanges;
-    for (int g = lo; g < hi; ++g) {
-      __syncthreads();
-      {
-        float wv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (stage_row >= 0) {
-          const size_t blk = (size_t)stage_row * groups + g;
-          const uint32_t word =
-              reinterpret_cast<const uint32_t*>(src_codes)[blk * 4 + sword];
-          const float d = half_to_float(src_scales[blk]);
-          const float m8d = -8.0f * d;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            wv[b] = fmaf_((float)((word >> (8 * b)) & 0xFu), d, m8d);
-            wv[4 + b] = fmaf_((float)((word >> (8 * b + 4)) & 0xFu), d, m8d);
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          ws[srow * kWStride + 4 * sword + b] = wv[b];
-          ws[srow * kWStride + 16 + 4 * sword + b] = wv[4 + b];
-        }
-        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (xlive) xv = *reinterpret_cast<const float4*>(xrow + g * 32 + 4 * xpart);
-        xs[(4 * xpart + 0) * kTileTokens + xtok] = xv.x;
-        xs[(4 * xpart + 1) * kTileTokens + xtok] = xv.y;
-        xs[(4 * xpart + 2) * kTileTokens + xtok] = xv.z;
-        xs[(4 * xpart + 3) * kTileTokens + xtok] = xv.w;
-      }
-      __syncthreads();
-#pragma unroll 8
-      for (int k = 0; k < 32; ++k) {
-        const float wk = ws[slot * kWStride + k];
-        const float4 x0 = *reinterpret_cast<const float4*>(&xs[k * kTileTokens + octet * 8]);
-        const float4 x1 = *reinterpret_cast<const float4*>(&xs[k * kTileTokens + octet * 8 + 4]);
-        s[0] = fmaf_(wk, x0.x, s[0]);
-        s[1] = fmaf_(wk, x0.y, s[1]);
-        s[2] = fmaf_(wk, x0.z, s[2]);
-        s[3] = fmaf_(wk, x0.w, s[3]);
-        s[4] = fmaf_(wk, x1.x, s[4]);
-        s[5] = fmaf_(wk, x1.y, s[5]);
-        s[6] = fmaf_(wk, x1.z, s[6]);
-        s[7] = fmaf_(wk, x1.w, s[7]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) total[i] = total[i] + s[i];
+  for (int m = 0; m < Tile<NB, GATED>::kMats; ++m) {
+    W.c[m] = __builtin_bit_cast(uint4,
+                                __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 16 * blk, 0, 0));
+    W.d[m] = __builtin_amdgcn_raw_buffer_load_b16(T.scales[m], 2 * blk, 0, 0);
   }
-  if (!GATED) {
-    const int row = blockIdx.x * kTileRows + slot;
-    if (row < w.rows) {
+}
+
+// One step t: stage step t + 1's inputs (loaded a step ago), start the loads
+// of step t + 2's inputs and t + 1's weights, then per matrix decode this
+// step's weights and chain its 32 products per block from buffer B (from
+// zero if the step opens a pass). Vector instructions do not run beside the
+// fp32 matrix instructions, so each kind is kept in one run.
+template <int NB, bool GATED, int B, bool OPENS>
+__device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepInfo<NB>& I1,
+                                           const StepInfo<NB>& I2, float4 (&G)[8],
+                                           const Weights<GATED>& W, Weights<GATED>& W_next,
+                                           typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
+  constexpr int kMats = Tile<NB, GATED>::kMats;
+  stage_inputs(T, I1, B ^ 1, G);
+  load_inputs(T, I2, G);
+  load_weights(T, I1, W_next);
+  // The loads stay here, a step ahead of their use.
+  __builtin_amdgcn_sched_barrier(0);
+  float4 xv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int tok = token0 + octet * 8 + i;
-        if (tok < tokens) y[(size_t)tok * y_stride + row] = total[i];
+  for (int i = 0; i < 8; ++i) xv[i] = T.x_get[B][i];
+  const typename Mfma<NB>::Acc zero = {};
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+    float wk[32];
+    decode_group(W.c[m], W.d[m], wk);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float xk = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
+        acc[m] = Mfma<NB>::op(wk[4 * i + j], xk, (OPENS && i == 0 && j == 0) ? zero : acc[m]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wave_sync();
+}
+
+// A pass's range sums join the totals in range order.
+template <int NB>
+__device__ __forceinline__ void close_pass(const typename Mfma<NB>::Acc& acc,
+                                           float (&total)[Mfma<NB>::kSlots]) {
+  constexpr int S = Mfma<NB>::kSlots;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int o = 0; o < S; ++o) total[o] = total[o] + acc[S * b + o];
+  }
+}
+
+// Step t, with the schedule of steps t .. t + 2 in hand; starts reading
+// step t + 3's (first used a step later, so its wait costs nothing).
+template <int NB, bool GATED, int B>
+__device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedule<NB>& S, int t,
+                                         StepInfo<NB> (&I)[4], float4 (&G)[8],
+                                         const Weights<GATED>& W, Weights<GATED>& W_next,
+                                         typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
+                                         float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
+  I[3] = step_info(S, t + 3);
+  if (I[0].flags & kOpens) {
+    chain_step<NB, GATED, B, true>(T, I[1], I[2], G, W, W_next, acc);
   } else {
-    // Gate totals meet their up totals in LDS (reusing the weight tile).
-    __syncthreads();
-    float* meet = ws;  // [32 neurons][32 tokens + 1]
-    if (slot >= 32) {
+    chain_step<NB, GATED, B, false>(T, I[1], I[2], G, W, W_next, acc);
+  }
+  if (I[0].flags & kCloses) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) meet[(slot - 32) * 33 + octet * 8 + i] = total[i];
-    }
-    __syncthreads();
-    if (slot < 32) {
-      const int n = blockIdx.x * 32 + slot;
-      if (n < w.rows) {
+    for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
+  }
+  I[0] = I[1];
+  I[1] = I[2];
+  I[2] = I[3];
+}
+
+// Grid: x = D-row tiles, y = groups of kTileWaves x D tokens. Rows and
+// tokens past the ends are read clamped and not stored.
+template <int NB, bool GATED>
+__global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
+    const DevStep* __restrict__ step, Q4Matrix w, Q4Matrix up,
+    const float* __restrict__ x, int x_stride, uint32_t x_bytes, float* __restrict__ y,
+    int y_stride, const uint32_t* __restrict__ edits, int layer, const Schedule<NB> S) {
+  using M = Mfma<NB>;
+  constexpr int D = M::kDim;
+  constexpr int SL = M::kSlots;
+  constexpr int kMats = GATED ? 2 : 1;
+  __shared__ float4 staged[kTileWaves][2][kXBuf];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tokens = (int)step->tokens;
+  const int token0 = (blockIdx.y * kTileWaves + wave) * D;
+  if (token0 >= tokens) return;  // whole waves; the kernel has no barriers
+  const int groups = w.cols >> 5;
+
+  Tile<NB, GATED> T;
+  T.block = lane / D;
+  const int row = min((int)blockIdx.x * D + lane % D, w.rows - 1);
+  const uint32_t blocks = (uint32_t)w.rows * (uint32_t)groups;
+  T.row_group0 = (uint32_t)row * (uint32_t)groups;
+  T.codes[0] = buffer_of(w.codes, 16 * blocks);
+  T.scales[0] = buffer_of(w.scales, 2 * blocks);
+  if (GATED) {
+    T.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
+    T.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
+  }
+  T.x = buffer_of(x, x_bytes);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int tok = token0 + octet * 8 + i;
-          if (tok < tokens) {
-            float v = gelu_tanh(total[i]) * meet[slot * 33 + octet * 8 + i];
-            if (edits) v = apply_edits(edits, layer, (uint32_t)n, step->position + tok, v);
-            y[(size_t)tok * y_stride + n] = v;
-          }
-        }
-      }
+  for (int i = 0; i < Tile<NB, GATED>::kTokenRows; ++i) {
+    // line 8 i + lane / 8 is token (8 i + lane / 8) % D
+    const int tok = min(token0 + (8 * i + (lane >> 3)) % D, tokens - 1);
+    T.x_off[i] = 4u * ((uint32_t)tok * (uint32_t)x_stride + 4u * (uint32_t)(lane & 7));
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    T.x_put[b] = staged[wave][b] + (lane >> 3) * kXLine + (lane & 7);
+    T.x_get[b] = staged[wave][b] + lane * kXLine;
+  }
+
+  typename M::Acc acc[kMats];
+  float total[kMats][SL];
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int o = 0; o < SL; ++o) total[m][o] = 0.0f;
+  }
+
+  // Step 0 staged; step 1's inputs and step 0's weights in registers.
+  StepInfo<NB> I[4];
+  I[0] = step_info(S, 0);
+  I[1] = step_info(S, 1);
+  I[2] = step_info(S, 2);
+  float4 G[8];
+  load_inputs(T, I[0], G);
+  stage_inputs(T, I[0], 0, G);
+  load_inputs(T, I[1], G);
+  Weights<GATED> W0, W1;
+  load_weights(T, I[0], W0);
+  wave_sync();
+  for (int t = 0; t < S.steps; t += 2) {
+    run_step<NB, GATED, 0>(T, S, t, I, G, W0, W1, acc, total);
+    if (t + 1 >= S.steps) break;
+    run_step<NB, GATED, 1>(T, S, t + 1, I, G, W1, W0, acc, total);
+  }
+
+  const int tok = token0 + lane % D;
+  if (tok >= tokens) return;
+  float* yrow = y + (size_t)tok * y_stride;
+  const int row0 = blockIdx.x * D;
+  const uint32_t position = step->position + (uint32_t)tok;
+#pragma unroll
+  for (int o = 0; o < SL; ++o) {
+    const int n = row0 + M::slot_row(lane, o);
+    if (n >= w.rows) continue;
+    if (!GATED) {
+      yrow[n] = total[0][o];
+    } else {
+      float v = gelu_tanh(total[0][o]) * total[kMats - 1][o];
+      if (edits) v = apply_edits(edits, layer, (uint32_t)n, position, v);
+      yrow[n] = v;
     }
   }
+}
+
+// Pass p holds ranges NB p .. NB p + NB - 1 and runs for its longest range;
+// passes of empty ranges are left out (their sums add zero). False when the
+// product has more steps than a schedule holds.
+template <int NB>
+bool build_schedule(int groups, Schedule<NB>& S) {
+  S = Schedule<NB>{};
+  int t = 0;
+  for (int p = 0; p < kRanges / NB; ++p) {
+    int lo[NB], len[NB], steps = 0;
+    for (int b = 0; b < NB; ++b) {
+      const int r = NB * p + b;
+      lo[b] = r * groups / kRanges;
+      len[b] = (r + 1) * groups / kRanges - lo[b];
+      steps = std::max(steps, len[b]);
+    }
+    for (int s = 0; s < steps; ++s, ++t) {
+      if (t >= kMaxSteps) return false;
+      uint32_t f = (s == 0 ? kOpens : 0u) | (s + 1 == steps ? kCloses : 0u);
+      for (int b = 0; b < NB; ++b) {
+        const bool done = s >= len[b];
+        const uint32_t g = (uint32_t)std::min(lo[b] + s, groups - 1);
+        const uint32_t e = g | (done ? 0x8000u : 0u);
+        S.word[t * Schedule<NB>::kWords + b / 2] |= e << (16 * (b & 1));
+        if (done) f |= kPads;
+      }
+      S.flags[t >> 3] |= f << (4 * (t & 7));
+    }
+  }
+  S.steps = t;
+  return t > 0;
+}
+
+template <int NB, bool GATED>
+hipError_t launch_ranges(hipStream_t s, const DevStep* step, Q4Matrix w, Q4Matrix up,
+                         const float* x, int x_stride, float* y, int y_stride, int max_tokens,
+                         const uint32_t* edits, int layer) {
+  constexpr int D = Mfma<NB>::kDim;
+  const int groups = w.cols >> 5;
+  const uint64_t x_bytes = 4ull * (uint64_t)x_stride * (uint64_t)max_tokens;
+  const uint64_t code_bytes = 16ull * (uint64_t)w.rows * (uint64_t)groups;
+  Schedule<NB> S;
+  if (groups >= 0x8000 || x_bytes >= (1ull << 31) || code_bytes >= (1ull << 31) ||
+      !build_schedule<NB>(groups, S)) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid((w.rows + D - 1) / D, (max_tokens + kTileWaves * D - 1) / (kTileWaves * D));
+  hipLaunchKernelGGL((gemm_ranges<NB, GATED>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
+                     x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, S);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -196,11 +491,13 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
     in.x = x + (size_t)(last_token ? max_tokens - 1 : 0) * x_stride;
     return launch_gemv_decode(s, step, w, in, 0, y);
   }
-  const dim3 grid((w.rows + kTileRows - 1) / kTileRows,
-                  (max_tokens + kTileTokens - 1) / kTileTokens);
-  hipLaunchKernelGGL(gemm_tiled<false>, grid, dim3(kThreads), 0, s, step, w, w, x,
-                     x_stride, y, y_stride, (const uint32_t*)nullptr, 0);
-  return hipGetLastError();
+  // Tiles of 32 x 32 (two ranges in flight) when they are enough to cover
+  // most of the chip's 1,024 SIMDs; else 16 x 16 tiles (four ranges), four
+  // times as many.
+  if ((size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024) {
+    return launch_ranges<2, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens, nullptr, 0);
+  }
+  return launch_ranges<4, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens, nullptr, 0);
 }
 
 hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
@@ -213,10 +510,8 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
     in.x = x;
     return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
   }
-  const dim3 grid((gate.rows + 31) / 32, (max_tokens + kTileTokens - 1) / kTileTokens);
-  hipLaunchKernelGGL(gemm_tiled<true>, grid, dim3(kThreads), 0, s, step, gate, up, x,
-                     gate.cols, act, gate.rows, edits, layer);
-  return hipGetLastError();
+  return launch_ranges<2, true>(s, step, gate, up, x, gate.cols, act, gate.rows, max_tokens, edits,
+                               layer);
 }
 
 }  // namespace frz

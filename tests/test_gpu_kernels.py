@@ -105,6 +105,24 @@ def test_gemv_tiled_is_decode_bits(device, rows, cols, tokens):
         assert_same_bits(got[t], orc.gemv(w, rows, cols, x[t]), f"token {t}")
 
 
+def test_gemv_tiled_subnormal_products(device):
+    # Products and sums below f32's normal range: the prefill's chains keep
+    # subnormals exactly as the reference's fma does.
+    rng = np.random.default_rng(5)
+    rows, cols, tokens = 80, 128, 17
+    w = q4_blocks(rng, rows, cols)
+    x = (rng.normal(0, 1, (tokens, cols)) * 1e-37).astype(np.float32)
+    codes, scales = _q4_dev(device, w)
+    dx = device.array(x)
+    dy = device.empty((tokens, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gemv(device.handle, codes.ptr, scales.ptr, rows, cols,
+                                        dx.ptr, cols, dy.ptr, rows, tokens, 0))
+    got = dy.numpy()
+    assert np.count_nonzero((got != 0) & (np.abs(got) < np.float32(1.1754944e-38))) > 0
+    for t in range(tokens):
+        assert_same_bits(got[t], orc.gemv(w, rows, cols, x[t]), f"token {t}")
+
+
 def test_gemv_last_token(device):
     rng = np.random.default_rng(9)
     rows, cols, tokens = 40000, 1152, 7
@@ -118,7 +136,7 @@ def test_gemv_last_token(device):
     assert_same_bits(dy.numpy(), orc.gemv(w, rows, cols, x[-1]), "head")
 
 
-@pytest.mark.parametrize("tokens", [1, 6])
+@pytest.mark.parametrize("tokens", [1, 6, 37])
 def test_gated_with_pins_bit_exact(device, tokens):
     rng = np.random.default_rng(11 + tokens)
     rows, cols, layers, layer = 6912, 1152, 3, 1
