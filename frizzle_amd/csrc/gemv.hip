@@ -119,33 +119,27 @@ struct Mfma<4> {
 //   fma(1024 + q, d, -1032 d) = (q - 8) d  and
 //   fma(1024 + 16 q, d / 16, -72 d) = (q - 8) d,
 // both exact: every operand and the result fit in 24 bits.
-__device__ __forceinline__ void decode_group(uint4 c, uint16_t dbits, float (&wk)[32]) {
+// Half H of a group: weights 16 H .. 16 H + 15.
+template <int H>
+__device__ __forceinline__ void decode_half(uint4 c, uint16_t dbits, float (&wk)[16]) {
   const float d = half_to_float(dbits);
-  const float lo_bias = -1032.0f * d;
-  const float d16 = 0.0625f * d;
-  const float hi_bias = -72.0f * d;
+  const float scale = H == 0 ? d : 0.0625f * d;
+  const float bias = H == 0 ? -1032.0f * d : -72.0f * d;
   const uint32_t words[4] = {c.x, c.y, c.z, c.w};
   // The exponent comes from a register the compiler cannot see into, so that
   // (s & mask) | (exp & ~mask) stays one bitfield insert.
   uint32_t kExp;
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
-  constexpr uint32_t kLo = 0x000F000Fu, kHi = 0x00F000F0u;
+  constexpr uint32_t kMask = H == 0 ? 0x000F000Fu : 0x00F000F0u;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const uint32_t s = words[w], t = words[w] >> 8;
     // even: bytes 0 and 2 of the word; odd: bytes 1 and 3.
-    const half2v le = __builtin_bit_cast(half2v, (s & kLo) | (kExp & ~kLo));
-    const half2v lo = __builtin_bit_cast(half2v, (t & kLo) | (kExp & ~kLo));
-    const half2v he = __builtin_bit_cast(half2v, (s & kHi) | (kExp & ~kHi));
-    const half2v ho = __builtin_bit_cast(half2v, (t & kHi) | (kExp & ~kHi));
-    wk[4 * w + 0] = __builtin_fmaf((float)le.x, d, lo_bias);
-    wk[4 * w + 1] = __builtin_fmaf((float)lo.x, d, lo_bias);
-    wk[4 * w + 2] = __builtin_fmaf((float)le.y, d, lo_bias);
-    wk[4 * w + 3] = __builtin_fmaf((float)lo.y, d, lo_bias);
-    wk[16 + 4 * w + 0] = __builtin_fmaf((float)he.x, d16, hi_bias);
-    wk[16 + 4 * w + 1] = __builtin_fmaf((float)ho.x, d16, hi_bias);
-    wk[16 + 4 * w + 2] = __builtin_fmaf((float)he.y, d16, hi_bias);
-    wk[16 + 4 * w + 3] = __builtin_fmaf((float)ho.y, d16, hi_bias);
+    const half2v e = __builtin_bit_cast(half2v, (words[w] & kMask) | (kExp & ~kMask));
+    const half2v o = __builtin_bit_cast(half2v, ((words[w] >> 8) & kMask) | (kExp & ~kMask));
+    wk[4 * w + 0] = __builtin_fmaf((float)e.x, scale, bias);
+    wk[4 * w + 1] = __builtin_fmaf((float)o.x, scale, bias);
+    wk[4 * w + 2] = __builtin_fmaf((float)e.y, scale, bias);
+    wk[4 * w + 3] = __builtin_fmaf((float)o.y, scale, bias);
   }
 }
 
@@ -269,11 +263,37 @@ __device__ __forceinline__ void load_weights(const Tile<NB, GATED>& T, const Ste
   }
 }
 
+// Products for k = 16 H .. 16 H + 15 of a step, per matrix: decode the
+// weights, then the 16 products per block.
+template <int NB, bool GATED, int B, bool OPENS, int H>
+__device__ __forceinline__ void chain_half(const Tile<NB, GATED>& T, const Weights<GATED>& W,
+                                           typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
+  float4 xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xv[i] = T.x_get[B][4 * H + i];
+  const typename Mfma<NB>::Acc zero = {};
+#pragma unroll
+  for (int m = 0; m < Tile<NB, GATED>::kMats; ++m) {
+    float wk[16];
+    decode_half<H>(W.c[m], W.d[m], wk);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float xk = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
+        acc[m] = Mfma<NB>::op(wk[4 * i + j], xk, (OPENS && i == 0 && j == 0) ? zero : acc[m]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // One step t: stage step t + 1's inputs (loaded a step ago), start the loads
 // of step t + 2's inputs and t + 1's weights, then per matrix decode this
 // step's weights and chain its 32 products per block from buffer B (from
 // zero if the step opens a pass). Vector instructions do not run beside the
-// fp32 matrix instructions, so each kind is kept in one run.
+// fp32 matrix instructions, so each kind is kept in runs.
 template <int NB, bool GATED, int B, bool OPENS>
 __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepInfo<NB>& I1,
                                            const StepInfo<NB>& I2, float4 (&G)[8],
@@ -285,31 +305,15 @@ __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepI
   load_weights(T, I1, W_next);
   // The loads stay here, a step ahead of their use.
   __builtin_amdgcn_sched_barrier(0);
-  float4 xv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) xv[i] = T.x_get[B][i];
-  const typename Mfma<NB>::Acc zero = {};
-#pragma unroll
-  for (int m = 0; m < kMats; ++m) {
-    float wk[32];
-    decode_group(W.c[m], W.d[m], wk);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float xk = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
-        acc[m] = Mfma<NB>::op(wk[4 * i + j], xk, (OPENS && i == 0 && j == 0) ? zero : acc[m]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  // Half a group (16 k) at a time, to keep registers for a second wave.
+  chain_half<NB, GATED, B, OPENS, 0>(T, W, acc);
+  chain_half<NB, GATED, B, false, 1>(T, W, acc);
   wave_sync();
 }
 
 // A pass's range sums join the totals in range order.
 template <int NB>
-__device__ __forceinline__ void close_pass(const typename Mfma<NB>::Acc& acc,
+__device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
                                            float (&total)[Mfma<NB>::kSlots]) {
   constexpr int S = Mfma<NB>::kSlots;
 #pragma unroll
@@ -317,6 +321,8 @@ __device__ __forceinline__ void close_pass(const typename Mfma<NB>::Acc& acc,
 #pragma unroll
     for (int o = 0; o < S; ++o) total[o] = total[o] + acc[S * b + o];
   }
+#pragma unroll
+  for (int i = 0; i < NB * S; ++i) acc[i] = 0.0f;
 }
 
 // Step t, with the schedule of steps t .. t + 2 in hand; starts reading
@@ -328,11 +334,7 @@ __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedul
                                          typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
                                          float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
   I[3] = step_info(S, t + 3);
-  if (I[0].flags & kOpens) {
-    chain_step<NB, GATED, B, true>(T, I[1], I[2], G, W, W_next, acc);
-  } else {
-    chain_step<NB, GATED, B, false>(T, I[1], I[2], G, W, W_next, acc);
-  }
+  chain_step<NB, GATED, B, false>(T, I[1], I[2], G, W, W_next, acc);
   if (I[0].flags & kCloses) {
 #pragma unroll
     for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
@@ -388,6 +390,8 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   float total[kMats][SL];
 #pragma unroll
   for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int i = 0; i < NB * SL; ++i) acc[m][i] = 0.0f;
 #pragma unroll
     for (int o = 0; o < SL; ++o) total[m][o] = 0.0f;
   }
