@@ -193,9 +193,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
                                            0x00020000);
 }
 
-// A step's inputs pass through LDS: 64 lines (line L = block L / D,
-// token L % D) of 32 floats, stored 9 float4s apart so that the lanes' line
-// reads fall in distinct banks. Lane l loads float4 l % 8 of lines 8 i + l / 8.
+// A step's inputs pass through LDS, one buffer per wave: 64 lines (line L =
+// block L / D, token L % D) of 32 floats, stored 9 float4s apart so that the
+// lanes' line reads fall in distinct banks. Lane l loads float4 l % 8 of
+// lines 8 i + l / 8.
 constexpr int kXLine = 9;
 constexpr int kXBuf = 64 * kXLine;
 
@@ -207,8 +208,8 @@ struct Tile {
   __amdgpu_buffer_rsrc_t x, codes[kMats], scales[kMats];
   uint32_t x_off[kTokenRows];  // byte offset of float4 lane % 8 of each token it loads
   uint32_t row_group0;         // this lane's row times the row's groups
-  float4* x_put[2];            // its load slots, per buffer (+ 8 kXLine i)
-  const float4* x_get[2];      // its own line, per buffer
+  float4* x_put;               // its load slots (+ 8 kXLine i)
+  const float4* x_get;         // its own line
   int block;                   // lane / D
 };
 
@@ -229,7 +230,7 @@ __device__ __forceinline__ void load_inputs(const Tile<NB, GATED>& T, const Step
 
 template <int NB, bool GATED>
 __device__ __forceinline__ void stage_inputs(const Tile<NB, GATED>& T, const StepInfo<NB>& I,
-                                             int buf, float4 (&G)[8]) {
+                                             float4 (&G)[8]) {
   constexpr int kPer = Tile<NB, GATED>::kTokenRows;
   if (I.flags & kPads) {
 #pragma unroll
@@ -238,7 +239,7 @@ __device__ __forceinline__ void stage_inputs(const Tile<NB, GATED>& T, const Ste
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) T.x_put[buf][8 * kXLine * i] = G[i];
+  for (int i = 0; i < 8; ++i) T.x_put[8 * kXLine * i] = G[i];
 }
 
 template <bool GATED>
@@ -265,49 +266,48 @@ __device__ __forceinline__ void load_weights(const Tile<NB, GATED>& T, const Ste
 
 // Products for k = 16 H .. 16 H + 15 of a step, per matrix: decode the
 // weights, then the 16 products per block.
-template <int NB, bool GATED, int B, bool OPENS, int H>
-__device__ __forceinline__ void chain_half(const Tile<NB, GATED>& T, const Weights<GATED>& W,
+template <int NB, bool GATED, int H>
+__device__ __forceinline__ void chain_half(const float4 (&xv)[8], const Weights<GATED>& W,
                                            typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
-  float4 xv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xv[i] = T.x_get[B][4 * H + i];
-  const typename Mfma<NB>::Acc zero = {};
-#pragma unroll
-  for (int m = 0; m < Tile<NB, GATED>::kMats; ++m) {
+  for (int m = 0; m < (GATED ? 2 : 1); ++m) {
     float wk[16];
     decode_half<H>(W.c[m], W.d[m], wk);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float xk = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
-        acc[m] = Mfma<NB>::op(wk[4 * i + j], xk, (OPENS && i == 0 && j == 0) ? zero : acc[m]);
-      }
+      const float4 x4 = xv[4 * H + i];
+      acc[m] = Mfma<NB>::op(wk[4 * i + 0], x4.x, acc[m]);
+      acc[m] = Mfma<NB>::op(wk[4 * i + 1], x4.y, acc[m]);
+      acc[m] = Mfma<NB>::op(wk[4 * i + 2], x4.z, acc[m]);
+      acc[m] = Mfma<NB>::op(wk[4 * i + 3], x4.w, acc[m]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// One step t: stage step t + 1's inputs (loaded a step ago), start the loads
-// of step t + 2's inputs and t + 1's weights, then per matrix decode this
-// step's weights and chain its 32 products per block from buffer B (from
-// zero if the step opens a pass). Vector instructions do not run beside the
-// fp32 matrix instructions, so each kind is kept in runs.
-template <int NB, bool GATED, int B, bool OPENS>
+// One step: read this step's inputs from the wave's LDS buffer, then stage
+// step t + 1's there (loaded a step ago; a wave's LDS accesses run in
+// order), start the loads of step t + 2's inputs and t + 1's weights, and
+// chain this step's 32 products per block, half a group at a time so that
+// the decoded weights need few registers. Vector instructions do not run
+// beside the fp32 matrix instructions, so each kind is kept in runs.
+template <int NB, bool GATED>
 __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepInfo<NB>& I1,
                                            const StepInfo<NB>& I2, float4 (&G)[8],
                                            const Weights<GATED>& W, Weights<GATED>& W_next,
                                            typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
-  constexpr int kMats = Tile<NB, GATED>::kMats;
-  stage_inputs(T, I1, B ^ 1, G);
+  float4 xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xv[i] = T.x_get[i];
+  __builtin_amdgcn_sched_barrier(0);
+  stage_inputs(T, I1, G);
   load_inputs(T, I2, G);
   load_weights(T, I1, W_next);
   // The loads stay here, a step ahead of their use.
   __builtin_amdgcn_sched_barrier(0);
-  // Half a group (16 k) at a time, to keep registers for a second wave.
-  chain_half<NB, GATED, B, OPENS, 0>(T, W, acc);
-  chain_half<NB, GATED, B, false, 1>(T, W, acc);
+  chain_half<NB, GATED, 0>(xv, W, acc);
+  chain_half<NB, GATED, 1>(xv, W, acc);
   wave_sync();
 }
 
@@ -327,14 +327,14 @@ __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
 
 // Step t, with the schedule of steps t .. t + 2 in hand; starts reading
 // step t + 3's (first used a step later, so its wait costs nothing).
-template <int NB, bool GATED, int B>
+template <int NB, bool GATED>
 __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedule<NB>& S, int t,
                                          StepInfo<NB> (&I)[4], float4 (&G)[8],
                                          const Weights<GATED>& W, Weights<GATED>& W_next,
                                          typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
                                          float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
   I[3] = step_info(S, t + 3);
-  chain_step<NB, GATED, B, false>(T, I[1], I[2], G, W, W_next, acc);
+  chain_step<NB, GATED>(T, I[1], I[2], G, W, W_next, acc);
   if (I[0].flags & kCloses) {
 #pragma unroll
     for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   constexpr int D = M::kDim;
   constexpr int SL = M::kSlots;
   constexpr int kMats = GATED ? 2 : 1;
-  __shared__ float4 staged[kTileWaves][2][kXBuf];
+  __shared__ float4 staged[kTileWaves][kXBuf];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tokens = (int)step->tokens;
   const int token0 = (blockIdx.y * kTileWaves + wave) * D;
@@ -380,11 +380,8 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
     const int tok = min(token0 + (8 * i + (lane >> 3)) % D, tokens - 1);
     T.x_off[i] = 4u * ((uint32_t)tok * (uint32_t)x_stride + 4u * (uint32_t)(lane & 7));
   }
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    T.x_put[b] = staged[wave][b] + (lane >> 3) * kXLine + (lane & 7);
-    T.x_get[b] = staged[wave][b] + lane * kXLine;
-  }
+  T.x_put = staged[wave] + (lane >> 3) * kXLine + (lane & 7);
+  T.x_get = staged[wave] + lane * kXLine;
 
   typename M::Acc acc[kMats];
   float total[kMats][SL];
@@ -403,15 +400,15 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   I[2] = step_info(S, 2);
   float4 G[8];
   load_inputs(T, I[0], G);
-  stage_inputs(T, I[0], 0, G);
+  stage_inputs(T, I[0], G);
   load_inputs(T, I[1], G);
   Weights<GATED> W0, W1;
   load_weights(T, I[0], W0);
   wave_sync();
   for (int t = 0; t < S.steps; t += 2) {
-    run_step<NB, GATED, 0>(T, S, t, I, G, W0, W1, acc, total);
+    run_step<NB, GATED>(T, S, t, I, G, W0, W1, acc, total);
     if (t + 1 >= S.steps) break;
-    run_step<NB, GATED, 1>(T, S, t + 1, I, G, W1, W0, acc, total);
+    run_step<NB, GATED>(T, S, t + 1, I, G, W1, W0, acc, total);
   }
 
   const int tok = token0 + lane % D;
