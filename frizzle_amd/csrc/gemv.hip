@@ -6,9 +6,11 @@
 // zero. Every form below keeps that order, so a token's outputs are the same
 // bits whether it is decoded alone or prefilled in a tile.
 //
-// Q4_0 weight j of a block is ((code_j) - 8) * d, decoded exactly in f32
-// (q4_0.wgsl:71-83) as fma(code, d, -8 d): code * d and 8 d are exact, and
-// so is their difference, so the fma's one rounding changes nothing.
+// Q4_0 weight j of a block is ((code_j) - 8) * d (q4_0.wgsl:71-83), made
+// exactly in f32: the value needs at most 15 significant bits.
+//
+// Single-token steps go to the decode forms (gemv_decode.hip); steps of
+// several tokens run here on the fp32 matrix cores.
 
 #include <algorithm>
 

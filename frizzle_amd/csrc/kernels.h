@@ -48,7 +48,7 @@ struct Q4Matrix {
 // ---- products ----------------------------------------------------------
 // y[t][o] = sum_k W[o][k] x[t][k] for t < step.tokens (or only the last
 // token when last_token), in the reference's order. Decode form when the
-// step holds one token; tiled form otherwise.
+// step holds one token; matrix-core form otherwise.
 hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token);
