@@ -68,6 +68,9 @@ def parse():
                    help="launch decode kernels one by one instead of replaying a graph")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the GEMV roofline and a 256 MiB device copy (for counter runs)")
+    p.add_argument("--gguf-load", action="store_true",
+                   help="only: write the synthetic full-size model as a GGUF file, load it "
+                        "with frz_model_load_gguf, check its tokens, print one JSON line")
     p.add_argument("--prefill-only", action="store_true",
                    help="only the 2,048-token prefill, printed as one JSON line (for profiles)")
     p.add_argument("--gemv-stream", action="store_true",
@@ -154,6 +157,41 @@ def cpu_sample(orc, cfg, tensors, prompt, budget_s, max_tokens):
     return tokens, lg, elapsed, len(tokens) - 1
 
 
+def gguf_load(fz, seed):
+    """The full-size synthetic model through a GGUF file: write, then time
+    frz_model_load_gguf (index read, shape checks, file reads, uploads); its
+    tokens must equal those of the same weights set directly."""
+    import tempfile
+    from frizzle_amd import gguf
+    cfg = fz.gemma3_1b_config(context=4096)
+    tensors = synth_all(fz, cfg, seed)
+    dev = fz.Device(0)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "gemma3-1b-synthetic-q4_0.gguf"
+        t0 = time.perf_counter()
+        gguf.write_gemma3(path, cfg, lambda l, r: tensors[(l, r)].tobytes())
+        write_s = time.perf_counter() - t0
+        size = path.stat().st_size
+        del tensors
+        a = fz.Model(dev, cfg)
+        dev.sync()
+        t0 = time.perf_counter()
+        a.load_gguf(path)
+        dev.sync()
+        load_s = time.perf_counter() - t0
+    b = fz.Model(dev, cfg)
+    b.synthesize(seed)
+    prompt = np.random.default_rng(seed + 5).integers(0, cfg.vocab, 32).astype(np.uint32)
+    same = bool(np.array_equal(a.generate(prompt, max_tokens=16), b.generate(prompt, max_tokens=16)))
+    a.close()
+    b.close()
+    dev.close()
+    log(f"gguf: wrote {size / 1e6:.0f} MB in {write_s:.1f}s, loaded in {load_s:.2f}s")
+    print(json.dumps({"gguf_load": True, "file_bytes": size, "load_seconds": load_s,
+                      "load_gbs": size / load_s / 1e9, "tokens_identical_to_direct_upload": same,
+                      "model": "full 26-layer Gemma-3-1B shape, synthetic Q4_0"}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -171,6 +209,10 @@ def main():
         achieved = GEMV_BYTES / (us * 1e-6) / 1e9
         print(json.dumps({"roofline_only": True, "us_per_launch": us, "achieved_gbs": achieved,
                           "frac": achieved / HBM_PEAK_GBS}))
+        return
+
+    if args.gguf_load:
+        gguf_load(fz, args.seed)
         return
 
     context = 8192

@@ -54,7 +54,14 @@ class Edit(ctypes.Structure):
                 ("value", c_float), ("from_", c_uint32), ("until", c_uint32)]
 
 
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", c_char * 65), ("type", c_uint32), ("dimensions", c_uint32),
+                ("shape", c_uint64 * 4), ("elements", c_uint64), ("offset", c_uint64),
+                ("bytes", c_uint64)]
+
+
 _P = c_void_p
+_S = ctypes.c_char_p
 _SIGS = {
     "frz_last_error": (ctypes.c_char_p, []),
     "frz_open": (c_int, [c_int, POINTER(c_void_p), POINTER(Limits)]),
@@ -123,6 +130,22 @@ _SIGS = {
                                       POINTER(Sampling), POINTER(c_double)]),
     "frz_generate": (c_int, [_P, _P, c_uint32, _P, c_uint32, POINTER(Sampling),
                              c_uint32, _P, c_uint32, _P, POINTER(c_uint32)]),
+    "frz_model_get_config": (c_int, [_P, POINTER(ModelConfig)]),
+    "frz_gguf_read": (c_int, [_P, c_uint64, c_uint64, POINTER(c_void_p), POINTER(c_uint64)]),
+    "frz_gguf_open": (c_int, [_S, POINTER(c_void_p)]),
+    "frz_gguf_free": (None, [_P]),
+    "frz_gguf_error_text": (_S, [c_int]),
+    "frz_gguf_format": (c_int, [c_uint32, POINTER(_S), POINTER(c_uint32), POINTER(c_uint32)]),
+    "frz_gguf_tensor_count": (c_uint64, [_P]),
+    "frz_gguf_tensor_at": (c_int, [_P, c_uint64, POINTER(GgufTensor)]),
+    "frz_gguf_find": (c_int, [_P, _S, POINTER(GgufTensor)]),
+    "frz_gguf_metadata_count": (c_uint64, [_P]),
+    "frz_gguf_get_u32": (c_int, [_P, _S, POINTER(c_uint32)]),
+    "frz_gguf_get_f32": (c_int, [_P, _S, POINTER(c_float)]),
+    "frz_gguf_get_string": (c_int, [_P, _S, _P, c_uint64, POINTER(c_uint64)]),
+    "frz_gguf_get_array": (c_int, [_P, _S, POINTER(c_uint32), POINTER(c_uint64)]),
+    "frz_gemma3_config_from_gguf": (c_int, [_P, c_int, POINTER(ModelConfig)]),
+    "frz_model_load_gguf": (c_int, [_P, _S]),
 }
 
 _lib = None

@@ -579,6 +579,12 @@ int frz_model_set_tensor(frz_model* m, int layer, int role, const void* data, ui
   }
 }
 
+int frz_model_get_config(const frz_model* m, frz_model_config* out) {
+  if (!m || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_get_config: null argument");
+  *out = m->c;
+  return FRZ_OK;
+}
+
 int frz_model_synthesize(frz_model* m, uint64_t seed) {
   if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_synthesize: null model");
   std::vector<uint8_t> buf;

@@ -211,6 +211,10 @@ class Model:
         check(self.lib.frz_model_set_tensor(self.handle, layer, _lib.ROLE[role],
                                             a.ctypes.data, a.nbytes))
 
+    def load_gguf(self, path):
+        """Every tensor of a Gemma 3 GGUF file of this model's shapes."""
+        check(self.lib.frz_model_load_gguf(self.handle, str(path).encode()))
+
     def synthesize(self, seed):
         check(self.lib.frz_model_synthesize(self.handle, seed))
 

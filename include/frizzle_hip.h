@@ -280,6 +280,8 @@ int frz_model_set_tensor(frz_model* model, int layer, int role,
                          const void* data, uint64_t bytes);
 /* Every tensor from frz_synth_tensor(seed). */
 int frz_model_synthesize(frz_model* model, uint64_t seed);
+/* The shapes the model was created with. */
+int frz_model_get_config(const frz_model* model, frz_model_config* out);
 /* The edit table, u32 words in the reference's layout (src/core/edit/
  * edit.h: per layer [first, count], then [neuron, kind, value bits, first
  * position, end position] per edit), used by every later step. */
@@ -330,6 +332,107 @@ int frz_generate(frz_model* model, const uint32_t* prompt, uint32_t prompt_len,
                  const frz_sampling* sampling, uint32_t max_tokens,
                  const uint32_t* stop_ids, uint32_t stops,
                  uint32_t* tokens_out, uint32_t* drawn);
+
+/* ---- GGUF files (replaces the reference's gguf::read_index and the
+ *      Gemma 3 load, src/core/gguf/reader.h:12-107, index.h,
+ *      src/core/arch/gemma3/gemma3.cpp:21-95, describe.cpp:205-290) ------- */
+
+/* The ways reading a file's index can fail, each a named rule of the file
+ * (the reference's ReadError, src/core/gguf/types.h:237-265). */
+enum frz_gguf_error {
+  FRZ_GGUF_OK = 0,
+  FRZ_GGUF_NEED_MORE_BYTES = 1,   /* inside the file, not yet supplied */
+  FRZ_GGUF_SHORT_READ = 2,        /* the file ends before this field */
+  FRZ_GGUF_BAD_MAGIC = 3,
+  FRZ_GGUF_UNSUPPORTED_VERSION = 4,
+  FRZ_GGUF_COUNT_TOO_LARGE = 5,   /* over 2^20 tensors or metadata entries */
+  FRZ_GGUF_STRING_TOO_LONG = 6,   /* over 2^20 bytes */
+  FRZ_GGUF_ARRAY_TOO_LONG = 7,    /* over 2^24 elements */
+  FRZ_GGUF_UNKNOWN_VALUE_TYPE = 8,
+  FRZ_GGUF_UNKNOWN_TENSOR_TYPE = 9,
+  FRZ_GGUF_ROW_NOT_WHOLE_BLOCKS = 10,
+  FRZ_GGUF_TOO_MANY_DIMENSIONS = 11,
+  FRZ_GGUF_NEGATIVE_DIMENSION = 12,
+  FRZ_GGUF_ELEMENT_COUNT_OVERFLOW = 13,
+  FRZ_GGUF_OFFSET_OVERFLOW = 14,
+  FRZ_GGUF_TENSOR_DATA_OUT_OF_BOUNDS = 15,
+  FRZ_GGUF_DUPLICATE_TENSOR_NAME = 16,
+  FRZ_GGUF_TENSOR_NAME_TOO_LONG = 17, /* over 64 bytes */
+  FRZ_GGUF_MISALIGNED_TENSOR_DATA = 18,
+  FRZ_GGUF_OVERLAPPING_TENSOR_DATA = 19,
+  FRZ_GGUF_BAD_ALIGNMENT = 20,    /* general.alignment: not a power-of-two uint32 */
+  FRZ_GGUF_EMPTY_KEY = 21,
+  FRZ_GGUF_DUPLICATE_METADATA_KEY = 22,
+  FRZ_GGUF_NESTED_ARRAY = 23
+};
+
+typedef struct frz_gguf frz_gguf;
+
+/* One tensor of the index: GGUF's format number, its extents (ne0 first,
+ * unused ones 1), and its absolute byte range in the file. */
+typedef struct frz_gguf_tensor {
+  char name[65];
+  uint32_t type;
+  uint32_t dimensions;
+  uint64_t shape[4];
+  uint64_t elements;
+  uint64_t offset;
+  uint64_t bytes;
+} frz_gguf_tensor;
+
+/* Reads the index of a file of `file_size` bytes whose first `resident`
+ * bytes are at `front`; tensor data is never read. Returns a
+ * frz_gguf_error. On FRZ_GGUF_OK, *out is a new index (frz_gguf_free); on
+ * FRZ_GGUF_NEED_MORE_BYTES, *bytes_needed is the length of front, from byte
+ * 0, the read needed; *out is untouched unless the read succeeds. -1 for a
+ * null `out`, or a null `front` with resident bytes. */
+int frz_gguf_read(const void* front, uint64_t resident, uint64_t file_size,
+                  frz_gguf** out, uint64_t* bytes_needed);
+/* The same from a file's path, reading its front as the index asks.
+ * Returns a frz_gguf_error, or -1 when the file cannot be opened or read. */
+int frz_gguf_open(const char* path, frz_gguf** out);
+void frz_gguf_free(frz_gguf* index);
+const char* frz_gguf_error_text(int error);
+/* A format's name and block (elements, bytes); FRZ_ERR_ARGUMENT for a number
+ * GGUF does not define. */
+int frz_gguf_format(uint32_t type, const char** name, uint32_t* block_elements,
+                    uint32_t* block_bytes);
+
+uint64_t frz_gguf_tensor_count(const frz_gguf* index);
+int frz_gguf_tensor_at(const frz_gguf* index, uint64_t i, frz_gguf_tensor* out);
+/* FRZ_ERR_ARGUMENT when no tensor has the name. */
+int frz_gguf_find(const frz_gguf* index, const char* name, frz_gguf_tensor* out);
+uint64_t frz_gguf_metadata_count(const frz_gguf* index);
+/* Metadata by key. An integer of any width that fits, a FLOAT32/FLOAT64
+ * as float, a string (length without the terminator; the text is cut to
+ * cap - 1 bytes and terminated), an array's element type and count.
+ * FRZ_ERR_ARGUMENT when the key is absent or holds another kind. */
+int frz_gguf_get_u32(const frz_gguf* index, const char* key, uint32_t* out);
+int frz_gguf_get_f32(const frz_gguf* index, const char* key, float* out);
+int frz_gguf_get_string(const frz_gguf* index, const char* key, char* buf,
+                        uint64_t cap, uint64_t* length);
+int frz_gguf_get_array(const frz_gguf* index, const char* key,
+                       uint32_t* element_type, uint64_t* count);
+
+/* A Gemma 3 model's shapes from its metadata and its token embedding
+ * (describe.cpp:205-290, gemma3.cpp:44-95): gemma3.block_count,
+ * embedding_length, feed_forward_length, attention.head_count,
+ * attention.head_count_kv, attention.key_length (default width / heads),
+ * attention.layer_norm_rms_epsilon, rope.freq_base, rope.freq_base_swa
+ * (default 10,000), attention.sliding_window, sliding_window_pattern
+ * (default 6); the vocabulary is token_embd.weight's second extent.
+ * `context` positions for the global caches (0: 8,192). */
+int frz_gemma3_config_from_gguf(const frz_gguf* index, int context,
+                                frz_model_config* out);
+/* Loads every tensor of a Gemma 3 GGUF file into a model created with that
+ * file's shapes: blk.N.{attn_q,attn_k,attn_v,attn_output,ffn_gate,ffn_up,
+ * ffn_down}.weight (Q4_0), blk.N.{attn_norm,attn_q_norm,attn_k_norm,
+ * post_attention_norm,ffn_norm,post_ffw_norm}.weight (F32),
+ * token_embd.weight (Q4_0, tied head) and output_norm.weight (F32).
+ * FRZ_ERR_ARGUMENT, naming the tensor, for a missing tensor, a shape that
+ * is not the model's, a format this backend does not run, or an untied
+ * output.weight. */
+int frz_model_load_gguf(frz_model* model, const char* path);
 
 #ifdef __cplusplus
 }

@@ -1,4 +1,7 @@
-"""Seeded inputs shared by the tests."""
+"""Seeded inputs and small readers shared by the tests."""
+import struct
+from pathlib import Path
+
 import numpy as np
 
 
@@ -39,3 +42,57 @@ def assert_same_bits(got, want, what=""):
         raise AssertionError(
             f"{what}: {diff.size} of {g.size} values differ; first at {i}: "
             f"got {np.float32(got.ravel()[i])!r} want {np.float32(want.ravel()[i])!r}")
+
+
+def read_gguf(path):
+    """The tensors of a GGUF v3 file: {name: (dims, type, bytes)}."""
+    data = Path(path).read_bytes()
+    at = 0
+
+    def take(fmt):
+        nonlocal at
+        v = struct.unpack_from(fmt, data, at)
+        at += struct.calcsize(fmt)
+        return v if len(v) > 1 else v[0]
+
+    def string():
+        nonlocal at
+        n = take("<Q")
+        s = data[at:at + n]
+        at += n
+        return s
+
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def value(t):
+        nonlocal at
+        if t == 8:
+            return string()
+        if t == 9:
+            et, n = take("<I"), take("<Q")
+            return [value(et) for _ in range(n)]
+        v = data[at:at + sizes[t]]
+        at += sizes[t]
+        return v
+
+    assert data[:4] == b"GGUF"
+    at = 4
+    version, tensors, kvs = take("<I"), take("<Q"), take("<Q")
+    assert version == 3
+    meta = {}
+    for _ in range(kvs):
+        key = string()
+        meta[key] = value(take("<I"))
+    infos = []
+    for _ in range(tensors):
+        name = string()
+        dims = [take("<q") for _ in range(take("<I"))]
+        infos.append((name, dims, take("<I"), take("<Q")))
+    align = struct.unpack("<I", meta[b"general.alignment"])[0]
+    base = (at + align - 1) // align * align
+    out = {}
+    for name, dims, ttype, off in infos:
+        n = int(np.prod(dims))
+        size = n // 32 * 18 if ttype == 2 else n * 4
+        out[name] = (dims, ttype, data[base + off:base + off + size])
+    return out

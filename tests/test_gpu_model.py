@@ -153,3 +153,96 @@ def test_seeded_sampling_token_identical(device):
     got = model.generate(prompt, samp=samp, max_tokens=steps)
     assert np.array_equal(got, want)
     model.close()
+
+
+# ---- GGUF files -------------------------------------------------------------------
+
+def _synth_all(cfg, seed):
+    t = {(l, r): fz.synth_tensor(cfg, seed, l, r) for l in range(cfg.layers) for r in ROLES}
+    t[(-1, "embedding")] = fz.synth_tensor(cfg, seed, -1, "embedding")
+    t[(-1, "output_norm")] = fz.synth_tensor(cfg, seed, -1, "output_norm")
+    return t
+
+
+def test_gguf_file_loads_the_same_model(device, tmp_path):
+    # A model read from a GGUF file (frz_model_load_gguf) is the model its
+    # tensors make when uploaded one by one: same logits, same tokens.
+    from frizzle_amd import gguf
+    cfg = small_config()
+    t = _synth_all(cfg, 31)
+    path = gguf.write_gemma3(tmp_path / "m.gguf", cfg, lambda l, r: t[(l, r)].tobytes())
+    fc = gguf.Index.open(path).gemma3_config(context=cfg.context)
+    for name in ("hidden", "ffn", "head_dim", "query_heads", "kv_heads", "layers", "vocab",
+                 "window", "pattern"):
+        assert getattr(fc, name) == getattr(cfg, name), name
+    a, _ = build_pair(device, cfg, 31)
+    b = fz.Model(device, cfg)
+    b.load_gguf(path)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 40).astype(np.uint32)
+    ta = a.generate(prompt, max_tokens=12)
+    la = a.logits()
+    tb = b.generate(prompt, max_tokens=12)
+    lb = b.logits()
+    assert np.array_equal(ta, tb)
+    assert_same_bits(lb, la, "logits after 12 tokens")
+    a.close()
+    b.close()
+
+
+def test_gguf_load_refusals(device, tmp_path):
+    from frizzle_amd import gguf
+    cfg = small_config()
+    t = _synth_all(cfg, 32)
+    model = fz.Model(device, cfg)
+    # a format this backend does not run, named with its tensor
+    q8 = lambda l, r: (np.zeros(cfg.vocab * cfg.hidden // 32 * 34, np.uint8).tobytes()
+                       if r == "embedding" else t[(l, r)].tobytes())
+    p = gguf.write_gemma3(tmp_path / "q8.gguf", cfg, q8, formats={"token_embd.weight": gguf.T_Q8_0})
+    with pytest.raises(fz.FrzError, match="token_embd.weight: format Q8_0"):
+        model.load_gguf(p)
+    # another model's shapes
+    other = small_config(layers=2)
+    t2 = _synth_all(other, 32)
+    p = gguf.write_gemma3(tmp_path / "two.gguf", other, lambda l, r: t2[(l, r)].tobytes())
+    with pytest.raises(fz.FrzError, match="shapes are not the model's"):
+        model.load_gguf(p)
+    # a missing tensor
+    ts = [(n, d, f, b) for n, d, f, b in _gemma3_tensors(cfg, t) if n != "blk.2.ffn_up.weight"]
+    p = gguf.write(tmp_path / "missing.gguf", ts, _gemma3_meta(cfg))
+    with pytest.raises(fz.FrzError, match="missing tensor blk.2.ffn_up.weight"):
+        model.load_gguf(p)
+    # a malformed file, named by its rule
+    whole = (tmp_path / "two.gguf").read_bytes()
+    first = min(d["offset"] for d in gguf.Index.open(tmp_path / "two.gguf").tensors)
+    p = tmp_path / "cut.gguf"
+    p.write_bytes(whole[:first + 100])  # the index whole, the data cut
+    with pytest.raises(fz.FrzError, match="tensor data lies outside the file"):
+        model.load_gguf(p)
+    model.close()
+
+
+def _gemma3_tensors(cfg, t):
+    from frizzle_amd import gguf
+    out = [("token_embd.weight", [cfg.hidden, cfg.vocab], gguf.T_Q4_0,
+            t[(-1, "embedding")].tobytes())]
+    for l in range(cfg.layers):
+        for role, leaf in gguf.LAYER_NAMES.items():
+            fmt = gguf.T_F32 if "norm" in role else gguf.T_Q4_0
+            out.append((f"blk.{l}.{leaf}", gguf._extents(cfg, role), fmt, t[(l, role)].tobytes()))
+    out.append(("output_norm.weight", [cfg.hidden], gguf.T_F32, t[(-1, "output_norm")].tobytes()))
+    return out
+
+
+def _gemma3_meta(cfg):
+    from frizzle_amd import gguf
+    return [("general.architecture", gguf.STRING, "gemma3"),
+            ("gemma3.block_count", gguf.U32, cfg.layers),
+            ("gemma3.embedding_length", gguf.U32, cfg.hidden),
+            ("gemma3.feed_forward_length", gguf.U32, cfg.ffn),
+            ("gemma3.attention.head_count", gguf.U32, cfg.query_heads),
+            ("gemma3.attention.head_count_kv", gguf.U32, cfg.kv_heads),
+            ("gemma3.attention.key_length", gguf.U32, cfg.head_dim),
+            ("gemma3.attention.layer_norm_rms_epsilon", gguf.F32, cfg.epsilon),
+            ("gemma3.rope.freq_base", gguf.F32, cfg.rope_global),
+            ("gemma3.attention.sliding_window", gguf.U32, cfg.window),
+            ("gemma3.attention.sliding_window_pattern", gguf.U32, cfg.pattern)]

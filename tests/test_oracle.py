@@ -10,14 +10,13 @@ stated definition and these tests bound its accuracy; the bits themselves
 stay "parity unpinned".
 """
 import math
-import struct
 from pathlib import Path
 
 import numpy as np
 import pytest
 
 import _oracle as orc
-from helpers import bits, dequant, q4_blocks
+from helpers import bits, dequant, q4_blocks, read_gguf
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 U = 2.0 ** -24  # unit roundoff of f32
@@ -36,65 +35,11 @@ def ulps(a, b):
 
 # ---- the reference's own fixture -------------------------------------------------
 
-def read_gguf(path):
-    """The tensors of a GGUF v3 file: {name: (dims, type, bytes)}."""
-    data = Path(path).read_bytes()
-    at = 0
-
-    def take(fmt):
-        nonlocal at
-        v = struct.unpack_from(fmt, data, at)
-        at += struct.calcsize(fmt)
-        return v if len(v) > 1 else v[0]
-
-    def string():
-        nonlocal at
-        n = take("<Q")
-        s = data[at:at + n]
-        at += n
-        return s
-
-    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
-
-    def value(t):
-        nonlocal at
-        if t == 8:
-            return string()
-        if t == 9:
-            et, n = take("<I"), take("<Q")
-            return [value(et) for _ in range(n)]
-        v = data[at:at + sizes[t]]
-        at += sizes[t]
-        return v
-
-    assert data[:4] == b"GGUF"
-    at = 4
-    version, tensors, kvs = take("<I"), take("<Q"), take("<Q")
-    assert version == 3
-    meta = {}
-    for _ in range(kvs):
-        key = string()
-        meta[key] = value(take("<I"))
-    infos = []
-    for _ in range(tensors):
-        name = string()
-        dims = [take("<q") for _ in range(take("<I"))]
-        infos.append((name, dims, take("<I"), take("<Q")))
-    align = struct.unpack("<I", meta[b"general.alignment"])[0]
-    base = (at + align - 1) // align * align
-    out = {}
-    for name, dims, ttype, off in infos:
-        n = int(np.prod(dims))
-        size = n // 32 * 18 if ttype == 2 else n * 4
-        out[name] = (dims, ttype, data[base + off:base + off + size])
-    return out
-
-
 def test_q4_0_matches_reference_fixture():
     # tests/fixtures/gguf/valid.gguf (made by make_gguf_fixtures.py:65-73):
     # token_embd.weight is Q4_0 [64, 2], four blocks of scale 0x3C00 (1.0)
     # and code byte 0x10, so each block is sixteen -8s then sixteen -7s.
-    t = read_gguf(GOLDEN / "valid.gguf")
+    t = read_gguf(GOLDEN / "gguf" / "valid.gguf")
     dims, ttype, raw = t[b"token_embd.weight"]
     assert dims == [64, 2] and ttype == 2 and len(raw) == 4 * 18
     blocks = np.frombuffer(raw, dtype=np.uint8).reshape(4, 18)
