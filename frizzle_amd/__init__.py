@@ -6,13 +6,15 @@ package does not load the library; the first call that needs it does, and
 raises if it has not been built.
 """
 from ._lib import FrzError, exported_symbols, load
-from .runtime import (TO_THE_END, Device, DeviceArray, Edit, EditError,
-                      EditKind, Model, edit_apply, edit_check, edit_table,
-                      gemma3_1b_config, q4_0_split, rope_turns, sampling,
-                      synth_tensor, tensor_bytes)
+from .runtime import (Q4_0, Q4_1, Q8_0, TO_THE_END, Device, DeviceArray,
+                      Edit, EditError, EditKind, Model, block_split,
+                      edit_apply, edit_check, edit_table, gemma3_1b_config,
+                      q4_0_split, rope_turns, sampling, synth_tensor,
+                      tensor_bytes)
 
 __all__ = [
-    "FrzError", "exported_symbols", "load", "TO_THE_END", "Device",
+    "FrzError", "exported_symbols", "load", "Q4_0", "Q4_1", "Q8_0",
+    "TO_THE_END", "Device", "block_split",
     "DeviceArray", "Edit", "EditError", "EditKind", "Model", "edit_apply",
     "edit_check", "edit_table", "gemma3_1b_config", "q4_0_split",
     "rope_turns", "sampling", "synth_tensor", "tensor_bytes",

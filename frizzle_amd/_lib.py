@@ -74,6 +74,11 @@ _SIGS = {
     "frz_fill_zero": (c_int, [_P, _P, c_uint64]),
     "frz_copy": (c_int, [_P, _P, _P, c_uint64]),
     "frz_q4_0_split": (c_int, [_P, c_uint64, _P, _P]),
+    "frz_block_split": (c_int, [c_int, _P, c_uint64, _P, _P]),
+    "frz_op_gemv_format": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P, c_int, _P, c_int,
+                                   c_uint32, c_int]),
+    "frz_op_gather_format": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P, c_uint32, c_float,
+                                     _P]),
     "frz_op_gemv": (c_int, [_P, _P, _P, c_int, c_int, _P, c_int, _P, c_int,
                             c_uint32, c_int]),
     "frz_op_gated": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P, _P,
@@ -114,6 +119,7 @@ _SIGS = {
     "frz_model_create": (c_int, [_P, POINTER(ModelConfig), POINTER(c_void_p)]),
     "frz_model_destroy": (None, [_P]),
     "frz_model_set_tensor": (c_int, [_P, c_int, c_int, _P, c_uint64]),
+    "frz_model_set_tensor_format": (c_int, [_P, c_int, c_int, c_int, _P, c_uint64]),
     "frz_model_synthesize": (c_int, [_P, c_uint64]),
     "frz_model_set_edits": (c_int, [_P, _P, c_uint32]),
     "frz_model_set_graphs": (c_int, [_P, c_int]),

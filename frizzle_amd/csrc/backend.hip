@@ -186,22 +186,35 @@ int frz_fill_zero(frz_device* dev, void* dev_dst, uint64_t bytes) {
 
 int frz_q4_0_split(const void* gguf_blocks, uint64_t blocks, void* codes_out,
                    void* scales_out) {
+  return frz_block_split(kQ4_0, gguf_blocks, blocks, codes_out, scales_out);
+}
+
+int frz_block_split(int format, const void* gguf_blocks, uint64_t blocks, void* codes_out,
+                    void* scales_out) {
   if (!gguf_blocks || !codes_out || !scales_out) {
-    return fail(FRZ_ERR_ARGUMENT, "frz_q4_0_split: null argument");
+    return fail(FRZ_ERR_ARGUMENT, "frz_block_split: null argument");
   }
+  if (format != kQ4_0 && format != kQ4_1 && format != kQ8_0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_block_split: format " + std::to_string(format) +
+                                      " (Q4_0 2, Q4_1 3 or Q8_0 8)");
+  }
+  // A block is its scale halves (d; Q4_1: d, m) then its code bytes.
+  const size_t cb = code_bytes(format), sb = 2 * scale_halves(format);
+  const size_t bb = gguf_block_bytes(format);
   const uint8_t* in = static_cast<const uint8_t*>(gguf_blocks);
   uint8_t* codes = static_cast<uint8_t*>(codes_out);
   uint8_t* scales = static_cast<uint8_t*>(scales_out);
   for (uint64_t b = 0; b < blocks; ++b) {
-    std::memcpy(codes + 16 * b, in + 18 * b + 2, 16);
-    std::memcpy(scales + 2 * b, in + 18 * b, 2);
+    std::memcpy(codes + cb * b, in + bb * b + sb, cb);
+    std::memcpy(scales + sb * b, in + bb * b, sb);
   }
   return FRZ_OK;
 }
 
-static Q4Matrix q4(const void* codes, const void* scales, int rows, int cols) {
-  return Q4Matrix{static_cast<const uint8_t*>(codes), static_cast<const uint16_t*>(scales), rows,
-                  cols};
+static QMatrix q4(const void* codes, const void* scales, int rows, int cols,
+                  int format = kQ4_0) {
+  return QMatrix{static_cast<const uint8_t*>(codes), static_cast<const uint16_t*>(scales), rows,
+                 cols, format};
 }
 
 static bool shape_ok(int rows, int cols) { return rows > 0 && cols > 0 && cols % 32 == 0; }
@@ -209,13 +222,23 @@ static bool shape_ok(int rows, int cols) { return rows > 0 && cols > 0 && cols %
 int frz_op_gemv(frz_device* dev, const void* codes, const void* scales, int rows, int cols,
                 const float* x, int x_stride, float* y, int y_stride, uint32_t tokens,
                 int last_token) {
+  return frz_op_gemv_format(dev, kQ4_0, codes, scales, rows, cols, x, x_stride, y, y_stride,
+                            tokens, last_token);
+}
+
+int frz_op_gemv_format(frz_device* dev, int format, const void* codes, const void* scales,
+                       int rows, int cols, const float* x, int x_stride, float* y, int y_stride,
+                       uint32_t tokens, int last_token) {
   if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
     return fail(FRZ_ERR_ARGUMENT, "frz_op_gemv: bad shape or tokens");
   }
+  if (format != kQ4_0 && format != kQ4_1 && format != kQ8_0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gemv: format " + std::to_string(format));
+  }
   if (int rc = device_put_step(dev, host_step(0, tokens))) return rc;
   return device_finish(dev,
-                       launch_gemv(dev->stream, dev->step, q4(codes, scales, rows, cols), x,
-                                   x_stride, y, y_stride, (int)tokens, last_token != 0),
+                       launch_gemv(dev->stream, dev->step, q4(codes, scales, rows, cols, format),
+                                   x, x_stride, y, y_stride, (int)tokens, last_token != 0),
                        "frz_op_gemv");
 }
 
@@ -321,16 +344,27 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
 
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales, int rows, int cols,
                   const uint32_t* ids, uint32_t tokens, float scale, float* hidden) {
+  return frz_op_gather_format(dev, kQ4_0, codes, scales, rows, cols, ids, tokens, scale, hidden);
+}
+
+int frz_op_gather_format(frz_device* dev, int format, const void* codes, const void* scales,
+                         int rows, int cols, const uint32_t* ids, uint32_t tokens, float scale,
+                         float* hidden) {
   if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
     return fail(FRZ_ERR_ARGUMENT, "frz_op_gather: bad shape or tokens");
+  }
+  if (format != kQ4_0 && format != kQ8_0) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gather: format " + std::to_string(format) +
+                                      " (Q4_0 2 or Q8_0 8)");
   }
   DevStep s = host_step(0, tokens);
   std::memcpy(s.ids, ids, tokens * sizeof(uint32_t));
   if (int rc = device_put_step(dev, s)) return rc;
-  return device_finish(dev,
-                       launch_gather(dev->stream, dev->step, q4(codes, scales, rows, cols),
-                                     nullptr, hidden, scale, (int)tokens),
-                       "frz_op_gather");
+  return device_finish(
+      dev,
+      launch_gather(dev->stream, dev->step, q4(codes, scales, rows, cols, format), nullptr,
+                    hidden, scale, (int)tokens),
+      "frz_op_gather");
 }
 
 int frz_op_edit(frz_device* dev, const uint32_t* edits_dev, int layer, float* act, int width,

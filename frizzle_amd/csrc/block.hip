@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
 
 // ---- gather (gather.wgsl:25-48) ---------------------------------------------
 __global__ __launch_bounds__(256) void gather_kernel(const DevStep* __restrict__ step,
-                                                     Q4Matrix table,
+                                                     QMatrix table,
                                                      const uint32_t* __restrict__ sampled,
                                                      float* __restrict__ hidden, float scale) {
   const int row = blockIdx.x;
@@ -174,13 +174,23 @@ __global__ __launch_bounds__(256) void gather_kernel(const DevStep* __restrict__
   const uint32_t token = step->fed ? sampled[0] : step->ids[row];
   if (token >= (uint32_t)table.rows) return;
   const int groups = table.cols / 32;
+  // A Q8_0 table (the file's embedding) holds weight j of a block as the
+  // signed byte j times d (q8_0.wgsl:10-21); a Q4_0 one as nibble (q - 8) d.
+  // Either product is exact, so the one rounding is that of the scale.
+  const bool bytes = table.format == kQ8_0;
   for (int i = threadIdx.x; i < table.cols; i += blockDim.x) {
     const size_t blk = (size_t)token * groups + i / 32;
     const int j = i % 32;
-    const uint8_t byte = table.codes[blk * 16 + (j & 15)];
-    const uint32_t q = j < 16 ? (byte & 0xFu) : (uint32_t)(byte >> 4);
     const float d = (float)__builtin_bit_cast(_Float16, table.scales[blk]);
-    hidden[(size_t)row * table.cols + i] = fmaf_((float)q, d, -8.0f * d) * scale;
+    float wv;
+    if (bytes) {
+      wv = (float)(int8_t)table.codes[blk * 32 + j] * d;
+    } else {
+      const uint8_t byte = table.codes[blk * 16 + (j & 15)];
+      const uint32_t q = j < 16 ? (byte & 0xFu) : (uint32_t)(byte >> 4);
+      wv = fmaf_((float)q, d, -8.0f * d);
+    }
+    hidden[(size_t)row * table.cols + i] = wv * scale;
   }
 }
 
@@ -224,9 +234,10 @@ hipError_t launch_rope(hipStream_t s, const DevStep* step, const RopeArgs& a,
   return hipGetLastError();
 }
 
-hipError_t launch_gather(hipStream_t s, const DevStep* step, Q4Matrix table,
+hipError_t launch_gather(hipStream_t s, const DevStep* step, QMatrix table,
                          const uint32_t* sampled, float* hidden, float scale,
                          int max_tokens) {
+  if (table.format != kQ4_0 && table.format != kQ8_0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gather_kernel, dim3(max_tokens), dim3(256), 0, s, step, table, sampled,
                      hidden, scale);
   return hipGetLastError();

@@ -76,8 +76,8 @@ bool is_global(const frz_model_config& c, int layer) {
 }
 
 struct Layer {
-  Q4Matrix qkv;  // Q rows, then K, then V (one product, matmul.h:27-33)
-  Q4Matrix o, gate, up, down;
+  QMatrix qkv;  // Q rows, then K, then V (one product, matmul.h:27-33)
+  QMatrix o, gate, up, down;
   float* gains[6];  // attn, q, k, post_attn, ffn, post_ffn
   uint16_t* kcache;
   uint16_t* vcache;
@@ -94,7 +94,7 @@ struct frz_model {
   frz_model_config c{};
   std::vector<void*> owned;
   std::vector<Layer> layers;
-  Q4Matrix embedding{};
+  QMatrix embedding{};
   float* output_norm = nullptr;
   // working buffers, a prefill block of rows each
   float *hidden = nullptr, *hidden_b = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr,
@@ -128,29 +128,70 @@ int alloc(frz_model* m, T** p, size_t bytes) {
   return FRZ_OK;
 }
 
-int alloc_q4(frz_model* m, Q4Matrix* w, int rows, int cols) {
+int alloc_q4(frz_model* m, QMatrix* w, int rows, int cols, int format = kQ4_0) {
   const size_t blocks = (size_t)rows * cols / 32;
   uint8_t* codes;
   uint16_t* scales;
-  if (int rc = alloc(m, &codes, blocks * 16)) return rc;
-  if (int rc = alloc(m, &scales, blocks * 2)) return rc;
-  *w = Q4Matrix{codes, scales, rows, cols};
+  if (int rc = alloc(m, &codes, blocks * code_bytes(format))) return rc;
+  if (int rc = alloc(m, &scales, blocks * 2 * scale_halves(format))) return rc;
+  *w = QMatrix{codes, scales, rows, cols, format};
   return FRZ_OK;
 }
 
-// Writes GGUF Q4_0 blocks into rows [row0, row0 + rows) of a device matrix.
-int upload_q4(frz_model* m, const Q4Matrix& w, int row0, int rows, const void* data) {
+// Frees one of the model's allocations.
+void release(frz_model* m, const void* p) {
+  auto it = std::find(m->owned.begin(), m->owned.end(), const_cast<void*>(p));
+  if (it == m->owned.end()) return;
+  hipFree(*it);
+  m->owned.erase(it);
+}
+
+// The caches no longer hold what the prompt-reuse record says: weights
+// changed, or a step the record does not track wrote them.
+void forget_prefix(frz_model* m) {
+  m->cached.clear();
+  m->cached_edits.clear();
+}
+
+// A matrix in `format`: the same one when it already is, else new buffers
+// (the old ones freed once the new exist, so a failure leaves the matrix as
+// it was; a captured decode graph holds the old addresses, so it is dropped
+// and captured again at the next decode).
+int reformat(frz_model* m, QMatrix* w, int format) {
+  if (w->format == format) return FRZ_OK;
+  if (int rc = check_hip(hipDeviceSynchronize(), "reformat sync")) return rc;
+  QMatrix fresh;
+  if (int rc = alloc_q4(m, &fresh, w->rows, w->cols, format)) return rc;
+  release(m, w->codes);
+  release(m, w->scales);
+  *w = fresh;
+  if (m->decode_exec) {
+    hipGraphExecDestroy(m->decode_exec);
+    m->decode_exec = nullptr;
+  }
+  if (m->decode_graph) {
+    hipGraphDestroy(m->decode_graph);
+    m->decode_graph = nullptr;
+  }
+  return FRZ_OK;
+}
+
+// Writes GGUF blocks of the matrix's format into rows [row0, row0 + rows):
+// each block's scale halves to the scale stream, its codes to the code
+// stream.
+int upload_q4(frz_model* m, const QMatrix& w, int row0, int rows, const void* data) {
   const size_t blocks = (size_t)rows * w.cols / 32;
   const size_t first = (size_t)row0 * w.cols / 32;
-  std::vector<uint8_t> codes(blocks * 16), scales(blocks * 2);
-  frz_q4_0_split(data, blocks, codes.data(), scales.data());
+  const int cb = code_bytes(w.format), sh = scale_halves(w.format);
+  std::vector<uint8_t> codes(blocks * cb), scales(blocks * 2 * sh);
+  if (int rc = frz_block_split(w.format, data, blocks, codes.data(), scales.data())) return rc;
   hipStream_t s = m->dev->stream;
-  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint8_t*>(w.codes) + first * 16, codes.data(),
+  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint8_t*>(w.codes) + first * cb, codes.data(),
                                         codes.size(), hipMemcpyHostToDevice, s),
                          "upload codes"))
     return rc;
-  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint16_t*>(w.scales) + first, scales.data(),
-                                        scales.size(), hipMemcpyHostToDevice, s),
+  if (int rc = check_hip(hipMemcpyAsync(const_cast<uint16_t*>(w.scales) + first * sh,
+                                        scales.data(), scales.size(), hipMemcpyHostToDevice, s),
                          "upload scales"))
     return rc;
   return check_hip(hipStreamSynchronize(s), "upload sync");
@@ -551,18 +592,42 @@ void frz_model_destroy(frz_model* m) {
 }
 
 int frz_model_set_tensor(frz_model* m, int layer, int role, const void* data, uint64_t bytes) {
+  return frz_model_set_tensor_format(m, layer, role, is_matrix(role) ? kQ4_0 : 0, data, bytes);
+}
+
+int frz_model_set_tensor_format(frz_model* m, int layer, int role, int format, const void* data,
+                                uint64_t bytes) {
   if (!m || !data) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: null argument");
+  forget_prefix(m);
   const frz_model_config& c = m->c;
-  if (bytes != frz_tensor_bytes(&c, role) || bytes == 0) {
+  if (role < 0 || role > FRZ_ROLE_OUTPUT_NORM) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: role");
+  const bool ok_format = !is_matrix(role)          ? format == 0
+                         : role == FRZ_ROLE_DOWN   ? (format == kQ4_0 || format == kQ4_1 || format == kQ8_0)
+                         : role == FRZ_ROLE_EMBEDDING ? (format == kQ4_0 || format == kQ8_0)
+                                                      : format == kQ4_0;
+  if (!ok_format) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: format " + std::to_string(format) +
+                                      " is not run for this role (matrices Q4_0 (2); down also "
+                                      "Q4_1 (3) or Q8_0 (8); the embedding also Q8_0)");
+  }
+  const uint64_t want = is_matrix(role) ? frz_tensor_bytes(&c, role) / 18 * gguf_block_bytes(format)
+                                        : frz_tensor_bytes(&c, role);
+  if (bytes != want || bytes == 0) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: wrong size for the role");
   }
   if (role == FRZ_ROLE_EMBEDDING || role == FRZ_ROLE_OUTPUT_NORM) {
     if (layer != -1) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: global tensor, layer -1");
-    if (role == FRZ_ROLE_EMBEDDING) return upload_q4(m, m->embedding, 0, c.vocab, data);
+    if (role == FRZ_ROLE_EMBEDDING) {
+      if (int rc = reformat(m, &m->embedding, format)) return rc;
+      return upload_q4(m, m->embedding, 0, c.vocab, data);
+    }
     return check_hip(hipMemcpy(m->output_norm, data, bytes, hipMemcpyHostToDevice), "upload");
   }
   if (layer < 0 || layer >= c.layers) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: layer");
   Layer& L = m->layers[layer];
+  if (role == FRZ_ROLE_DOWN) {
+    if (int rc = reformat(m, &L.down, format)) return rc;
+  }
   const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
   switch (role) {
     case FRZ_ROLE_Q: return upload_q4(m, L.qkv, 0, qw, data);
@@ -639,8 +704,25 @@ int frz_model_set_edits(frz_model* m, const uint32_t* table, uint32_t words) {
   return check_hip(hipStreamSynchronize(m->dev->stream), "edit table sync");
 }
 
+static int model_step(frz_model* m, uint32_t position, uint32_t tokens, const uint32_t* ids,
+               int logits, const frz_sampling* sampling);
+static int model_decode(frz_model* m, uint32_t position, uint32_t steps, const frz_sampling* sampling,
+                 uint32_t* tokens_out, uint32_t* failed_out);
+
 int frz_model_step(frz_model* m, uint32_t position, uint32_t tokens, const uint32_t* ids,
                    int logits, const frz_sampling* sampling) {
+  if (m) forget_prefix(m);
+  return model_step(m, position, tokens, ids, logits, sampling);
+}
+
+int frz_model_decode(frz_model* m, uint32_t position, uint32_t steps,
+                     const frz_sampling* sampling, uint32_t* tokens_out, uint32_t* failed_out) {
+  if (m) forget_prefix(m);
+  return model_decode(m, position, steps, sampling, tokens_out, failed_out);
+}
+
+static int model_step(frz_model* m, uint32_t position, uint32_t tokens, const uint32_t* ids,
+               int logits, const frz_sampling* sampling) {
   if (!m || !ids || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_step: 1 to 512 tokens");
   }
@@ -666,8 +748,8 @@ int frz_model_step(frz_model* m, uint32_t position, uint32_t tokens, const uint3
   return enqueue_step(m, (int)tokens, logits != 0);
 }
 
-int frz_model_decode(frz_model* m, uint32_t position, uint32_t steps,
-                     const frz_sampling* sampling, uint32_t* tokens_out, uint32_t* failed_out) {
+static int model_decode(frz_model* m, uint32_t position, uint32_t steps, const frz_sampling* sampling,
+                 uint32_t* tokens_out, uint32_t* failed_out) {
   if (!m || !tokens_out) return fail(FRZ_ERR_ARGUMENT, "frz_model_decode: null argument");
   if (steps == 0) return FRZ_OK;
   if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
@@ -801,7 +883,7 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   while (pos < prompt_len) {
     const uint32_t n = std::min<uint32_t>(kPrefillBlock, prompt_len - pos);
     const bool last = pos + n == prompt_len;
-    if (int rc = frz_model_step(m, pos, n, prompt + pos, last ? 1 : 0, sampling)) return rc;
+    if (int rc = model_step(m, pos, n, prompt + pos, last ? 1 : 0, sampling)) return rc;
     pos += n;
   }
   m->cached.assign(prompt, prompt + prompt_len);
@@ -814,7 +896,7 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   bool stopped = record[1] != 0 || std::find(stop_ids, stop_ids + stops, record[0]) != stop_ids + stops;
   if (!stopped && max_tokens > 1) {
     std::vector<uint32_t> more(max_tokens - 1), failed(max_tokens - 1);
-    if (int rc = frz_model_decode(m, prompt_len, max_tokens - 1, sampling, more.data(),
+    if (int rc = model_decode(m, prompt_len, max_tokens - 1, sampling, more.data(),
                                   failed.data()))
       return rc;
     m->written_end = (uint64_t)prompt_len + max_tokens - 1;

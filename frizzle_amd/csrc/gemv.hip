@@ -145,6 +145,53 @@ __device__ __forceinline__ void decode_half(uint4 c, uint16_t dbits, float (&wk)
   }
 }
 
+// Q4_1, half H: (q - 0) d + m (q4_1.wgsl:12-25); the nibble placed as for
+// Q4_0 gives q d exactly, fma(1024 + q, d, -1024 d) or
+// fma(1024 + 16 q, d / 16, -64 d), and adding m is the one rounding.
+template <int H>
+__device__ __forceinline__ void decode_half_q4_1(uint4 c, uint32_t dm, float (&wk)[16]) {
+  const float d = half_to_float((uint16_t)(dm & 0xFFFFu));
+  const float m = half_to_float((uint16_t)(dm >> 16));
+  const float scale = H == 0 ? d : 0.0625f * d;
+  const float bias = H == 0 ? -1024.0f * d : -64.0f * d;
+  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+  constexpr uint32_t kMask = H == 0 ? 0x000F000Fu : 0x00F000F0u;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const half2v e = __builtin_bit_cast(half2v, (words[w] & kMask) | (kExp & ~kMask));
+    const half2v o = __builtin_bit_cast(half2v, ((words[w] >> 8) & kMask) | (kExp & ~kMask));
+    wk[4 * w + 0] = __builtin_fmaf((float)e.x, scale, bias) + m;
+    wk[4 * w + 1] = __builtin_fmaf((float)o.x, scale, bias) + m;
+    wk[4 * w + 2] = __builtin_fmaf((float)e.y, scale, bias) + m;
+    wk[4 * w + 3] = __builtin_fmaf((float)o.y, scale, bias) + m;
+  }
+}
+
+// Q8_0, half H: weights 16 H .. 16 H + 15 are code bytes 16 H .. 16 H + 15
+// (c holds them), each qs d (q8_0.wgsl:10-21). A code flipped to
+// u = qs + 128 sits under the exponent of 1024 as 1024 + u, and
+// fma(1024 + u, d, -1152 d) = qs d exactly.
+__device__ __forceinline__ void decode_half_q8_0(uint4 c, uint16_t dbits, float (&wk)[16]) {
+  const float d = half_to_float(dbits);
+  const float bias = -1152.0f * d;
+  const uint32_t words[4] = {c.x ^ 0x80808080u, c.y ^ 0x80808080u, c.z ^ 0x80808080u,
+                             c.w ^ 0x80808080u};
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+  constexpr uint32_t kMask = 0x00FF00FFu;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const half2v e = __builtin_bit_cast(half2v, (words[w] & kMask) | (kExp & ~kMask));
+    const half2v o = __builtin_bit_cast(half2v, ((words[w] >> 8) & kMask) | (kExp & ~kMask));
+    wk[4 * w + 0] = __builtin_fmaf((float)e.x, d, bias);
+    wk[4 * w + 1] = __builtin_fmaf((float)o.x, d, bias);
+    wk[4 * w + 2] = __builtin_fmaf((float)e.y, d, bias);
+    wk[4 * w + 3] = __builtin_fmaf((float)o.y, d, bias);
+  }
+}
+
 // Orders a wave's LDS accesses around it (a wave's LDS instructions execute
 // in program order; this keeps the compiler from moving them).
 __device__ __forceinline__ void wave_sync() {
@@ -244,15 +291,27 @@ __device__ __forceinline__ void stage_inputs(const Tile<NB, GATED>& T, const Ste
   for (int i = 0; i < 8; ++i) T.x_put[8 * kXLine * i] = G[i];
 }
 
-template <bool GATED>
+// A lane's weights for a step: one group of each matrix. A gated product's
+// matrices are Q4_0; a plain one's may be Q4_1 or Q8_0 as well.
+template <bool GATED, int F>
 struct Weights {
   uint4 c[GATED ? 2 : 1];
   uint16_t d[GATED ? 2 : 1];
 };
+template <>
+struct Weights<false, kQ8_0> {
+  uint4 c[2];  // code bytes 0..15, 16..31
+  uint16_t d[1];
+};
+template <>
+struct Weights<false, kQ4_1> {
+  uint4 c[1];
+  uint32_t d[1];  // d, then m in the high half
+};
 
-template <int NB, bool GATED>
+template <int NB, bool GATED, int F>
 __device__ __forceinline__ void load_weights(const Tile<NB, GATED>& T, const StepInfo<NB>& I,
-                                             Weights<GATED>& W) {
+                                             Weights<GATED, F>& W) {
   // this lane's block's group
   uint32_t g = I.entry(0);
 #pragma unroll
@@ -260,21 +319,39 @@ __device__ __forceinline__ void load_weights(const Tile<NB, GATED>& T, const Ste
   const uint32_t blk = T.row_group0 + (g & 0x7FFFu);
 #pragma unroll
   for (int m = 0; m < Tile<NB, GATED>::kMats; ++m) {
-    W.c[m] = __builtin_bit_cast(uint4,
-                                __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 16 * blk, 0, 0));
-    W.d[m] = __builtin_amdgcn_raw_buffer_load_b16(T.scales[m], 2 * blk, 0, 0);
+    if constexpr (F == kQ8_0) {
+      W.c[0] = __builtin_bit_cast(uint4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 32 * blk, 0, 0));
+      W.c[1] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 32 * blk + 16, 0, 0));
+      W.d[0] = __builtin_amdgcn_raw_buffer_load_b16(T.scales[m], 2 * blk, 0, 0);
+    } else if constexpr (F == kQ4_1) {
+      W.c[0] = __builtin_bit_cast(uint4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 16 * blk, 0, 0));
+      W.d[0] = __builtin_amdgcn_raw_buffer_load_b32(T.scales[m], 4 * blk, 0, 0);
+    } else {
+      W.c[m] = __builtin_bit_cast(uint4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(T.codes[m], 16 * blk, 0, 0));
+      W.d[m] = __builtin_amdgcn_raw_buffer_load_b16(T.scales[m], 2 * blk, 0, 0);
+    }
   }
 }
 
 // Products for k = 16 H .. 16 H + 15 of a step, per matrix: decode the
 // weights, then the 16 products per block.
-template <int NB, bool GATED, int H>
-__device__ __forceinline__ void chain_half(const float4 (&xv)[8], const Weights<GATED>& W,
+template <int NB, bool GATED, int F, int H>
+__device__ __forceinline__ void chain_half(const float4 (&xv)[8], const Weights<GATED, F>& W,
                                            typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
 #pragma unroll
   for (int m = 0; m < (GATED ? 2 : 1); ++m) {
     float wk[16];
-    decode_half<H>(W.c[m], W.d[m], wk);
+    if constexpr (F == kQ8_0) {
+      decode_half_q8_0(W.c[H], W.d[0], wk);
+    } else if constexpr (F == kQ4_1) {
+      decode_half_q4_1<H>(W.c[0], W.d[0], wk);
+    } else {
+      decode_half<H>(W.c[m], W.d[m], wk);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -294,10 +371,10 @@ __device__ __forceinline__ void chain_half(const float4 (&xv)[8], const Weights<
 // chain this step's 32 products per block, half a group at a time so that
 // the decoded weights need few registers. Vector instructions do not run
 // beside the fp32 matrix instructions, so each kind is kept in runs.
-template <int NB, bool GATED>
+template <int NB, bool GATED, int F>
 __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepInfo<NB>& I1,
                                            const StepInfo<NB>& I2, float4 (&G)[8],
-                                           const Weights<GATED>& W, Weights<GATED>& W_next,
+                                           const Weights<GATED, F>& W, Weights<GATED, F>& W_next,
                                            typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1]) {
   float4 xv[8];
 #pragma unroll
@@ -308,8 +385,8 @@ __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepI
   load_weights(T, I1, W_next);
   // The loads stay here, a step ahead of their use.
   __builtin_amdgcn_sched_barrier(0);
-  chain_half<NB, GATED, 0>(xv, W, acc);
-  chain_half<NB, GATED, 1>(xv, W, acc);
+  chain_half<NB, GATED, F, 0>(xv, W, acc);
+  chain_half<NB, GATED, F, 1>(xv, W, acc);
   wave_sync();
 }
 
@@ -329,14 +406,14 @@ __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
 
 // Step t, with the schedule of steps t .. t + 2 in hand; starts reading
 // step t + 3's (first used a step later, so its wait costs nothing).
-template <int NB, bool GATED>
+template <int NB, bool GATED, int F>
 __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedule<NB>& S, int t,
                                          StepInfo<NB> (&I)[4], float4 (&G)[8],
-                                         const Weights<GATED>& W, Weights<GATED>& W_next,
+                                         const Weights<GATED, F>& W, Weights<GATED, F>& W_next,
                                          typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
                                          float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
   I[3] = step_info(S, t + 3);
-  chain_step<NB, GATED>(T, I[1], I[2], G, W, W_next, acc);
+  chain_step<NB, GATED, F>(T, I[1], I[2], G, W, W_next, acc);
   if (I[0].flags & kCloses) {
 #pragma unroll
     for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
@@ -348,9 +425,9 @@ __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedul
 
 // Grid: x = D-row tiles, y = groups of kTileWaves x D tokens. Rows and
 // tokens past the ends are read clamped and not stored.
-template <int NB, bool GATED>
+template <int NB, bool GATED, int F = kQ4_0>
 __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
-    const DevStep* __restrict__ step, Q4Matrix w, Q4Matrix up,
+    const DevStep* __restrict__ step, QMatrix w, QMatrix up,
     const float* __restrict__ x, int x_stride, uint32_t x_bytes, float* __restrict__ y,
     int y_stride, const uint32_t* __restrict__ edits, int layer, const Schedule<NB> S) {
   using M = Mfma<NB>;
@@ -369,8 +446,8 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   const int row = min((int)blockIdx.x * D + lane % D, w.rows - 1);
   const uint32_t blocks = (uint32_t)w.rows * (uint32_t)groups;
   T.row_group0 = (uint32_t)row * (uint32_t)groups;
-  T.codes[0] = buffer_of(w.codes, 16 * blocks);
-  T.scales[0] = buffer_of(w.scales, 2 * blocks);
+  T.codes[0] = buffer_of(w.codes, (uint32_t)code_bytes(F) * blocks);
+  T.scales[0] = buffer_of(w.scales, 2u * (uint32_t)scale_halves(F) * blocks);
   if (GATED) {
     T.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
     T.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
@@ -404,13 +481,13 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   load_inputs(T, I[0], G);
   stage_inputs(T, I[0], G);
   load_inputs(T, I[1], G);
-  Weights<GATED> W0, W1;
+  Weights<GATED, F> W0, W1;
   load_weights(T, I[0], W0);
   wave_sync();
   for (int t = 0; t < S.steps; t += 2) {
-    run_step<NB, GATED>(T, S, t, I, G, W0, W1, acc, total);
+    run_step<NB, GATED, F>(T, S, t, I, G, W0, W1, acc, total);
     if (t + 1 >= S.steps) break;
-    run_step<NB, GATED>(T, S, t + 1, I, G, W1, W0, acc, total);
+    run_step<NB, GATED, F>(T, S, t + 1, I, G, W1, W0, acc, total);
   }
 
   const int tok = token0 + lane % D;
@@ -464,28 +541,28 @@ bool build_schedule(int groups, Schedule<NB>& S) {
   return t > 0;
 }
 
-template <int NB, bool GATED>
-hipError_t launch_ranges(hipStream_t s, const DevStep* step, Q4Matrix w, Q4Matrix up,
+template <int NB, bool GATED, int F = kQ4_0>
+hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
                          const float* x, int x_stride, float* y, int y_stride, int max_tokens,
                          const uint32_t* edits, int layer) {
   constexpr int D = Mfma<NB>::kDim;
   const int groups = w.cols >> 5;
   const uint64_t x_bytes = 4ull * (uint64_t)x_stride * (uint64_t)max_tokens;
-  const uint64_t code_bytes = 16ull * (uint64_t)w.rows * (uint64_t)groups;
+  const uint64_t codes = (uint64_t)code_bytes(F) * (uint64_t)w.rows * (uint64_t)groups;
   Schedule<NB> S;
-  if (groups >= 0x8000 || x_bytes >= (1ull << 31) || code_bytes >= (1ull << 31) ||
+  if (groups >= 0x8000 || x_bytes >= (1ull << 31) || codes >= (1ull << 31) ||
       !build_schedule<NB>(groups, S)) {
     return hipErrorInvalidValue;
   }
   const dim3 grid((w.rows + D - 1) / D, (max_tokens + kTileWaves * D - 1) / (kTileWaves * D));
-  hipLaunchKernelGGL((gemm_ranges<NB, GATED>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
+  hipLaunchKernelGGL((gemm_ranges<NB, GATED, F>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
                      x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, S);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
+hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token) {
   if (w.cols % 32 != 0 || w.rows <= 0) return hipErrorInvalidValue;
@@ -497,16 +574,36 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
   // Tiles of 32 x 32 (two ranges in flight) when they are enough to cover
   // most of the chip's 1,024 SIMDs; else 16 x 16 tiles (four ranges), four
   // times as many.
-  if ((size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024) {
-    return launch_ranges<2, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens, nullptr, 0);
+  const bool wide = (size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024;
+  switch (w.format) {
+    case kQ4_0:
+      if (wide)
+        return launch_ranges<2, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                       nullptr, 0);
+      return launch_ranges<4, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens, nullptr,
+                                     0);
+    case kQ4_1:
+      if (wide)
+        return launch_ranges<2, false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride,
+                                              max_tokens, nullptr, 0);
+      return launch_ranges<4, false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                            nullptr, 0);
+    case kQ8_0:
+      if (wide)
+        return launch_ranges<2, false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                              max_tokens, nullptr, 0);
+      return launch_ranges<4, false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                            nullptr, 0);
+    default:
+      return hipErrorInvalidValue;
   }
-  return launch_ranges<4, false>(s, step, w, w, x, x_stride, y, y_stride, max_tokens, nullptr, 0);
 }
 
-hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
-                        Q4Matrix up, const float* x, float* act,
+hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
+                        QMatrix up, const float* x, float* act,
                         int max_tokens, const uint32_t* edits, int layer) {
-  if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols)
+  if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
+      gate.format != kQ4_0 || up.format != kQ4_0)
     return hipErrorInvalidValue;
   if (max_tokens <= 1) {
     GemvInput in{};

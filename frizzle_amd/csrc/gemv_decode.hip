@@ -97,6 +97,60 @@ __device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits,
   return acc;
 }
 
+// Q8_0: weight k = qs[k] d (q8_0.wgsl:12-24), qs signed. A code flipped to
+// u = qs + 128 sits under the exponent of f16 1024 as 1024 + u, and
+// fma(1024 + u, d, -1152 d) = (u - 128) d = qs d, exact (19 bits at most).
+__device__ __forceinline__ float chain_group_q8_0(float acc, uint4 c0, uint4 c1, uint16_t dbits,
+                                                  const float* xg) {
+  const _Float16 dh = __builtin_bit_cast(_Float16, dbits);
+  const float bias = -1152.0f * (float)dh;
+  const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  constexpr uint32_t kMask = 0x00FF00FFu;
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const float4 x = *reinterpret_cast<const float4*>(xg + 4 * w);
+    const uint32_t s = words[w] ^ 0x80808080u;
+    // a: bytes 0 and 2 of the word; b: bytes 1 and 3.
+    const half2v a = __builtin_bit_cast(half2v, (s & kMask) | (kExp & ~kMask));
+    const half2v b = __builtin_bit_cast(half2v, ((s >> 8) & kMask) | (kExp & ~kMask));
+    acc = fmaf_(__builtin_fmaf((float)a.x, (float)dh, bias), x.x, acc);
+    acc = fmaf_(__builtin_fmaf((float)b.x, (float)dh, bias), x.y, acc);
+    acc = fmaf_(__builtin_fmaf((float)a.y, (float)dh, bias), x.z, acc);
+    acc = fmaf_(__builtin_fmaf((float)b.y, (float)dh, bias), x.w, acc);
+  }
+  return acc;
+}
+
+// Q4_1: weight = q d + m (q4_1.wgsl:12-25). fma(1024 + q, d, -1024 d) = q d
+// exactly; the one rounding is that of adding m, as in the reference.
+__device__ __forceinline__ float chain_group_q4_1(float acc, uint4 c, uint32_t dm,
+                                                  const float* xg) {
+  const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(dm & 0xFFFFu));
+  const float m = (float)__builtin_bit_cast(_Float16, (uint16_t)(dm >> 16));
+  const float bias = -1024.0f * (float)dh;
+  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+  constexpr uint32_t kMask = 0x000F000Fu;
+  uint32_t kExp;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float4 x = *reinterpret_cast<const float4*>(xg + 16 * hi + 4 * w);
+      const uint32_t s = words[w] >> (4 * hi);
+      const half2v a = __builtin_bit_cast(half2v, (s & kMask) | (kExp & ~kMask));
+      const half2v b = __builtin_bit_cast(half2v, ((s >> 8) & kMask) | (kExp & ~kMask));
+      acc = fmaf_(__builtin_fmaf((float)a.x, (float)dh, bias) + m, x.x, acc);
+      acc = fmaf_(__builtin_fmaf((float)b.x, (float)dh, bias) + m, x.y, acc);
+      acc = fmaf_(__builtin_fmaf((float)a.y, (float)dh, bias) + m, x.z, acc);
+      acc = fmaf_(__builtin_fmaf((float)b.y, (float)dh, bias) + m, x.w, acc);
+    }
+  }
+  return acc;
+}
+
 // ---- the input row ------------------------------------------------------------
 // T threads (128 to 1,024). With N = min(T, 256) norm threads, norm lane
 // t + k N (k < 256 / N) belongs to thread t and holds vec4s lane and
@@ -225,9 +279,11 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
       P.y[s] = ld4(in.output + 4 * q);
       P.pg[s] = ld4(in.post_gain + 4 * q);
     } else {
+      // vec4 q is weights 4 (q % 8) .. + 3 of group q / 8: in Q4_0 nibbles of
+      // word (q % 4) of the block's codes, in Q8_0 bytes of word q % 8.
       const size_t blk = (size_t)token * groups + (q >> 3);
-      const int j = (4 * q) & 31;
-      P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[blk * 4 + ((j & 15) >> 2)];
+      const size_t word = in.table.format == kQ8_0 ? blk * 8 + (q & 7) : blk * 4 + (q & 3);
+      P.word[s] = reinterpret_cast<const uint32_t*>(in.table.codes)[word];
       P.d[s] = in.table.scales[blk];
     }
     P.g[s] = ld4(in.gain + 4 * q);
@@ -345,10 +401,18 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
         const int shift = ((4 * q) & 31) < 16 ? 0 : 4;
         const float d = half_to_float(P.d[s]);
         float e[4];
+        if (in.table.format == kQ8_0) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const float code = (float)((P.word[s] >> (8 * b + shift)) & 0xFu);
-          e[b] = fmaf_(code, d, -8.0f * d) * in.scale;
+          for (int b = 0; b < 4; ++b) {
+            const float code = (float)(int8_t)(P.word[s] >> (8 * b));
+            e[b] = (code * d) * in.scale;
+          }
+        } else {
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const float code = (float)((P.word[s] >> (8 * b + shift)) & 0xFu);
+            e[b] = fmaf_(code, d, -8.0f * d) * in.scale;
+          }
         }
         P.v[s] = make_float4(e[0], e[1], e[2], e[3]);
       }
@@ -428,32 +492,51 @@ __device__ __forceinline__ void lane_plan(LanePlan<RH, MAXI>& P, int groups, int
   }
 }
 
-template <int MAXI>
+template <int MAXI, int F = kQ4_0>
 struct LaneWeights {
   uint4 codes[MAXI];
   uint16_t scale[MAXI];
+};
+template <int MAXI>
+struct LaneWeights<MAXI, kQ8_0> {
+  uint4 codes[2 * MAXI];
+  uint16_t scale[MAXI];
+};
+template <int MAXI>
+struct LaneWeights<MAXI, kQ4_1> {
+  uint4 codes[MAXI];
+  uint32_t scale[MAXI];  // d, then m in the high half
 };
 
 // Item it's block: row row0 + jrow of m (write products). Loaded
 // unconditionally (block 0 for no item or a row past the end, whose sums are
 // never written).
-template <int RH, int MAXI>
-__device__ __forceinline__ void load_rows(LaneWeights<MAXI>& W, const LanePlan<RH, MAXI>& P,
-                                          const Q4Matrix& m, int row0) {
+template <int RH, int MAXI, int F = kQ4_0>
+__device__ __forceinline__ void load_rows(LaneWeights<MAXI, F>& W, const LanePlan<RH, MAXI>& P,
+                                          const QMatrix& m, int row0) {
   const int groups = m.cols >> 5;
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
     const int row = row0 + P.jrow[it];
     const int blk = P.off[it] >= 0 && row < m.rows ? row * groups + P.off[it] : 0;
-    W.codes[it] = reinterpret_cast<const uint4*>(m.codes)[blk];
-    W.scale[it] = m.scales[blk];
+    if constexpr (F == kQ8_0) {
+      W.codes[2 * it] = reinterpret_cast<const uint4*>(m.codes)[2 * blk];
+      W.codes[2 * it + 1] = reinterpret_cast<const uint4*>(m.codes)[2 * blk + 1];
+      W.scale[it] = m.scales[blk];
+    } else if constexpr (F == kQ4_1) {
+      W.codes[it] = reinterpret_cast<const uint4*>(m.codes)[blk];
+      W.scale[it] = reinterpret_cast<const uint32_t*>(m.scales)[blk];
+    } else {
+      W.codes[it] = reinterpret_cast<const uint4*>(m.codes)[blk];
+      W.scale[it] = m.scales[blk];
+    }
   }
 }
 
 // Item it's block: row n of gate (jrow 0) or up (jrow 1).
 template <int MAXI>
 __device__ __forceinline__ void load_neuron(LaneWeights<MAXI>& W, const LanePlan<2, MAXI>& P,
-                                            const Q4Matrix& gate, const Q4Matrix& up, int n) {
+                                            const QMatrix& gate, const QMatrix& up, int n) {
   const int groups = gate.cols >> 5;
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
@@ -466,9 +549,10 @@ __device__ __forceinline__ void load_neuron(LaneWeights<MAXI>& W, const LanePlan
 }
 
 // The lane's chains; each range's sum goes to its parts entry.
-template <int RH, int MAXI>
-__device__ __forceinline__ void lane_chains(const LaneWeights<MAXI>& W, const LanePlan<RH, MAXI>& P,
-                                            const float* xs, float* parts) {
+template <int RH, int MAXI, int F = kQ4_0>
+__device__ __forceinline__ void lane_chains(const LaneWeights<MAXI, F>& W,
+                                            const LanePlan<RH, MAXI>& P, const float* xs,
+                                            float* parts) {
 #pragma unroll
   for (int j = 0; j < RH; ++j) {
     if (P.empty_dest[j] >= 0) parts[P.empty_dest[j]] = 0.0f;
@@ -477,7 +561,14 @@ __device__ __forceinline__ void lane_chains(const LaneWeights<MAXI>& W, const La
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
     if (P.xoff[it] >= 0) {
-      acc = chain_group(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
+      if constexpr (F == kQ8_0) {
+        acc = chain_group_q8_0(acc, W.codes[2 * it], W.codes[2 * it + 1], W.scale[it],
+                               xs + P.xoff[it]);
+      } else if constexpr (F == kQ4_1) {
+        acc = chain_group_q4_1(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
+      } else {
+        acc = chain_group(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
+      }
       if (P.dest[it] >= 0) {
         parts[P.dest[it]] = acc;
         acc = 0.0f;
@@ -534,9 +625,9 @@ constexpr int plain_vec4s() {
 // before it computes the one before. The tiles are unrolled into
 // straight-line code over two register buffers, so every wait is for the
 // oldest loads only.
-template <int RH, int MAXI, int MODE, int TPW, int WAVES>
+template <int RH, int MAXI, int MODE, int TPW, int WAVES, int F = kQ4_0>
 __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* __restrict__ step,
-                                                                Q4Matrix w, GemvInput in,
+                                                                QMatrix w, GemvInput in,
                                                                 float* __restrict__ y) {
   extern __shared__ __align__(16) float smem[];
   constexpr int T = 64 * WAVES;
@@ -554,14 +645,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* _
   lane_plan<RH, MAXI>(plan, w.cols >> 5, slot0, r);
   Prologue<T, X4> pro;
   prologue_load<MODE, T, X4>(pro, in, step, w.cols);
-  LaneWeights<MAXI> buf[2];
-  load_rows<RH, MAXI>(buf[0], plan, w, tile_of(0) * kRows + slot0);
+  LaneWeights<MAXI, F> buf[2];
+  load_rows<RH, MAXI, F>(buf[0], plan, w, tile_of(0) * kRows + slot0);
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < TPW; ++k) {
-    if (k + 1 < TPW) load_rows<RH, MAXI>(buf[(k + 1) & 1], plan, w, tile_of(k + 1) * kRows + slot0);
-    lane_chains<RH, MAXI>(buf[k & 1], plan, xs, parts);
+    if (k + 1 < TPW) load_rows<RH, MAXI, F>(buf[(k + 1) & 1], plan, w, tile_of(k + 1) * kRows + slot0);
+    lane_chains<RH, MAXI, F>(buf[k & 1], plan, xs, parts);
     wave_sync();
     if (r < RH) {
       const int row = tile_of(k) * kRows + slot0 + r;
@@ -575,7 +666,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* _
 // (rotated ranges), then gelu_tanh(gate) * up and the layer's pins.
 template <int MAXI, int MODE, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* __restrict__ step,
-                                                                Q4Matrix gate, Q4Matrix up,
+                                                                QMatrix gate, QMatrix up,
                                                                 GemvInput in, float* __restrict__ act,
                                                                 const uint32_t* __restrict__ edits,
                                                                 int layer) {
@@ -634,29 +725,29 @@ int max_items(int cols, int rh) {
 // its input row is staged once for all of them.
 constexpr int kHeadTilesPerGroup = 8;
 
-template <int RH, int MAXI, int MODE, int TPW, int WAVES>
-hipError_t launch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w, const GemvInput& in,
+template <int RH, int MAXI, int MODE, int TPW, int WAVES, int F = kQ4_0>
+hipError_t launch_write(hipStream_t s, const DevStep* step, const QMatrix& w, const GemvInput& in,
                         float* y) {
   constexpr int kRows = 2 * RH * WAVES;
   const size_t lds = (size_t)(kRows * kPartStride + kRedFloats + (w.cols / 32) * kXStride) * 4;
   const int tiles = (w.rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE, TPW, WAVES>), dim3((tiles + TPW - 1) / TPW),
-                     dim3(64 * WAVES), lds, s, step, w, in, y);
+  hipLaunchKernelGGL((gemv_write_kernel<RH, MAXI, MODE, TPW, WAVES, F>),
+                     dim3((tiles + TPW - 1) / TPW), dim3(64 * WAVES), lds, s, step, w, in, y);
   return hipGetLastError();
 }
 
-template <int MODE>
-hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+template <int MODE, int F = kQ4_0>
+hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
                           const GemvInput& in, float* y) {
   const int items1 = max_items(w.cols, 1);
   const int items2 = max_items(w.cols, 2);
   // Many rows: two rows a half-wave, ranges rotated, where that balances.
   if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536)
-    return launch_write<2, 3, MODE, kHeadTilesPerGroup, 2>(s, step, w, in, y);
-  if (items1 <= 1) return launch_write<1, 1, MODE, 1, 2>(s, step, w, in, y);
-  if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2>(s, step, w, in, y);
-  if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2>(s, step, w, in, y);
-  if (items1 <= 8) return launch_write<1, 8, MODE, 1, 2>(s, step, w, in, y);
+    return launch_write<2, 3, MODE, kHeadTilesPerGroup, 2, F>(s, step, w, in, y);
+  if (items1 <= 1) return launch_write<1, 1, MODE, 1, 2, F>(s, step, w, in, y);
+  if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2, F>(s, step, w, in, y);
+  if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2, F>(s, step, w, in, y);
+  if (items1 <= 8) return launch_write<1, 8, MODE, 1, 2, F>(s, step, w, in, y);
   return hipErrorInvalidValue;
 }
 
@@ -665,8 +756,8 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const Q4Matrix& w,
 constexpr int kGatedWaves = 4;
 
 template <int MAXI, int MODE, int kWaves = kGatedWaves>
-hipError_t launch_gated(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
-                        const Q4Matrix& up, const GemvInput& in, float* act,
+hipError_t launch_gated(hipStream_t s, const DevStep* step, const QMatrix& gate,
+                        const QMatrix& up, const GemvInput& in, float* act,
                         const uint32_t* edits, int layer) {
   constexpr int kNeurons = 2 * kWaves;
   const size_t lds =
@@ -679,13 +770,22 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, const Q4Matrix& gate
 
 }  // namespace
 
-hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix& w,
                               const GemvInput& in, int mode, float* y) {
   if (w.cols % 32 != 0 || w.rows <= 0 || w.cols > 8 * 1024 ||
       (long long)w.rows * (w.cols / 32) >= (1ll << 31)) {
     return hipErrorInvalidValue;
   }
   if (mode != 0 && w.cols > kNormMaxCols) return hipErrorInvalidValue;
+  if (mode == 2 && in.table.format != kQ4_0 && in.table.format != kQ8_0)
+    return hipErrorInvalidValue;
+  // Q4_1 and Q8_0 weights (a file's downs and tied head) take a plain row.
+  if (w.format != kQ4_0) {
+    if (mode != 0) return hipErrorInvalidValue;
+    if (w.format == kQ8_0) return dispatch_write<0, kQ8_0>(s, step, w, in, y);
+    if (w.format == kQ4_1) return dispatch_write<0, kQ4_1>(s, step, w, in, y);
+    return hipErrorInvalidValue;
+  }
   switch (mode) {
     case 0: return dispatch_write<0>(s, step, w, in, y);
     case 1: return dispatch_write<1>(s, step, w, in, y);
@@ -698,13 +798,13 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix
   }
 }
 
-hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
-                               const Q4Matrix& up, const GemvInput& in, int mode, float* act,
+hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix& gate,
+                               const QMatrix& up, const GemvInput& in, int mode, float* act,
                                const uint32_t* edits, int layer) {
   // Gate and up rows together: two rows' ranges, at most 4 items to K = 2,048.
   if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
       gate.cols > kNormMaxCols || (long long)gate.rows * (gate.cols / 32) >= (1ll << 31) ||
-      (mode != 0 && mode != 1)) {
+      (mode != 0 && mode != 1) || gate.format != kQ4_0 || up.format != kQ4_0) {
     return hipErrorInvalidValue;
   }
   const int items = max_items(gate.cols, 2);

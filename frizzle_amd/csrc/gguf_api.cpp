@@ -312,24 +312,37 @@ int frz_model_load_gguf(frz_model* model, const char* path) {
   auto load = [&](int layer, int role, const std::string& name) -> int {
     const Tensor* t = g.index.tensor(name);
     if (!t) return fail(FRZ_ERR_ARGUMENT, "missing tensor " + name);
-    const uint32_t want_type = is_matrix(role) ? 2u : 0u;  // Q4_0 or F32
-    if (t->type != want_type) {
-      const frz::gguf::Layout* l = frz::gguf::layout_of(t->type);
-      return fail(FRZ_ERR_ARGUMENT, name + ": format " + (l ? l->name : "?") +
-                                        " is not run here (matrices Q4_0, norms F32)");
+    // The formats the pinned file mixes (device_layout.h:64-66): Q4_0
+    // matrices, Q4_1 in the first downs, a Q8_0 embedding; F32 gains.
+    const uint32_t type = t->type;
+    const bool format_ok =
+        !is_matrix(role) ? type == FRZ_FORMAT_F32
+        : role == FRZ_ROLE_DOWN
+            ? type == FRZ_FORMAT_Q4_0 || type == FRZ_FORMAT_Q4_1 || type == FRZ_FORMAT_Q8_0
+        : role == FRZ_ROLE_EMBEDDING ? type == FRZ_FORMAT_Q4_0 || type == FRZ_FORMAT_Q8_0
+                                     : type == FRZ_FORMAT_Q4_0;
+    if (!format_ok) {
+      const frz::gguf::Layout* l = frz::gguf::layout_of(type);
+      return fail(FRZ_ERR_ARGUMENT,
+                  name + ": format " + (l ? l->name : "?") +
+                      " is not run here (matrices Q4_0; downs also Q4_1 or Q8_0; the embedding"
+                      " also Q8_0; norms F32)");
     }
     uint64_t ne0, ne1;
     expected_shape(c, role, &ne0, &ne1);
     const bool shape_ok = t->shape[0] == ne0 && t->shape[1] == ne1 && t->shape[2] == 1 &&
                           t->shape[3] == 1 && (ne1 == 1 ? t->dims >= 1 : t->dims >= 2);
-    if (!shape_ok || t->bytes != frz_tensor_bytes(&c, role)) {
+    const uint64_t want_bytes =
+        is_matrix(role) ? frz_tensor_bytes(&c, role) / 18 * frz::gguf::layout_of(type)->bytes
+                        : frz_tensor_bytes(&c, role);
+    if (!shape_ok || t->bytes != want_bytes) {
       return fail(FRZ_ERR_ARGUMENT, name + ": shape is not the model's");
     }
     buf.resize(t->bytes);
     if (!file.read(t->offset, buf.data(), t->bytes)) {
       return fail(FRZ_ERR_ARGUMENT, name + ": read failed");
     }
-    return frz_model_set_tensor(model, layer, role, buf.data(), t->bytes);
+    return frz_model_set_tensor_format(model, layer, role, (int)type, buf.data(), t->bytes);
   };
   if (int rc = load(-1, FRZ_ROLE_EMBEDDING, "token_embd.weight")) return rc;
   if (int rc = load(-1, FRZ_ROLE_OUTPUT_NORM, "output_norm.weight")) return rc;

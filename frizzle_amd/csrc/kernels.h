@@ -35,27 +35,41 @@ struct DevStep {
   uint32_t ids[kPrefillBlock];
 };
 
-// A Q4_0 matrix on the device: `rows` rows of `cols` weights as two streams,
-// every block's 16 code bytes in row-major block order, then every block's
-// fp16 scale (the reference's device layout, device_layout.h:114-115).
-struct Q4Matrix {
-  const uint8_t* codes;    // rows * cols / 32 blocks of 16 bytes
-  const uint16_t* scales;  // rows * cols / 32 halves
+// Block formats, by GGUF's numbers (the reference's formats/*: q4_0, q4_1,
+// q8_0).
+constexpr int kQ4_0 = 2;  // 32 weights: f16 d, 16 bytes of 4-bit codes
+constexpr int kQ4_1 = 3;  // f16 d, f16 minimum m, 16 bytes of 4-bit codes
+constexpr int kQ8_0 = 8;  // f16 d, 32 signed 8-bit codes
+constexpr int code_bytes(int format) { return format == kQ8_0 ? 32 : 16; }
+// Halves of scale a block has on the device: d (Q4_0, Q8_0) or d then m.
+constexpr int scale_halves(int format) { return format == kQ4_1 ? 2 : 1; }
+constexpr int gguf_block_bytes(int format) {
+  return format == kQ8_0 ? 34 : format == kQ4_1 ? 20 : 18;
+}
+
+// A quantized matrix on the device: `rows` rows of `cols` weights as two
+// streams, every block's code bytes in row-major block order, then every
+// block's scale halves (the reference's device layout,
+// device_layout.h:114-115).
+struct QMatrix {
+  const uint8_t* codes;    // rows * cols / 32 blocks of code_bytes(format)
+  const uint16_t* scales;  // rows * cols / 32 blocks of scale_halves(format)
   int rows;
   int cols;
+  int format = kQ4_0;
 };
 
 // ---- products ----------------------------------------------------------
 // y[t][o] = sum_k W[o][k] x[t][k] for t < step.tokens (or only the last
 // token when last_token), in the reference's order. Decode form when the
 // step holds one token; matrix-core form otherwise.
-hipError_t launch_gemv(hipStream_t s, const DevStep* step, Q4Matrix w,
+hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token);
 // act[t][j] = gelu_tanh(gate_j) * up_j, then layer `layer`'s pins at the
 // row's position (edit table in the reference's layout; null for none).
-hipError_t launch_gated(hipStream_t s, const DevStep* step, Q4Matrix gate,
-                        Q4Matrix up, const float* x, float* act,
+hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
+                        QMatrix up, const float* x, float* act,
                         int max_tokens, const uint32_t* edits, int layer);
 
 // The input row of a decode product, made in the product's prologue.
@@ -72,7 +86,7 @@ struct GemvInput {
   const float* post_gain;
   const float* gain;
   float* hidden_out;
-  Q4Matrix table;
+  QMatrix table;
   const uint32_t* sampled;
   float scale;
   float epsilon;
@@ -81,12 +95,12 @@ struct GemvInput {
   int window;
 };
 constexpr int kFoldPrologueChunks = 10;
-hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const Q4Matrix& w,
+hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix& w,
                               const GemvInput& in, int mode, float* y);
 // The gated decode product (prologue mode 0 or 1): act = gelu(gate) * up,
 // then layer `layer`'s pins.
-hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const Q4Matrix& gate,
-                               const Q4Matrix& up, const GemvInput& in, int mode, float* act,
+hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix& gate,
+                               const QMatrix& up, const GemvInput& in, int mode, float* act,
                                const uint32_t* edits, int layer);
 
 // ---- per-row kernels ---------------------------------------------------
@@ -177,7 +191,7 @@ hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldA
                                  int max_tokens);
 constexpr int kMaxFoldChunks = 224;  // chunk states a fold stages in LDS: 14,272 keys
 
-hipError_t launch_gather(hipStream_t s, const DevStep* step, Q4Matrix table,
+hipError_t launch_gather(hipStream_t s, const DevStep* step, QMatrix table,
                          const uint32_t* sampled, float* hidden, float scale,
                          int max_tokens);
 hipError_t launch_edit(hipStream_t s, const DevStep* step,

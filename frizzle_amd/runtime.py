@@ -120,6 +120,23 @@ def q4_0_split(blocks):
     return codes, scales
 
 
+# GGUF format numbers of the weight formats the library computes in.
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
+_BLOCK = {Q4_0: (18, 16, 2), Q4_1: (20, 16, 4), Q8_0: (34, 32, 2)}  # bytes, codes, scales
+
+
+def block_split(fmt, blocks):
+    """GGUF blocks of a weight format to its (codes, scales) streams."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    bb, cb, sb = _BLOCK.get(fmt, (1, 0, 0))  # another format: the library refuses it
+    n = blocks.size // bb
+    codes = np.empty(n * cb, dtype=np.uint8)
+    scales = np.empty(n * sb, dtype=np.uint8)
+    check(load().frz_block_split(fmt, blocks.ctypes.data, n, codes.ctypes.data,
+                                 scales.ctypes.data))
+    return codes, scales
+
+
 def rope_turns(base, head_dim):
     out = (ctypes.c_float * (head_dim // 2))()
     load().frz_rope_turns(base, head_dim, out)
@@ -206,10 +223,16 @@ class Model:
         check(self.lib.frz_model_create(device.handle, byref(cfg), byref(h)))
         self.handle = h.value
 
-    def set_tensor(self, layer, role, data):
+    def set_tensor(self, layer, role, data, fmt=None):
+        """A role's tensor as GGUF bytes; fmt a GGUF format number (Q4_1 or
+        Q8_0 where the role takes one), else the role's Q4_0 or F32."""
         a = np.ascontiguousarray(data)
-        check(self.lib.frz_model_set_tensor(self.handle, layer, _lib.ROLE[role],
-                                            a.ctypes.data, a.nbytes))
+        if fmt is None:
+            check(self.lib.frz_model_set_tensor(self.handle, layer, _lib.ROLE[role],
+                                                a.ctypes.data, a.nbytes))
+        else:
+            check(self.lib.frz_model_set_tensor_format(self.handle, layer, _lib.ROLE[role], fmt,
+                                                       a.ctypes.data, a.nbytes))
 
     def load_gguf(self, path):
         """Every tensor of a Gemma 3 GGUF file of this model's shapes."""

@@ -71,6 +71,18 @@ int frz_copy(frz_device* dev, void* dev_dst, const void* dev_src, uint64_t bytes
  * block's 16 code bytes, then every block's scale. Host to host. */
 int frz_q4_0_split(const void* gguf_blocks, uint64_t blocks, void* codes_out,
                    void* scales_out);
+/* The same transform for any weight format the library computes in (GGUF
+ * numbers: FRZ_FORMAT_Q4_0 2, FRZ_FORMAT_Q4_1 3, FRZ_FORMAT_Q8_0 8), with
+ * the device layouts of src/core/formats/device_layout.h:114-119: Q4_0 16
+ * code bytes and one scale half a block; Q4_1 16 code bytes and two halves
+ * (d, m); Q8_0 32 code bytes and one half. GGUF blocks are 18, 20 and 34
+ * bytes. */
+#define FRZ_FORMAT_F32 0
+#define FRZ_FORMAT_Q4_0 2
+#define FRZ_FORMAT_Q4_1 3
+#define FRZ_FORMAT_Q8_0 8
+int frz_block_split(int format, const void* gguf_blocks, uint64_t blocks,
+                    void* codes_out, void* scales_out);
 
 /* ---- one kernel at a time (the reference's launchers, each a Launch of
  *      src/core/kernels/interface.h:320-363, run alone as the kernel contract
@@ -85,6 +97,14 @@ int frz_q4_0_split(const void* gguf_blocks, uint64_t blocks, void* codes_out,
 int frz_op_gemv(frz_device* dev, const void* codes, const void* scales,
                 int rows, int cols, const float* x, int x_stride, float* y,
                 int y_stride, uint32_t tokens, int last_token);
+/* The same product over Q4_1 or Q8_0 weights as well (codes and scales in
+ * frz_block_split's layout): a format supplies only its unpack
+ * (src/core/formats/format.h; q4_1.wgsl, q8_0.wgsl), the order of addition
+ * is the same. */
+int frz_op_gemv_format(frz_device* dev, int format, const void* codes,
+                       const void* scales, int rows, int cols, const float* x,
+                       int x_stride, float* y, int y_stride, uint32_t tokens,
+                       int last_token);
 /* act[t][j] = gelu_tanh(gate_j) * up_j with layer `layer`'s pins applied at
  * position + t (matmul.wgsl:247-276 and src/core/edit/edit.wgsl:55-76 fused);
  * edits_dev may be null for none. */
@@ -128,6 +148,12 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales,
                   int rows, int cols, const uint32_t* ids, uint32_t tokens,
                   float scale, float* hidden);
+/* The same from a Q4_0 or Q8_0 table (gather.h: the file's embedding is
+ * Q8_0). */
+int frz_op_gather_format(frz_device* dev, int format, const void* codes,
+                         const void* scales, int rows, int cols,
+                         const uint32_t* ids, uint32_t tokens, float scale,
+                         float* hidden);
 /* One layer's pins alone (src/core/edit/edit.wgsl:55-76). */
 int frz_op_edit(frz_device* dev, const uint32_t* edits_dev, int layer,
                 float* act, int width, uint32_t position, uint32_t tokens);
@@ -278,6 +304,13 @@ void frz_model_destroy(frz_model* model);
 /* One tensor from host bytes as a GGUF file holds it (Upload::write). */
 int frz_model_set_tensor(frz_model* model, int layer, int role,
                          const void* data, uint64_t bytes);
+/* The same in a given GGUF format (FRZ_FORMAT_*), as the pinned file mixes
+ * them (src/core/formats/device_layout.h:64-66): the down matrices may be
+ * Q4_0, Q4_1 or Q8_0, the embedding (and so the tied head) Q4_0 or Q8_0,
+ * every other matrix Q4_0, the gains F32 (0). bytes = the role's blocks
+ * times the format's block size. */
+int frz_model_set_tensor_format(frz_model* model, int layer, int role,
+                                int format, const void* data, uint64_t bytes);
 /* Every tensor from frz_synth_tensor(seed). */
 int frz_model_synthesize(frz_model* model, uint64_t seed);
 /* The shapes the model was created with. */

@@ -214,18 +214,60 @@ void orc_q4_0_unpack(const uint8_t* block, float out[32]) {
   }
 }
 
+// A Q4_1 block's 32 weights (q4_1.wgsl:12-25): weight j = (qs[j] & 0xF) * d
+// + m, weight j + 16 = (qs[j] >> 4) * d + m. The product of a 4-bit code and
+// an f16 scale is exact in f32, so the one rounding is the addition's.
+void orc_q4_1_unpack(const uint8_t* block, float out[32]) {
+  const float d = orc_f16_unpack(static_cast<uint16_t>(block[0] | (block[1] << 8)));
+  const float m = orc_f16_unpack(static_cast<uint16_t>(block[2] | (block[3] << 8)));
+  for (int j = 0; j < 16; ++j) {
+    const uint8_t q = block[4 + j];
+    out[j] = static_cast<float>(q & 0xF) * d + m;
+    out[j + 16] = static_cast<float>(q >> 4) * d + m;
+  }
+}
+
+// A Q8_0 block's 32 weights (q8_0.wgsl:12-24): weight j = qs[j] * d, qs
+// signed bytes; exact in f32.
+void orc_q8_0_unpack(const uint8_t* block, float out[32]) {
+  const float d = orc_f16_unpack(static_cast<uint16_t>(block[0] | (block[1] << 8)));
+  for (int j = 0; j < 32; ++j) out[j] = static_cast<float>(static_cast<int8_t>(block[2 + j])) * d;
+}
+
+int orc_block_bytes(int format) {
+  switch (format) {
+    case 0: case 2: return 18;
+    case 3: return 20;
+    case 8: return 34;
+    default: return 0;
+  }
+}
+
 namespace {
+void unpack_format(int format, const uint8_t* block, float out[32]) {
+  if (format == 3) {
+    orc_q4_1_unpack(block, out);
+  } else if (format == 8) {
+    orc_q8_0_unpack(block, out);
+  } else {
+    orc_q4_0_unpack(block, out);
+  }
+}
+
 // One output of a product in the reference's order (matmul.h:88-97,
 // matmul.wgsl:154-185): range r's products chained by fma from zero, k in
-// order; then the 32 range sums added in order to a total from zero.
-float row_total(const uint8_t* row, int cols, const float* x) {
+// order; then the 32 range sums added in order to a total from zero. The
+// order is the same whatever the weights' format (format.h: each format
+// only supplies its unpack).
+float format_row_total(int format, const uint8_t* row, int cols, const float* x) {
   const int groups = cols / 32;
+  const int bb = orc_block_bytes(format);
   float total = 0.0f;
   float w[32];
   for (int r = 0; r < kRanges; ++r) {
     float s = 0.0f;
     for (int g = range_lo(r, groups); g < range_lo(r + 1, groups); ++g) {
-      orc_q4_0_unpack(row + static_cast<size_t>(g) * 18, w);
+      unpack_format(format, row + static_cast<size_t>(g) * bb, w);
       const float* xg = x + g * 32;
       for (int i = 0; i < 32; ++i) s = std::fma(w[i], xg[i], s);
     }
@@ -233,13 +275,22 @@ float row_total(const uint8_t* row, int cols, const float* x) {
   }
   return total;
 }
+
+float row_total(const uint8_t* row, int cols, const float* x) {
+  return format_row_total(2, row, cols, x);
+}
 }  // namespace
 
 void orc_gemv(const uint8_t* w, int rows, int cols, const float* x,
               float* y) {
-  const size_t row_bytes = static_cast<size_t>(cols) / 32 * 18;
+  orc_gemv_format(2, w, rows, cols, x, y);
+}
+
+void orc_gemv_format(int format, const uint8_t* w, int rows, int cols, const float* x,
+                     float* y) {
+  const size_t row_bytes = static_cast<size_t>(cols) / 32 * orc_block_bytes(format);
 #pragma omp parallel for schedule(static)
-  for (int o = 0; o < rows; ++o) y[o] = row_total(w + o * row_bytes, cols, x);
+  for (int o = 0; o < rows; ++o) y[o] = format_row_total(format, w + o * row_bytes, cols, x);
 }
 
 // gelu_tanh(gate) * up, gate and up each in the order above
@@ -474,10 +525,16 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
 // Token embedding row times the scale (gather.wgsl:25-48).
 void orc_gather_row(const uint8_t* table, int width, uint32_t token,
                     float scale, float* hidden) {
-  const size_t row_bytes = static_cast<size_t>(width) / 32 * 18;
+  orc_gather_row_format(2, table, width, token, scale, hidden);
+}
+
+void orc_gather_row_format(int format, const uint8_t* table, int width, uint32_t token,
+                           float scale, float* hidden) {
+  const int bb = orc_block_bytes(format);
+  const size_t row_bytes = static_cast<size_t>(width) / 32 * bb;
   float w[32];
   for (int g = 0; g < width / 32; ++g) {
-    orc_q4_0_unpack(table + token * row_bytes + g * 18, w);
+    unpack_format(format, table + token * row_bytes + static_cast<size_t>(g) * bb, w);
     for (int i = 0; i < 32; ++i) hidden[g * 32 + i] = w[i] * scale;
   }
 }
@@ -690,7 +747,8 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
   const int H = c.hidden;
   const int qw = c.query_heads * c.head_dim;
   const int kvw = c.kv_heads * c.head_dim;
-  orc_gather_row(m->embedding, H, token, std::sqrt(static_cast<float>(H)),
+  orc_gather_row_format(c.embedding_format, m->embedding, H, token,
+                        std::sqrt(static_cast<float>(H)),
                  m->hidden.data());
   const float* pending = nullptr;
   const float scale_log2e = static_cast<float>(
@@ -718,12 +776,12 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
     orc_gated(w.gate, w.up, c.ffn, H, m->normed.data(), m->act.data());
     orc_edit_row(m->edits.data(), l, static_cast<uint32_t>(position), c.ffn,
                  m->act.data());
-    orc_gemv(w.down, H, c.ffn, m->act.data(), m->output.data());
+    orc_gemv_format(w.down_format, w.down, H, c.ffn, m->act.data(), m->output.data());
     pending = w.post_ffn_norm;
   }
   orc_norm_row(m->output_norm, pending, 1, 1, 1.0f, c.epsilon, H,
                m->hidden.data(), m->output.data(), m->normed.data());
-  if (logits) orc_gemv(m->embedding, c.vocab, H, m->normed.data(), logits);
+  if (logits) orc_gemv_format(c.embedding_format, m->embedding, c.vocab, H, m->normed.data(), logits);
 }
 
 const float* orc_model_normed(const orc_model* m) { return m->normed.data(); }

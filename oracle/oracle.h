@@ -37,6 +37,11 @@
  *   orc_rope_row      f64 rotation; the cache as numpy's f16 of the clamp
  *   orc_attention_row f64 softmax attention; keys outside the window inert
  *   orc_gather_row    the dequantized row times the scale
+ *   orc_q8_0_unpack,  every code x every finite f16 scale (and minimum)
+ *   orc_q4_1_unpack   against the exact value rounded once to f32; the
+ *                     fixture-style blocks their generator states
+ *   orc_gemv_format   Q4_0 equal to orc_gemv; exact integer results for
+ *                     Q8_0 and Q4_1 (the order is orc_gemv's, pinned above)
  *   orc_edit_row      the edit kernel contract (edit_kernel_test.cpp:1-21)
  *   orc_topk          brute-force stable sort in the total order
  *   orc_philox        Random123 known answers; orc_mulhi against 64-bit
@@ -48,8 +53,10 @@
  *                     accuracy against f64 only: their bits, as the
  *                     reference's built-ins give them, are parity unpinned
  *
- * Weights are Q4_0 blocks as GGUF stores them: 18 bytes, an fp16 scale d then
- * 16 code bytes; a matrix of N rows of K is N * K / 32 blocks, row-major.
+ * Weights are blocks as GGUF stores them, a matrix of N rows of K being
+ * N * K / 32 blocks, row-major: Q4_0 (format 2) 18 bytes, an fp16 scale d
+ * then 16 code bytes; Q4_1 (3) 20 bytes, d, an fp16 minimum m, 16 code
+ * bytes; Q8_0 (8) 34 bytes, d then 32 signed codes.
  */
 #ifndef FRIZZLE_ORACLE_H
 #define FRIZZLE_ORACLE_H
@@ -73,6 +80,12 @@ float orc_dot4(const float* a, const float* b);
 
 /* ---- formats and products --------------------------------------------- */
 void orc_q4_0_unpack(const uint8_t* block, float out[32]);
+void orc_q4_1_unpack(const uint8_t* block, float out[32]);
+void orc_q8_0_unpack(const uint8_t* block, float out[32]);
+/* Bytes of one block of GGUF format `format` (2, 3 or 8); 0 for others. */
+int orc_block_bytes(int format);
+void orc_gemv_format(int format, const uint8_t* w, int rows, int cols,
+                     const float* x, float* y);
 void orc_gemv(const uint8_t* w, int rows, int cols, const float* x,
               float* y);
 void orc_gated(const uint8_t* gate, const uint8_t* up, int rows, int cols,
@@ -94,6 +107,8 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
                        const uint16_t* value_cache, float* out);
 void orc_gather_row(const uint8_t* table, int width, uint32_t token,
                     float scale, float* hidden);
+void orc_gather_row_format(int format, const uint8_t* table, int width,
+                           uint32_t token, float scale, float* hidden);
 void orc_edit_row(const uint32_t* table, int layer, uint32_t position,
                   int width, float* activation);
 void orc_topk(const float* logits, int count, uint32_t* bits,
@@ -124,9 +139,11 @@ typedef struct orc_config {
   float rope_local;
   float rope_global;
   float epsilon;
+  int embedding_format; /* the tied embedding/head's format (0 means Q4_0) */
 } orc_config;
 
-/* Borrowed pointers to one layer's weights (GGUF Q4_0 blocks; F32 gains). */
+/* Borrowed pointers to one layer's weights (GGUF Q4_0 blocks, the down
+ * matrix in `down_format` (0 means Q4_0); F32 gains). */
 typedef struct orc_layer_weights {
   const uint8_t* q;    /* query_heads*head_dim rows of hidden */
   const uint8_t* k;    /* kv_heads*head_dim rows of hidden */
@@ -141,6 +158,7 @@ typedef struct orc_layer_weights {
   const float* post_attn_norm;
   const float* ffn_norm;
   const float* post_ffn_norm;
+  int down_format;
 } orc_layer_weights;
 
 typedef struct orc_model orc_model;

@@ -20,13 +20,14 @@ class OrcConfig(ctypes.Structure):
     _fields_ = [(n, c_int) for n in (
         "hidden", "ffn", "head_dim", "query_heads", "kv_heads", "layers",
         "vocab", "window", "pattern", "context", "local_slots")] + [
-        ("rope_local", c_float), ("rope_global", c_float), ("epsilon", c_float)]
+        ("rope_local", c_float), ("rope_global", c_float), ("epsilon", c_float),
+        ("embedding_format", c_int)]
 
 
 class OrcLayer(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in (
         "q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm",
-        "k_norm", "post_attn_norm", "ffn_norm", "post_ffn_norm")]
+        "k_norm", "post_attn_norm", "ffn_norm", "post_ffn_norm")] + [("down_format", c_int)]
 
 
 _P = c_void_p
@@ -42,6 +43,10 @@ _SIGS = {
     "orc_dot4": (c_float, [_P, _P]),
     "orc_q4_0_unpack": (None, [_P, _P]),
     "orc_gemv": (None, [_P, c_int, c_int, _P, _P]),
+    "orc_gemv_format": (None, [c_int, _P, c_int, c_int, _P, _P]),
+    "orc_q4_1_unpack": (None, [_P, _P]),
+    "orc_q8_0_unpack": (None, [_P, _P]),
+    "orc_block_bytes": (c_int, [c_int]),
     "orc_gated": (None, [_P, _P, c_int, c_int, _P, _P]),
     "orc_norm_row": (None, [_P, _P, c_int, c_int, c_float, c_float, c_int, _P,
                             _P, _P]),
@@ -51,6 +56,7 @@ _SIGS = {
     "orc_attention_row": (None, [c_int, c_int, c_int, c_int, c_int, c_int,
                                  c_float, _P, _P, _P, _P]),
     "orc_gather_row": (None, [_P, c_int, c_uint32, c_float, _P]),
+    "orc_gather_row_format": (None, [c_int, _P, c_int, c_uint32, c_float, _P]),
     "orc_edit_row": (None, [_P, c_int, c_uint32, c_int, _P]),
     "orc_topk": (None, [_P, c_int, _P, _P]),
     "orc_philox": (None, [_P, _P, _P]),
@@ -118,6 +124,29 @@ def gated(gate_blocks, up_blocks, rows, cols, x):
     return y
 
 
+def gemv_format(fmt, w_blocks, rows, cols, x):
+    y = np.empty(rows, dtype=np.float32)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().orc_gemv_format(fmt, _p(w), rows, cols, _p(x), _p(y))
+    return y
+
+
+def unpack_format(fmt, block):
+    out = np.empty(32, dtype=np.float32)
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    {2: lib().orc_q4_0_unpack, 3: lib().orc_q4_1_unpack, 8: lib().orc_q8_0_unpack}[fmt](
+        _p(b), _p(out))
+    return out
+
+
+def gather_row_format(fmt, table, width, token, scale):
+    out = np.empty(width, dtype=np.float32)
+    t = np.ascontiguousarray(table, dtype=np.uint8)
+    lib().orc_gather_row_format(fmt, _p(t), width, token, scale, _p(out))
+    return out
+
+
 def q4_0_unpack(block):
     out = np.empty(32, dtype=np.float32)
     b = np.ascontiguousarray(block, dtype=np.uint8)
@@ -175,8 +204,11 @@ def draw(cand_bits, cand_ids, top_k=1, temperature=0.0, top_p=1.0, min_p=0.0,
 class OracleModel:
     """The oracle's model over host weight arrays (kept alive here)."""
 
-    def __init__(self, cfg_dict, tensors):
-        self.cfg = OrcConfig(**cfg_dict)
+    def __init__(self, cfg_dict, tensors, formats=None):
+        """formats: {(layer, "down") or (-1, "embedding"): GGUF format
+        number}; every other matrix is Q4_0."""
+        formats = formats or {}
+        self.cfg = OrcConfig(**cfg_dict, embedding_format=formats.get((-1, "embedding"), 2))
         self.tensors = tensors  # {(layer, role): array}
         n = self.cfg.layers
         self.layers = (OrcLayer * n)()
@@ -186,7 +218,7 @@ class OracleModel:
                          "q_norm", "k_norm", "post_attn_norm", "ffn_norm",
                          "post_ffn_norm"):
                 fields[role] = tensors[(l, role)].ctypes.data
-            self.layers[l] = OrcLayer(**fields)
+            self.layers[l] = OrcLayer(**fields, down_format=formats.get((l, "down"), 2))
         self.handle = lib().orc_model_create(
             ctypes.byref(self.cfg), self.layers,
             tensors[(-1, "embedding")].ctypes.data,

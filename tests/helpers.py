@@ -16,6 +16,36 @@ def q4_blocks(rng, rows, cols, scale_std=0.02):
     return out.reshape(-1)
 
 
+def q4_1_blocks(rng, rows, cols, scale_std=0.02):
+    """rows x cols Q4_1 weights as GGUF blocks: d = fp16(|N(0, std)|), a
+    block minimum m = fp16(-u d) with u uniform in [6, 10] (so weights lie
+    about zero, as a quantizer's minimum puts them), codes uniform in 0..15."""
+    n = rows * cols // 32
+    out = np.empty((n, 20), dtype=np.uint8)
+    d = np.abs(rng.normal(0.0, scale_std, n)).astype(np.float16)
+    m = (-d.astype(np.float32) * rng.uniform(6.0, 10.0, n)).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    out[:, 2:4] = m.view(np.uint8).reshape(n, 2)
+    out[:, 4:] = rng.integers(0, 256, size=(n, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def q8_0_blocks(rng, rows, cols, scale_std=0.002):
+    """rows x cols Q8_0 weights as GGUF blocks: d = fp16(|N(0, std)|), codes
+    uniform signed bytes."""
+    n = rows * cols // 32
+    out = np.empty((n, 34), dtype=np.uint8)
+    d = np.abs(rng.normal(0.0, scale_std, n)).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    out[:, 2:] = rng.integers(0, 256, size=(n, 32), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def format_blocks(rng, fmt, rows, cols):
+    """Seeded GGUF blocks of format fmt (2 Q4_0, 3 Q4_1, 8 Q8_0)."""
+    return {2: q4_blocks, 3: q4_1_blocks, 8: q8_0_blocks}[fmt](rng, rows, cols)
+
+
 def dequant(blocks, rows, cols):
     """Q4_0 blocks to float64 weights, by the format's definition
     (q4_0.h:21-23): weight j = ((qs[j] & 15) - 8) d, weight j+16 =

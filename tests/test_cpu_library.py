@@ -46,6 +46,22 @@ def test_q4_0_split_streams():
     assert np.array_equal(scales.reshape(10, 2), blocks[:, :2])
 
 
+@pytest.mark.parametrize("fmt,bb,sb", [(2, 18, 2), (3, 20, 4), (8, 34, 2)])
+def test_block_split_streams(fmt, bb, sb):
+    # A block is its scale halves (d; Q4_1 d then m) and then its codes
+    # (device_layout.h:114-119 keeps them as two streams).
+    rng = np.random.default_rng(fmt)
+    blocks = rng.integers(0, 256, (10, bb), dtype=np.uint8)
+    codes, scales = fz.block_split(fmt, blocks.reshape(-1))
+    assert np.array_equal(codes.reshape(10, bb - sb), blocks[:, sb:])
+    assert np.array_equal(scales.reshape(10, sb), blocks[:, :sb])
+
+
+def test_block_split_refuses_other_formats():
+    with pytest.raises(fz.FrzError):
+        fz.block_split(0, np.zeros(64, dtype=np.uint8))
+
+
 def test_rope_turns_match_oracle_and_f64():
     for base in (1e4, 1e6):
         t = fz.rope_turns(base, 256)

@@ -6,7 +6,7 @@ import pytest
 
 import _oracle as orc
 import frizzle_amd as fz
-from helpers import assert_same_bits, bits, q4_blocks
+from helpers import assert_same_bits, bits, format_blocks, q4_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -134,6 +134,83 @@ def test_gemv_last_token(device):
     fz._lib.check(fz.load().frz_op_gemv(device.handle, codes.ptr, scales.ptr, rows, cols,
                                         dx.ptr, cols, dy.ptr, rows, tokens, 1))
     assert_same_bits(dy.numpy(), orc.gemv(w, rows, cols, x[-1]), "head")
+
+
+# ---- Q4_1 and Q8_0 weights (the pinned file's first downs and its embedding,
+#      which is also the tied head) -------------------------------------------
+
+def _format_dev(device, fmt, blocks):
+    codes, scales = fz.block_split(fmt, blocks)
+    return device.array(codes), device.array(scales)
+
+
+def _gemv_format(device, fmt, w, rows, cols, x, tokens, last_token=0):
+    codes, scales = _format_dev(device, fmt, w)
+    dx = device.array(x)
+    n_out = 1 if (tokens == 1 or last_token) else tokens
+    dy = device.empty((n_out, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gemv_format(device.handle, fmt, codes.ptr, scales.ptr, rows,
+                                               cols, dx.ptr, cols, dy.ptr, rows, tokens,
+                                               last_token))
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("fmt,rows,cols", [(3, 1152, 6912), (8, 1152, 6912), (3, 1536, 1152),
+                                           (8, 16384 + 40, 1152), (3, 100, 64), (8, 100, 64)])
+def test_gemv_format_decode_bit_exact(device, fmt, rows, cols):
+    rng = np.random.default_rng(fmt * 1000 + rows + cols)
+    w = format_blocks(rng, fmt, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    got = _gemv_format(device, fmt, w, rows, cols, x, 1)[0]
+    assert_same_bits(got, orc.gemv_format(fmt, w, rows, cols, x), f"format {fmt} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("fmt,rows,cols,tokens", [(3, 1152, 6912, 37), (8, 1152, 6912, 37),
+                                                  (3, 200, 96, 3), (8, 200, 96, 3),
+                                                  (3, 1600, 1152, 512), (8, 1600, 1152, 512)])
+def test_gemv_format_tiled_bit_exact(device, fmt, rows, cols, tokens):
+    # 1600 x 512 outputs take the 32 x 32 tiles, the others the 16 x 16 ones.
+    rng = np.random.default_rng(fmt + rows + tokens)
+    w = format_blocks(rng, fmt, rows, cols)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    got = _gemv_format(device, fmt, w, rows, cols, x, tokens)
+    for t in range(tokens):
+        assert_same_bits(got[t], orc.gemv_format(fmt, w, rows, cols, x[t]), f"token {t}")
+
+
+def test_gemv_q8_0_head_last_token(device):
+    rng = np.random.default_rng(19)
+    rows, cols, tokens = 40000, 1152, 7
+    w = format_blocks(rng, 8, rows, cols)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    got = _gemv_format(device, 8, w, rows, cols, x, tokens, last_token=1)[0]
+    assert_same_bits(got, orc.gemv_format(8, w, rows, cols, x[-1]), "Q8_0 head")
+
+
+def test_gemv_format_refusals(device):
+    codes = device.empty((64,), np.uint8)
+    x = device.empty((64,), np.float32)
+    y = device.empty((2,), np.float32)
+    for fmt in (0, 1, 6):
+        with pytest.raises(fz.FrzError, match="format"):
+            fz._lib.check(fz.load().frz_op_gemv_format(device.handle, fmt, codes.ptr, codes.ptr,
+                                                       2, 32, x.ptr, 32, y.ptr, 2, 1, 0))
+
+
+def test_gather_q8_0_bit_exact(device):
+    rng = np.random.default_rng(37)
+    rows, cols = 5000, 1152
+    table = format_blocks(rng, 8, rows, cols)
+    ids = np.array([0, 4999, 17, 17, 2500], dtype=np.uint32)
+    codes, scales = _format_dev(device, 8, table)
+    dh = device.empty((ids.size, cols), np.float32)
+    scale = np.float32(np.sqrt(np.float32(cols)))
+    fz._lib.check(fz.load().frz_op_gather_format(device.handle, 8, codes.ptr, scales.ptr, rows,
+                                                 cols, ids.ctypes.data, ids.size, scale, dh.ptr))
+    got = dh.numpy()
+    for i, tok in enumerate(ids):
+        assert_same_bits(got[i], orc.gather_row_format(8, table, cols, int(tok), scale),
+                         f"row {i}")
 
 
 @pytest.mark.parametrize("tokens", [1, 6, 37])

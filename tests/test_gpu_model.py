@@ -5,7 +5,7 @@ import pytest
 
 import _oracle as orc
 import frizzle_amd as fz
-from helpers import assert_same_bits
+from helpers import assert_same_bits, q4_1_blocks, q8_0_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -155,6 +155,22 @@ def test_seeded_sampling_token_identical(device):
     model.close()
 
 
+def test_prompt_reuse_forgotten_after_direct_steps(device):
+    # generate() reuses the cached prefix of a repeated prompt; a step made
+    # outside it rewrites the caches, so the next generate() starts over.
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=13)
+    rng = np.random.default_rng(6)
+    prompt = rng.integers(0, cfg.vocab, 30).astype(np.uint32)
+    first = model.generate(prompt, max_tokens=6)
+    model.set_edits(np.zeros(2 * cfg.layers, dtype=np.uint32))
+    model.step(0, rng.integers(0, cfg.vocab, 20).astype(np.uint32), logits=False)
+    again = model.generate(prompt, max_tokens=6)
+    want, _ = oracle_run(oracle, prompt, 6, cfg)
+    assert np.array_equal(first, want) and np.array_equal(again, want), (first, again, want)
+    model.close()
+
+
 # ---- GGUF files -------------------------------------------------------------------
 
 def _synth_all(cfg, seed):
@@ -194,11 +210,12 @@ def test_gguf_load_refusals(device, tmp_path):
     cfg = small_config()
     t = _synth_all(cfg, 32)
     model = fz.Model(device, cfg)
-    # a format this backend does not run, named with its tensor
-    q8 = lambda l, r: (np.zeros(cfg.vocab * cfg.hidden // 32 * 34, np.uint8).tobytes()
-                       if r == "embedding" else t[(l, r)].tobytes())
-    p = gguf.write_gemma3(tmp_path / "q8.gguf", cfg, q8, formats={"token_embd.weight": gguf.T_Q8_0})
-    with pytest.raises(fz.FrzError, match="token_embd.weight: format Q8_0"):
+    # a format this backend does not run for the role, named with its tensor
+    q8 = lambda l, r: (np.zeros(cfg.ffn * cfg.hidden // 32 * 34, np.uint8).tobytes()
+                       if (l, r) == (1, "gate") else t[(l, r)].tobytes())
+    p = gguf.write_gemma3(tmp_path / "q8.gguf", cfg, q8,
+                          formats={"blk.1.ffn_gate.weight": gguf.T_Q8_0})
+    with pytest.raises(fz.FrzError, match="blk.1.ffn_gate.weight: format Q8_0"):
         model.load_gguf(p)
     # another model's shapes
     other = small_config(layers=2)
@@ -218,6 +235,101 @@ def test_gguf_load_refusals(device, tmp_path):
     p.write_bytes(whole[:first + 100])  # the index whole, the data cut
     with pytest.raises(fz.FrzError, match="tensor data lies outside the file"):
         model.load_gguf(p)
+    model.close()
+
+
+# ---- the pinned file's formats: a Q8_0 embedding (and so head), Q4_1 downs ----
+
+MIXED = {(-1, "embedding"): fz.Q8_0, (0, "down"): fz.Q4_1, (1, "down"): fz.Q4_1,
+         (2, "down"): fz.Q8_0}
+
+
+def _mixed_tensors(cfg, seed):
+    t = _synth_all(cfg, seed)
+    rng = np.random.default_rng(seed)
+    t[(-1, "embedding")] = q8_0_blocks(rng, cfg.vocab, cfg.hidden, scale_std=0.004)
+    t[(0, "down")] = q4_1_blocks(rng, cfg.hidden, cfg.ffn, scale_std=0.01)
+    t[(1, "down")] = q4_1_blocks(rng, cfg.hidden, cfg.ffn, scale_std=0.01)
+    t[(2, "down")] = q8_0_blocks(rng, cfg.hidden, cfg.ffn, scale_std=0.0006)
+    return t
+
+
+def _set_all(model, t, formats):
+    for (l, r), a in t.items():
+        model.set_tensor(l, r, a, formats.get((l, r)))
+
+
+def test_mixed_formats_prefill_and_decode_bit_exact(device):
+    cfg = small_config()
+    t = _mixed_tensors(cfg, 41)
+    oracle = orc.OracleModel(cfg.as_dict(), t, formats=MIXED)
+    model = fz.Model(device, cfg)
+    # First Q4_0 everywhere, decoded once (its graph captured), then the
+    # mixed formats: the matrices change format and the graph is captured
+    # again over the new buffers.
+    _set_all(model, _synth_all(cfg, 41), {})
+    model.generate(np.arange(5, dtype=np.uint32), max_tokens=3)
+    _set_all(model, t, MIXED)
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, cfg.vocab, 90).astype(np.uint32)
+    model.set_edits(np.zeros(2 * cfg.layers, dtype=np.uint32))
+    model.step(0, prompt[:41], logits=False)
+    model.step(41, prompt[41:], logits=True)
+    _, want_logits = oracle_run(oracle, prompt, 0, cfg)
+    assert_same_bits(model.logits(), want_logits, "prompt-end logits")
+    for l in range(cfg.layers):
+        n = oracle.key_cache(l).size
+        assert np.array_equal(model.cache(l, False, n), oracle.key_cache(l)), f"keys {l}"
+    oracle.close()
+    oracle = orc.OracleModel(cfg.as_dict(), t, formats=MIXED)
+    steps = 24
+    want, _ = oracle_run(oracle, prompt, steps, cfg)
+    got = model.generate(prompt, max_tokens=steps)
+    assert np.array_equal(got, want), (got, want)
+    lg = oracle.token(int(want[-2]), len(prompt) + steps - 2)
+    assert_same_bits(model.logits(), lg, "last decode logits")
+    model.close()
+
+
+def test_mixed_formats_gguf_load(device, tmp_path):
+    # The file's formats reach the model as they are: a GGUF file with a Q8_0
+    # embedding and Q4_1 / Q8_0 downs loads to the model set tensor by tensor;
+    # then Q4_0 tensors put the matrices back in Q4_0.
+    from frizzle_amd import gguf
+    cfg = small_config()
+    t = _mixed_tensors(cfg, 43)
+    names = {(-1, "embedding"): "token_embd.weight", (0, "down"): "blk.0.ffn_down.weight",
+             (1, "down"): "blk.1.ffn_down.weight", (2, "down"): "blk.2.ffn_down.weight"}
+    path = gguf.write_gemma3(tmp_path / "mixed.gguf", cfg, lambda l, r: t[(l, r)].tobytes(),
+                             formats={names[k]: f for k, f in MIXED.items()})
+    a = fz.Model(device, cfg)
+    _set_all(a, t, MIXED)
+    b = fz.Model(device, cfg)
+    b.load_gguf(path)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 30).astype(np.uint32)
+    ta, tb = a.generate(prompt, max_tokens=10), b.generate(prompt, max_tokens=10)
+    assert np.array_equal(ta, tb)
+    assert_same_bits(b.logits(), a.logits(), "logits after 10 tokens")
+    q = _synth_all(cfg, 44)
+    _set_all(b, q, {})
+    c, _ = build_pair(device, cfg, 44)
+    assert np.array_equal(b.generate(prompt, max_tokens=10), c.generate(prompt, max_tokens=10))
+    assert_same_bits(b.logits(), c.logits(), "back in Q4_0")
+    for m in (a, b, c):
+        m.close()
+
+
+def test_set_tensor_format_refusals(device):
+    cfg = small_config()
+    model = fz.Model(device, cfg)
+    rng = np.random.default_rng(2)
+    q8 = q8_0_blocks(rng, cfg.ffn, cfg.hidden)
+    with pytest.raises(fz.FrzError, match="format 8 is not run for this role"):
+        model.set_tensor(0, "gate", q8, fz.Q8_0)
+    with pytest.raises(fz.FrzError, match="format 3 is not run for this role"):
+        model.set_tensor(-1, "embedding", q4_1_blocks(rng, cfg.vocab, cfg.hidden), fz.Q4_1)
+    with pytest.raises(fz.FrzError, match="wrong size"):
+        model.set_tensor(0, "down", q8[:-34], fz.Q8_0)
     model.close()
 
 

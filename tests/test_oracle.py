@@ -535,3 +535,115 @@ def test_draw_inverse_transform_against_f64():
         want = int(np.searchsorted(run, u * run[-1], side="right"))
         near = np.min(np.abs(run - u * run[-1])) < 1e-5 * run[-1]
         assert rec[0] == want or near
+
+
+# ---- Q8_0 and Q4_1 (the pinned file's head and downs) ----------------------------
+
+def _round_f32(v):
+    """The f32 nearest the exact rational v, ties to even."""
+    from fractions import Fraction
+    a = np.float32(float(v))
+    best = a
+    for c in (np.nextafter(a, np.float32(-np.inf)), np.nextafter(a, np.float32(np.inf))):
+        da, dc = abs(Fraction(float(best)) - v), abs(Fraction(float(c)) - v)
+        if dc < da or (dc == da and (int(np.array(c).view(np.uint32)) & 1) == 0):
+            best = c
+    return best
+
+
+def test_q8_0_exact_for_every_code_and_sampled_scale():
+    # weight j = qs[j] d (q8_0.wgsl:12-24), exact in f32: compare with f64.
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = h[np.isfinite(h.view(np.float16))]
+    codes = np.arange(256, dtype=np.uint8)
+    for s in finite[::53]:
+        for half in range(8):
+            block = np.empty(34, dtype=np.uint8)
+            block[0:2] = np.array([s], dtype=np.uint16).view(np.uint8)
+            block[2:] = codes[32 * half:32 * half + 32]
+            w = orc.unpack_format(8, block)
+            dv = np.float64(np.array([s], dtype=np.uint16).view(np.float16)[0])
+            want = codes[32 * half:32 * half + 32].view(np.int8).astype(np.float64) * dv
+            assert np.array_equal(w.astype(np.float64), want), hex(s)
+
+
+def test_q4_1_rounds_once_for_every_code():
+    # weight = q d + m (q4_1.wgsl:12-25): q d is exact, so the value is the
+    # exact q d + m rounded once to f32.
+    from fractions import Fraction
+    rng = np.random.default_rng(13)
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = h[np.isfinite(h.view(np.float16))]
+    for _ in range(300):
+        d_bits, m_bits = rng.choice(finite, 2)
+        block = np.empty(20, dtype=np.uint8)
+        block[0:2] = np.array([d_bits], dtype=np.uint16).view(np.uint8)
+        block[2:4] = np.array([m_bits], dtype=np.uint16).view(np.uint8)
+        block[4:] = (np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4))
+        w = orc.unpack_format(3, block)
+        d = Fraction(float(np.array([d_bits], dtype=np.uint16).view(np.float16)[0]))
+        m = Fraction(float(np.array([m_bits], dtype=np.uint16).view(np.float16)[0]))
+        lo = np.arange(16)
+        qs = np.concatenate([lo, lo[::-1]])
+        want = np.array([_round_f32(int(q) * d + m) for q in qs], dtype=np.float32)
+        assert np.array_equal(bits(w), bits(want)), (hex(d_bits), hex(m_bits))
+
+
+def _blocks_exact(rng, fmt, rows, cols):
+    """Blocks whose weights are small integers (d = 1, m small), so that
+    every product and sum of a short row is exact in f32."""
+    n = rows * cols // 32
+    bb = {2: 18, 3: 20, 8: 34}[fmt]
+    out = np.zeros((n, bb), dtype=np.uint8)
+    out[:, 0:2] = np.array([0x3C00], dtype=np.uint16).view(np.uint8)  # d = 1
+    if fmt == 3:
+        m = rng.integers(-3, 4, n).astype(np.float16)
+        out[:, 2:4] = m.view(np.uint8).reshape(n, 2)
+        out[:, 4:] = rng.integers(0, 256, (n, 16), dtype=np.uint8)
+    elif fmt == 8:
+        out[:, 2:] = rng.integers(-20, 21, (n, 32)).astype(np.int8).view(np.uint8)
+    else:
+        out[:, 2:] = rng.integers(0, 256, (n, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def _dequant_format(fmt, blocks, rows, cols):
+    b = blocks.reshape(-1, {2: 18, 3: 20, 8: 34}[fmt])
+    return np.stack([orc.unpack_format(fmt, blk) for blk in b]).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("fmt", [3, 8])
+def test_gemv_format_exact_integers(fmt):
+    rng = np.random.default_rng(fmt)
+    rows, cols = 24, 256
+    w = _blocks_exact(rng, fmt, rows, cols)
+    x = rng.integers(-4, 5, cols).astype(np.float32)
+    y = orc.gemv_format(fmt, w, rows, cols, x)
+    want = _dequant_format(fmt, w, rows, cols).astype(np.float64) @ x.astype(np.float64)
+    assert np.array_equal(y.astype(np.float64), want)
+    # and the rows' blocks by an independent unpack of the layout
+    b = w.reshape(rows, cols // 32, -1)
+    if fmt == 8:
+        q = b[:, :, 2:].view(np.int8).astype(np.float64).reshape(rows, cols)
+        assert np.array_equal(q @ x.astype(np.float64), want)
+
+
+def test_gemv_format_q4_0_is_gemv():
+    rng = np.random.default_rng(4)
+    rows, cols = 40, 1152
+    w = q4_blocks(rng, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    assert np.array_equal(bits(orc.gemv_format(2, w, rows, cols, x)), bits(orc.gemv(w, rows, cols, x)))
+
+
+@pytest.mark.parametrize("fmt", [2, 8])
+def test_gather_format_is_row_times_scale(fmt):
+    rng = np.random.default_rng(6 + fmt)
+    rows, cols = 7, 128
+    w = _blocks_exact(rng, fmt, rows, cols)
+    w.reshape(-1, {2: 18, 8: 34}[fmt])[:, 0:2] = np.abs(rng.normal(0, 0.02, rows * cols // 32)).astype(
+        np.float16).view(np.uint8).reshape(-1, 2)
+    scale = np.float32(np.sqrt(np.float32(cols)))
+    got = orc.gather_row_format(fmt, w, cols, 5, scale)
+    want = (_dequant_format(fmt, w, rows, cols)[5].astype(np.float32) * scale).astype(np.float32)
+    assert np.array_equal(bits(got), bits(want))
