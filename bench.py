@@ -64,6 +64,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--parity-tokens", type=int, default=256)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-pinned", action="store_true",
+                   help="skip the decode over the pinned file's Q8_0/Q4_1 formats")
     p.add_argument("--eager", action="store_true",
                    help="launch decode kernels one by one instead of replaying a graph")
     p.add_argument("--roofline-only", action="store_true",
@@ -192,6 +194,53 @@ def gguf_load(fz, seed):
                       "model": "full 26-layer Gemma-3-1B shape, synthetic Q4_0"}))
 
 
+def pinned_formats(fz, model, cfg, seed):
+    """Gives the model the pinned file's formats (device_layout.h:64-66): the
+    embedding, and so the tied head, in Q8_0 and the first three downs in
+    Q4_1, as seeded blocks of the same scales as the Q4_0 ones."""
+    rng = np.random.default_rng(seed + 5)
+
+    def blocks(rows, cols, fmt):
+        n = rows * cols // 32
+        d = np.abs(rng.normal(0.0, 0.02, n)).astype(np.float16)
+        if fmt == fz.Q8_0:
+            d = (d.astype(np.float32) / 16).astype(np.float16)  # codes 16 times wider
+            out = np.empty((n, 34), dtype=np.uint8)
+            out[:, 2:] = rng.integers(0, 256, size=(n, 32), dtype=np.uint8)
+        else:
+            m = (-d.astype(np.float32) * 8).astype(np.float16)
+            out = np.empty((n, 20), dtype=np.uint8)
+            out[:, 2:4] = m.view(np.uint8).reshape(n, 2)
+            out[:, 4:] = rng.integers(0, 256, size=(n, 16), dtype=np.uint8)
+        out[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+        return out.reshape(-1)
+
+    model.set_tensor(-1, "embedding", blocks(cfg.vocab, cfg.hidden, fz.Q8_0), fz.Q8_0)
+    for layer in range(3):
+        model.set_tensor(layer, "down", blocks(cfg.hidden, cfg.ffn, fz.Q4_1), fz.Q4_1)
+
+
+def timed_decode(model, dev, prompt, warmup, steps, greedy):
+    """The prompt in 512-token steps, `warmup` decode steps, then `steps`
+    timed ones: (prefill seconds, wall seconds, µs/step by HIP events)."""
+    model.set_edits(np.zeros(2 * model.cfg.layers, dtype=np.uint32))
+    t0 = time.perf_counter()
+    for p0 in range(0, len(prompt), 512):
+        ids = prompt[p0:p0 + 512]
+        model.step(p0, ids, logits=(p0 + len(ids) == len(prompt)), samp=greedy)
+    dev.sync()
+    prefill_s = time.perf_counter() - t0
+    pos = len(prompt)
+    if warmup:
+        model.decode(pos, warmup, greedy)
+        pos += warmup
+    dev.sync()
+    t0 = time.perf_counter()
+    us_events = model.time_decode(pos, steps, greedy)
+    dev.sync()
+    return prefill_s, time.perf_counter() - t0, us_events
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -284,26 +333,24 @@ def main():
 
     # The workload: a 4,096-token prompt, then greedy decode.
     prompt = rng.integers(0, cfg.vocab, args.prompt).astype(np.uint32)
-    model.set_edits(np.zeros(2 * cfg.layers, dtype=np.uint32))
-    t0 = time.perf_counter()
-    for p0 in range(0, args.prompt, 512):
-        ids = prompt[p0:p0 + 512]
-        model.step(p0, ids, logits=(p0 + len(ids) == args.prompt), samp=greedy)
-    dev.sync()
-    prefill_s = time.perf_counter() - t0
+    prefill_s, wall, us_events = timed_decode(model, dev, prompt, args.warmup, args.steps,
+                                              greedy)
     log(f"prefill {args.prompt} tokens in {prefill_s:.3f}s")
-    pos = args.prompt
-    if args.warmup:
-        model.decode(pos, args.warmup, greedy)
-        pos += args.warmup
-    dev.sync()
-    t0 = time.perf_counter()
-    us_events = model.time_decode(pos, args.steps, greedy)
-    dev.sync()
-    wall = time.perf_counter() - t0
     ms_per_step = wall * 1000.0 / args.steps
     log(f"decode {args.steps} steps: {ms_per_step * 1000:.1f} us/step wall, "
         f"{us_events:.1f} us/step events")
+
+    # The same workload over the pinned file's formats (reported beside the
+    # Q4_0 figure, which is the metric's).
+    pinned = None
+    if not args.no_pinned:
+        pinned_formats(fz, model, cfg, args.seed)
+        _, pwall, pus = timed_decode(model, dev, prompt, args.warmup, args.steps, greedy)
+        pinned = {"workload": "the same decode with the pinned file's formats: Q8_0 "
+                              "embedding and tied head (320,864,256 B), Q4_1 downs in "
+                              "layers 0-2, Q4_0 elsewhere",
+                  "tok_per_s": args.steps / pwall, "us_per_step_hip_events": pus}
+        log(f"pinned formats: {args.steps / pwall:.1f} tok/s, {pus:.1f} us/step events")
 
     us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
                        not args.gemv_stream)
@@ -336,6 +383,7 @@ def main():
                      "us_per_launch": us, "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,
         "parity": parity,
+        "pinned_formats": pinned,
         "prefill": {"workload": f"Gemma-3-1B Q4_0 prefill of {PREFILL_TOKENS} seeded ids in "
                                 "512-token steps, logits at the last position",
                     "seconds": prefill_2048, "flop": PREFILL_FLOP,
