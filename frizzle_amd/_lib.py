@@ -137,6 +137,8 @@ _SIGS = {
     "frz_generate": (c_int, [_P, _P, c_uint32, _P, c_uint32, POINTER(Sampling),
                              c_uint32, _P, c_uint32, _P, POINTER(c_uint32)]),
     "frz_model_get_config": (c_int, [_P, POINTER(ModelConfig)]),
+    "frz_generate_variants": (c_int, [_P, _P, c_uint32, c_uint32, _P, c_uint32,
+                                      POINTER(Sampling), c_uint32, _P, c_uint32, _P, _P, _P]),
     "frz_gguf_read": (c_int, [_P, c_uint64, c_uint64, POINTER(c_void_p), POINTER(c_uint64)]),
     "frz_gguf_open": (c_int, [_S, POINTER(c_void_p)]),
     "frz_gguf_free": (None, [_P]),

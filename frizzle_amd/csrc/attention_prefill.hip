@@ -14,15 +14,17 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
   __shared__ ChunkShared S;
   const int row = blockIdx.y;
   if (row >= (int)step->tokens) return;
-  const int p = (int)step->position + row;
+  // A variants step: every row at the step's position, over its own caches.
+  const int p = (int)step->position + (step->variants ? 0 : row);
+  const size_t cache_at = step->variants ? (size_t)row * a.cache_stride : 0;
   const ChunkRange r = chunk_range(p, a.window, blockIdx.x);
   if ((int)blockIdx.x >= r.count) return;
   const int h = blockIdx.z, t = threadIdx.x;
   uint4 kr[kKeyLoads], vr[kValueLoads];
   float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
   if (t < D / 4) q = ld4f(a.query + (size_t)row * a.q_stride + h * D + 4 * t);
-  key_load(kr, a.key_cache, a.slots, r, -1);
-  value_load(vr, a.value_cache, a.slots, r, -1);
+  key_load(kr, a.key_cache + cache_at, a.slots, r, -1);
+  value_load(vr, a.value_cache + cache_at, a.slots, r, -1);
   if (t < D / 4) {
     const float sc = a.scale_log2e;
     *reinterpret_cast<float4*>(S.q + 4 * t) = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   extern __shared__ __align__(16) float fold_smem[];
   const int row = blockIdx.y;
   if (row >= (int)step->tokens) return;
-  const int p = (int)step->position + row;
+  const int p = (int)step->position + (step->variants ? 0 : row);
   const int count = chunk_range(p, f.window, 0).count;
   const int h = blockIdx.x / (D / kFoldDims), dim0 = (blockIdx.x % (D / kFoldDims)) * kFoldDims;
   const int t = threadIdx.x;

@@ -86,6 +86,14 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
       }
     }
   }
+  if (a.capture) {
+    float* cap = a.capture + (size_t)step->drawn * a.capture_step + base;
+#pragma unroll
+    for (int k = 0; k < kNormMaxVec4; ++k) {
+      const int q = i + k * kNormThreads;
+      if (k < per && q < vec4s) st4(cap + 4 * q, x[k]);
+    }
+  }
   float squares = 0.0f;
 #pragma unroll
   for (int k = 0; k < kNormMaxVec4; ++k) {
@@ -117,7 +125,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
   __shared__ float partial[256];
   const int row = blockIdx.x;
   if (row >= (int)step->tokens) return;
-  const uint32_t p = step->position + (uint32_t)row;
+  const uint32_t p = step->position + (step->variants ? 0u : (uint32_t)row);
+  const size_t cache_at = step->variants ? (size_t)row * a.cache_stride : 0;
   const int lanes = a.head_dim / 8, half = a.head_dim / 2;
   const int heads = a.query_heads + 2 * a.kv_heads;
   const int t = threadIdx.x;
@@ -157,7 +166,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
     st4(dst + half + 4 * lane, vb);
   } else {
     const uint32_t slot = p % (uint32_t)a.slots;
-    uint16_t* cache = (is_value ? a.value_cache : a.key_cache) +
+    uint16_t* cache = (is_value ? a.value_cache : a.key_cache) + cache_at +
                       ((size_t)slot * a.kv_heads + kv) * a.head_dim;
     *reinterpret_cast<ushort4*>(cache + 4 * lane) = pack4_f16(va);
     *reinterpret_cast<ushort4*>(cache + half + 4 * lane) = pack4_f16(vb);
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const DevStep* __restrict__
                                                      float* __restrict__ hidden, float scale) {
   const int row = blockIdx.x;
   if (row >= (int)step->tokens) return;
-  const uint32_t token = step->fed ? sampled[0] : step->ids[row];
+  const uint32_t token = step->fed ? sampled[step->variants ? 4 * row : 0] : step->ids[row];
   if (token >= (uint32_t)table.rows) return;
   const int groups = table.cols / 32;
   // A Q8_0 table (the file's embedding) holds weight j of a block as the
@@ -203,7 +212,7 @@ __global__ __launch_bounds__(64) void edit_kernel(const DevStep* __restrict__ st
   if (row >= (int)step->tokens) return;
   const uint32_t first = table[2 * layer];
   const uint32_t count = table[2 * layer + 1];
-  const uint32_t position = step->position + (uint32_t)row;
+  const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)row);
   for (uint32_t i = threadIdx.x; i < count; i += 64) {
     const uint32_t* e = table + first + 5 * i;
     if (position < e[3] || position >= e[4]) continue;

@@ -22,6 +22,7 @@ namespace {
 
 constexpr uint32_t kToTheEnd = 0xFFFFFFFFu;  // edit/edit.h: kToTheEnd
 constexpr int kMaxEdits = 4096;              // edit/edit.h: kMaxEdits
+constexpr int kMaxVariants = 64;             // rows of a variants step
 
 // ---- the synthetic weights -------------------------------------------------
 // SplitMix64 (Steele, Lea, Flood 2014), one stream per (seed, layer, role).
@@ -115,6 +116,20 @@ struct frz_model {
   std::vector<uint32_t> cached_edits;
   uint64_t written_end = 0;  // one past the last position any step wrote
   std::vector<uint32_t> edit_words;
+  // Buffers of a variants step (frz_generate_variants), grown on demand:
+  // each layer's caches once per variant, `rows` rows of logits and
+  // selection, the edit tables edit_stride words apart, the token log and
+  // the residual capture of `steps` steps.
+  struct Variants {
+    int rows = 0;
+    uint32_t steps = 0, edit_stride = 0;
+    bool capture = false;  // this run writes the residual capture
+    std::vector<uint16_t*> kcache, vcache;
+    float* logits = nullptr;
+    float* residuals = nullptr;
+    uint32_t *scratch = nullptr, *candidates = nullptr, *sampled = nullptr, *token_log = nullptr,
+             *edits = nullptr;
+  } variants;
 };
 
 namespace {
@@ -215,37 +230,50 @@ float scale_log2e_of(const frz_model_config& c) {
   return (float)((double)(1.0f / std::sqrt((float)c.head_dim)) * 1.4426950408889634);
 }
 
-// A step of several tokens, in the graph's order (graph.cpp:290-470): the
+// A step of several rows, in the graph's order (graph.cpp:290-470): the
 // embedding; per layer the attention norm (adding the last block's
 // post-normed output), Q/K/V, rope and the cache append, attention, O; the
 // feed-forward norm, gate-up with GELU and the pins, down; then the final
-// norm of the last row and, with logits, the output block.
-int enqueue_prefill(frz_model* m, int max_tokens, bool logits) {
+// norm and, with logits, the output block. The rows are one sequence's
+// positions (the final norm and head on the last row only), or with `v` a
+// variants step: each row its own sequence over its own caches and edit
+// table, every row's logits drawn from, the residual entering each layer
+// captured.
+int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Variants* v) {
   const frz_model_config& c = m->c;
   hipStream_t s = m->dev->stream;
   const int H = c.hidden, qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
   const int qkv_stride = qw + 2 * kvw;
   const float scale_log2e = scale_log2e_of(c);
-  hipError_t e = launch_gather(s, m->step, m->embedding, m->sampled, m->hidden,
+  hipError_t e = launch_gather(s, m->step, m->embedding, v ? v->sampled : m->sampled, m->hidden,
                                std::sqrt((float)H), max_tokens);
   const float* pending = nullptr;
   for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
     const Layer& L = m->layers[l];
     NormArgs attn_norm{L.gains[0], pending, m->output, m->hidden, m->normed,
                        c.epsilon, H, false};
+    if (v && v->capture) {
+      // [step][layer][row][hidden] for this step's rows
+      attn_norm.capture = v->residuals + (size_t)l * max_tokens * H;
+      attn_norm.capture_step = (size_t)c.layers * max_tokens * H;
+    }
+    uint16_t* kcache = v ? v->kcache[l] : L.kcache;
+    uint16_t* vcache = v ? v->vcache[l] : L.vcache;
+    const size_t cache_stride = v ? (size_t)L.slots * kvw : 0;
     e = launch_norm(s, m->step, attn_norm, max_tokens);
     if (e == hipSuccess)
       e = launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens, false);
     if (e == hipSuccess) {
       RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     m->qkv + qw,
-                 m->qkv + qw + kvw, qkv_stride, qkv_stride, L.kcache, L.vcache,
-                 L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon};
+                 m->qkv + qw + kvw, qkv_stride, qkv_stride, kcache, vcache,
+                 L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon, cache_stride};
       e = launch_rope(s, m->step, r, max_tokens);
     }
     if (e == hipSuccess) {
-      AttentionArgs a{m->qkv,     qkv_stride, L.kcache,     L.vcache,       m->attn,
+      AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
                       m->partials, m->partials + m->partial_floats, L.slots, L.window,
-                      c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e};
+                      c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
+                      cache_stride};
       e = launch_attention(s, m->step, a, max_tokens);
     }
     if (e == hipSuccess)
@@ -256,18 +284,30 @@ int enqueue_prefill(frz_model* m, int max_tokens, bool logits) {
       e = launch_norm(s, m->step, ffn_norm, max_tokens);
     }
     if (e == hipSuccess)
-      e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens, m->edits, l);
+      e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens,
+                       v ? v->edits : m->edits, l, v ? v->edit_stride : 0);
     if (e == hipSuccess)
       e = launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
     pending = L.gains[5];
   }
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden, m->normed,
-                        c.epsilon, H, true};
+                        c.epsilon, H, v == nullptr};
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
-  if (logits && e == hipSuccess) e = enqueue_output(m, max_tokens, false);
-  return check_hip(e, "enqueue_prefill");
+  if (logits && e == hipSuccess) {
+    if (!v) {
+      e = enqueue_output(m, max_tokens, false);
+    } else {
+      e = launch_gemv(s, m->step, m->embedding, m->normed, H, v->logits, c.vocab, max_tokens,
+                      false);
+      if (e == hipSuccess) {
+        e = launch_select_rows(s, m->step, v->logits, c.vocab, max_tokens, v->scratch,
+                               v->candidates, v->sampled, v->token_log);
+      }
+    }
+  }
+  return check_hip(e, "enqueue_rows");
 }
 
 // A step of one token: five launches a layer, each norm inside the product
@@ -348,7 +388,7 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
 // the step parameters for the next.
 int enqueue_step(frz_model* m, int max_tokens, bool logits, bool advance = false) {
   return max_tokens == 1 ? enqueue_decode(m, logits, advance)
-                         : enqueue_prefill(m, max_tokens, logits);
+                         : enqueue_rows(m, max_tokens, logits, nullptr);
 }
 
 int build_decode_graph(frz_model* m) {
@@ -674,28 +714,36 @@ int frz_model_set_graphs(frz_model* m, int enabled) {
   return FRZ_OK;
 }
 
-int frz_model_set_edits(frz_model* m, const uint32_t* table, uint32_t words) {
-  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: null model");
-  const size_t cap = 2 * (size_t)m->c.layers + 5 * (size_t)kMaxEdits;
-  std::vector<uint32_t> t;
-  if (table && words) t.assign(table, table + words);
-  if (t.size() < (size_t)(2 * m->c.layers)) t.resize(2 * m->c.layers, 0);
-  if (t.size() > cap) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: more than 4096 edits");
-  for (int l = 0; l < m->c.layers; ++l) {
+// An edit table as the kernels read it (edit.h:50-60), padded to the
+// per-layer words; refused when an edit's words run past it, a neuron or
+// kind is out of range, or a layer's edits are not sorted by neuron.
+static int check_table(const frz_model_config& c, std::vector<uint32_t>& t, const char* what) {
+  const size_t cap = 2 * (size_t)c.layers + 5 * (size_t)kMaxEdits;
+  if (t.size() < (size_t)(2 * c.layers)) t.resize(2 * c.layers, 0);
+  if (t.size() > cap) return fail(FRZ_ERR_ARGUMENT, std::string(what) + ": more than 4096 edits");
+  for (int l = 0; l < c.layers; ++l) {
     const uint64_t first = t[2 * l], count = t[2 * l + 1];
     if (count && first + 5 * count > t.size()) {
-      return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: a layer's edits run past the table");
+      return fail(FRZ_ERR_ARGUMENT, std::string(what) + ": a layer's edits run past the table");
     }
     for (uint64_t i = 0; i < count; ++i) {
       const uint32_t* e = t.data() + first + 5 * i;
-      if (e[0] >= (uint32_t)m->c.ffn || e[1] > 2u) {
-        return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: neuron or kind out of range");
+      if (e[0] >= (uint32_t)c.ffn || e[1] > 2u) {
+        return fail(FRZ_ERR_ARGUMENT, std::string(what) + ": neuron or kind out of range");
       }
       if (i > 0 && e[0] < e[-5]) {
-        return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: a layer's edits are not by neuron");
+        return fail(FRZ_ERR_ARGUMENT, std::string(what) + ": a layer's edits are not by neuron");
       }
     }
   }
+  return FRZ_OK;
+}
+
+int frz_model_set_edits(frz_model* m, const uint32_t* table, uint32_t words) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_edits: null model");
+  std::vector<uint32_t> t;
+  if (table && words) t.assign(table, table + words);
+  if (int rc = check_table(m->c, t, "frz_model_set_edits")) return rc;
   m->edit_words = t;
   if (int rc = check_hip(hipMemcpyAsync(m->edits, t.data(), t.size() * 4, hipMemcpyHostToDevice,
                                         m->dev->stream),
@@ -911,6 +959,184 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   }
   std::copy(out.begin(), out.end(), tokens_out);
   *drawn = (uint32_t)out.size();
+  return FRZ_OK;
+}
+
+// Grows the variants buffers to `rows` rows, `steps` steps, tables of
+// `stride` words and, when `residuals`, the capture; what is already large
+// enough is kept.
+static int ensure_variants(frz_model* m, int rows, uint32_t steps, uint32_t stride,
+                           bool residuals) {
+  frz_model::Variants& v = m->variants;
+  const frz_model_config& c = m->c;
+  const size_t kvw = (size_t)c.kv_heads * c.head_dim;
+  if (rows > v.rows) {
+    for (uint16_t* p : v.kcache) release(m, p);
+    for (uint16_t* p : v.vcache) release(m, p);
+    v.kcache.assign(c.layers, nullptr);
+    v.vcache.assign(c.layers, nullptr);
+    for (void* p : {(void*)v.logits, (void*)v.scratch, (void*)v.candidates, (void*)v.sampled})
+      release(m, p);
+    v.logits = nullptr;
+    v.scratch = v.candidates = v.sampled = nullptr;
+    v.rows = 0;
+    for (int l = 0; l < c.layers; ++l) {
+      const size_t bytes = (size_t)rows * m->layers[l].slots * kvw * 2;
+      if (int rc = alloc(m, &v.kcache[l], bytes)) return rc;
+      if (int rc = alloc(m, &v.vcache[l], bytes)) return rc;
+    }
+    if (int rc = alloc(m, &v.logits, (size_t)rows * c.vocab * 4)) return rc;
+    if (int rc = alloc(m, &v.scratch, (size_t)rows * topk_scratch_words(c.vocab) * 4)) return rc;
+    if (int rc = alloc(m, &v.candidates, (size_t)rows * 2 * kCandidates * 4)) return rc;
+    if (int rc = alloc(m, &v.sampled, (size_t)rows * 16)) return rc;
+    v.rows = rows;
+    v.steps = 0;  // the token log and capture are sized by rows too
+    v.edit_stride = 0;
+  }
+  if (steps > v.steps || (residuals && !v.residuals)) {
+    release(m, v.token_log);
+    release(m, v.residuals);
+    v.token_log = nullptr;
+    v.residuals = nullptr;
+    v.steps = 0;
+    const uint32_t n = std::max(steps, v.steps);
+    if (int rc = alloc(m, &v.token_log, (size_t)n * v.rows * 2 * 4)) return rc;
+    if (residuals) {
+      if (int rc = alloc(m, &v.residuals, (size_t)n * c.layers * v.rows * c.hidden * 4))
+        return rc;
+    }
+    v.steps = n;
+  }
+  if (stride > v.edit_stride) {
+    release(m, v.edits);
+    v.edits = nullptr;
+    v.edit_stride = 0;
+    if (int rc = alloc(m, &v.edits, (size_t)v.rows * stride * 4)) return rc;
+    v.edit_stride = stride;
+  }
+  return FRZ_OK;
+}
+
+int frz_generate_variants(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
+                          uint32_t variants, const uint32_t* edit_tables, uint32_t table_words,
+                          const frz_sampling* sampling, uint32_t max_tokens,
+                          const uint32_t* stop_ids, uint32_t stops, uint32_t* tokens_out,
+                          uint32_t* drawn_out, float* residuals_out) {
+  if (!m || !prompt || prompt_len == 0 || !tokens_out || !drawn_out) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_generate_variants: null argument or empty prompt");
+  }
+  const frz_model_config& c = m->c;
+  if (variants < 1 || variants > (uint32_t)kMaxVariants) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_generate_variants: 1 to 64 variants");
+  }
+  if (max_tokens == 0 || (uint64_t)prompt_len + max_tokens > (uint64_t)c.context) {
+    return fail(FRZ_ERR_ARGUMENT,
+                "frz_generate_variants: at least one token, and prompt and reply within the "
+                "context");
+  }
+  for (uint32_t i = 0; i < prompt_len; ++i) {
+    if (prompt[i] >= (uint32_t)c.vocab)
+      return fail(FRZ_ERR_ARGUMENT, "frz_generate_variants: token id");
+  }
+  if (sampling && (sampling->top_k < 1 || sampling->top_k > (uint32_t)kCandidates)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_generate_variants: top_k outside 1..64");
+  }
+  // Each variant's table placed at the prompt's last position, as
+  // frz_generate places one; none acts before it, so the prompt but its
+  // last token is one prefix for all.
+  const uint32_t origin = prompt_len - 1;
+  std::vector<std::vector<uint32_t>> placed(variants);
+  uint32_t stride = 2 * c.layers;
+  for (uint32_t v = 0; v < variants; ++v) {
+    placed[v] = place_table(c, edit_tables ? edit_tables + (size_t)v * table_words : nullptr,
+                            edit_tables ? table_words : 0, origin);
+    if (int rc = check_table(c, placed[v], "frz_generate_variants")) return rc;
+    stride = std::max<uint32_t>(stride, (uint32_t)placed[v].size());
+  }
+  // The shared prefix through the model's own caches, reusing what they hold.
+  const std::vector<uint32_t> none = place_table(c, nullptr, 0, origin);
+  if (int rc = frz_model_set_edits(m, none.data(), (uint32_t)none.size())) return rc;
+  uint32_t common = 0;
+  while (common < m->cached.size() && common < origin && m->cached[common] == prompt[common])
+    ++common;
+  common = std::min(common, first_edit_difference(c, m->cached_edits, none));
+  if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
+  for (uint32_t pos = common; pos < origin;) {
+    const uint32_t n = std::min<uint32_t>(kPrefillBlock, origin - pos);
+    if (int rc = model_step(m, pos, n, prompt + pos, 0, sampling)) return rc;
+    pos += n;
+  }
+  m->cached.assign(prompt, prompt + origin);
+  m->cached_edits = none;
+  m->written_end = origin;
+  if (int rc = ensure_variants(m, (int)variants, max_tokens, stride, residuals_out != nullptr))
+    return rc;
+  frz_model::Variants& V = m->variants;
+  V.capture = residuals_out != nullptr;
+  hipStream_t s = m->dev->stream;
+  // Every variant's caches start as the prefix's.
+  const size_t kvw = (size_t)c.kv_heads * c.head_dim;
+  for (int l = 0; l < c.layers; ++l) {
+    const Layer& L = m->layers[l];
+    const size_t bytes = (size_t)L.slots * kvw * 2, elems = (size_t)L.slots * kvw;
+    for (uint32_t v = 0; v < variants; ++v) {
+      if (int rc = check_hip(hipMemcpyAsync(V.kcache[l] + v * elems, L.kcache, bytes,
+                                            hipMemcpyDeviceToDevice, s),
+                             "variant keys"))
+        return rc;
+      if (int rc = check_hip(hipMemcpyAsync(V.vcache[l] + v * elems, L.vcache, bytes,
+                                            hipMemcpyDeviceToDevice, s),
+                             "variant values"))
+        return rc;
+    }
+  }
+  std::vector<uint32_t> tables((size_t)variants * V.edit_stride, 0);
+  for (uint32_t v = 0; v < variants; ++v)
+    std::copy(placed[v].begin(), placed[v].end(), tables.begin() + (size_t)v * V.edit_stride);
+  if (int rc = check_hip(hipMemcpyAsync(V.edits, tables.data(), tables.size() * 4,
+                                        hipMemcpyHostToDevice, s),
+                         "variant tables"))
+    return rc;
+  // Step 0: every variant's row of the prompt's last token; its draw is each
+  // variant's first token. The selection advances the step, so each later
+  // step feeds every row its own draw.
+  DevStep& st = *m->step_host;
+  std::memset(&st, 0, sizeof st);
+  st.position = origin;
+  st.tokens = variants;
+  st.logits = 1;
+  st.variants = 1;
+  fill_sampling(st, sampling);
+  for (uint32_t v = 0; v < variants; ++v) st.ids[v] = prompt[origin];
+  if (int rc = put_step(m)) return rc;
+  for (uint32_t t = 0; t < max_tokens; ++t) {
+    if (int rc = enqueue_rows(m, (int)variants, true, &V)) return rc;
+  }
+  std::vector<uint32_t> log((size_t)max_tokens * variants * 2);
+  if (int rc = check_hip(hipMemcpyAsync(log.data(), V.token_log, log.size() * 4,
+                                        hipMemcpyDeviceToHost, s),
+                         "variant tokens"))
+    return rc;
+  if (residuals_out) {
+    const size_t n = (size_t)max_tokens * c.layers * variants * c.hidden;
+    if (int rc = check_hip(hipMemcpyAsync(residuals_out, V.residuals, n * 4,
+                                          hipMemcpyDeviceToHost, s),
+                           "variant residuals"))
+      return rc;
+  }
+  if (int rc = check_hip(hipStreamSynchronize(s), "variants sync")) return rc;
+  // Each variant's reply as frz_generate ends one: at a failed draw or a
+  // stop token, which it keeps.
+  for (uint32_t v = 0; v < variants; ++v) {
+    uint32_t n = 0;
+    for (uint32_t t = 0; t < max_tokens; ++t) {
+      const uint32_t token = log[2 * ((size_t)t * variants + v)];
+      const uint32_t failed = log[2 * ((size_t)t * variants + v) + 1];
+      tokens_out[(size_t)v * max_tokens + n++] = token;
+      if (failed || std::find(stop_ids, stop_ids + stops, token) != stop_ids + stops) break;
+    }
+    drawn_out[v] = n;
+  }
   return FRZ_OK;
 }
 

@@ -429,7 +429,8 @@ template <int NB, bool GATED, int F = kQ4_0>
 __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
     const DevStep* __restrict__ step, QMatrix w, QMatrix up,
     const float* __restrict__ x, int x_stride, uint32_t x_bytes, float* __restrict__ y,
-    int y_stride, const uint32_t* __restrict__ edits, int layer, const Schedule<NB> S) {
+    int y_stride, const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride,
+    const Schedule<NB> S) {
   using M = Mfma<NB>;
   constexpr int D = M::kDim;
   constexpr int SL = M::kSlots;
@@ -494,7 +495,9 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   if (tok >= tokens) return;
   float* yrow = y + (size_t)tok * y_stride;
   const int row0 = blockIdx.x * D;
-  const uint32_t position = step->position + (uint32_t)tok;
+  // A variants step: every row at the step's position, under its own table.
+  const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tok);
+  if (edits && step->variants) edits += (size_t)tok * edit_stride;
 #pragma unroll
   for (int o = 0; o < SL; ++o) {
     const int n = row0 + M::slot_row(lane, o);
@@ -544,7 +547,7 @@ bool build_schedule(int groups, Schedule<NB>& S) {
 template <int NB, bool GATED, int F = kQ4_0>
 hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
                          const float* x, int x_stride, float* y, int y_stride, int max_tokens,
-                         const uint32_t* edits, int layer) {
+                         const uint32_t* edits, int layer, uint32_t edit_stride = 0) {
   constexpr int D = Mfma<NB>::kDim;
   const int groups = w.cols >> 5;
   const uint64_t x_bytes = 4ull * (uint64_t)x_stride * (uint64_t)max_tokens;
@@ -556,7 +559,7 @@ hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix 
   }
   const dim3 grid((w.rows + D - 1) / D, (max_tokens + kTileWaves * D - 1) / (kTileWaves * D));
   hipLaunchKernelGGL((gemm_ranges<NB, GATED, F>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
-                     x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, S);
+                     x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, S);
   return hipGetLastError();
 }
 
@@ -601,7 +604,7 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
 
 hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
                         QMatrix up, const float* x, float* act,
-                        int max_tokens, const uint32_t* edits, int layer) {
+                        int max_tokens, const uint32_t* edits, int layer, uint32_t edit_stride) {
   if (gate.cols % 32 != 0 || gate.rows != up.rows || gate.cols != up.cols ||
       gate.format != kQ4_0 || up.format != kQ4_0)
     return hipErrorInvalidValue;
@@ -611,7 +614,7 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
     return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
   }
   return launch_ranges<2, true>(s, step, gate, up, x, gate.cols, act, gate.rows, max_tokens, edits,
-                               layer);
+                               layer, edit_stride);
 }
 
 }  // namespace frz

@@ -31,7 +31,11 @@ struct DevStep {
   float min_p;
   float log_min_p;
   uint32_t drawn;     // draws recorded so far (index into the token log)
-  uint32_t pad[4];
+  // Nonzero: the rows are `tokens` sequences (variants) at one position,
+  // row r with its own caches and edit table, fed from its own draw
+  // (record r); zero: the rows are one sequence's positions position + r.
+  uint32_t variants;
+  uint32_t pad[3];
   uint32_t ids[kPrefillBlock];
 };
 
@@ -68,9 +72,11 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
                        int max_tokens, bool last_token);
 // act[t][j] = gelu_tanh(gate_j) * up_j, then layer `layer`'s pins at the
 // row's position (edit table in the reference's layout; null for none).
+// A variants step gives row r the table at edits + r * edit_stride words.
 hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
                         QMatrix up, const float* x, float* act,
-                        int max_tokens, const uint32_t* edits, int layer);
+                        int max_tokens, const uint32_t* edits, int layer,
+                        uint32_t edit_stride = 0);
 
 // The input row of a decode product, made in the product's prologue.
 // mode 0: x as given. mode 1: hidden + post-norm(output) (written to
@@ -113,6 +119,10 @@ struct NormArgs {
   float epsilon;
   int width;
   bool last_token;         // only the step's last row
+  // Not null: hidden after the add (the residual entering the layer) is also
+  // written to capture + step.drawn * capture_step + row * width.
+  float* capture = nullptr;
+  size_t capture_step = 0;
 };
 hipError_t launch_norm(hipStream_t s, const DevStep* step, const NormArgs& a,
                        int max_tokens);
@@ -133,6 +143,7 @@ struct RopeArgs {
   int query_heads;
   int kv_heads;
   float epsilon;
+  size_t cache_stride = 0;  // elements from one variant's cache to the next
 };
 hipError_t launch_rope(hipStream_t s, const DevStep* step, const RopeArgs& a,
                        int max_tokens);
@@ -152,6 +163,7 @@ struct AttentionArgs {
   int kv_heads;
   int max_chunks;             // chunks a row may reach: the grid's width
   float scale_log2e;
+  size_t cache_stride = 0;    // elements from one variant's cache to the next
 };
 hipError_t launch_attention(hipStream_t s, const DevStep* step,
                             const AttentionArgs& a, int max_tokens);
@@ -210,6 +222,13 @@ hipError_t launch_topk(hipStream_t s, const float* logits, int count,
 hipError_t launch_select(hipStream_t s, DevStep* step, const float* logits, int count,
                          uint32_t* scratch, uint32_t* candidates, uint32_t* sampled,
                          uint32_t* token_log, bool advance);
+// A variants step's selection: for each of `rows` rows of logits (count
+// apart), its top-64 into candidates + 128 r and its draw into record r of
+// sampled (token_log entry drawn * rows + r); then the step's advance to
+// the next position, every row fed from its own record.
+hipError_t launch_select_rows(hipStream_t s, DevStep* step, const float* logits, int count,
+                              int rows, uint32_t* scratch, uint32_t* candidates,
+                              uint32_t* sampled, uint32_t* token_log);
 // The draw: record {token, failed, u bits, 0} into sampled; also appends
 // the token to token_log[step.drawn] when token_log is not null.
 hipError_t launch_draw(hipStream_t s, const DevStep* step,

@@ -84,11 +84,16 @@ __device__ __forceinline__ uint64_t merge_waves(uint64_t top, uint64_t (*lists)[
   return top;
 }
 
-// Pass one: the top 64 of each tile of 1,024 logits, sorted.
+// Pass one: the top 64 of each tile of 1,024 logits, sorted. Row y of the
+// grid reads in + y * in_stride and writes out + y * out_stride (words).
 __global__ __launch_bounds__(kTileThreads) void topk_tile_kernel(const uint32_t* __restrict__ in,
                                                                  int count,
-                                                                 uint32_t* __restrict__ out) {
+                                                                 uint32_t* __restrict__ out,
+                                                                 size_t in_stride,
+                                                                 size_t out_stride) {
   __shared__ uint64_t lists[kTileThreads / 64][64];
+  in += blockIdx.y * in_stride;
+  out += blockIdx.y * out_stride;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int base = blockIdx.x * kSelectionTile + wave * 4 * 64 + lane;
   uint64_t v[4];
@@ -127,8 +132,11 @@ __device__ __forceinline__ uint64_t merge_lists(const uint32_t* __restrict__ in,
 
 __global__ __launch_bounds__(64 * kMergeWaves) void topk_merge_kernel(const uint32_t* __restrict__ in,
                                                                       int lists,
-                                                                      uint32_t* __restrict__ out) {
+                                                                      uint32_t* __restrict__ out,
+                                                                      size_t stride) {
   __shared__ uint64_t shared[kMergeWaves][64];
+  in += blockIdx.y * stride;
+  out += blockIdx.y * stride;
   const uint64_t top = merge_lists(in, lists, shared);
   if (threadIdx.x < 64) store_entry(out, blockIdx.x * kCandidates + threadIdx.x, top);
 }
@@ -144,8 +152,10 @@ __device__ __forceinline__ uint32_t mulhi16(uint32_t a, uint32_t b) {
 // The draw (draw.wgsl:77-170), by one lane: every sum the reference takes
 // runs in candidate order on one invocation there too, and the per-candidate
 // exponentials are independent, so one lane gives the same bits.
+// Row `row` of `rows`: a variants step's rows are sequences at one position,
+// each drawing as its own one-token step would.
 __device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __restrict__ sampled,
-                         uint32_t* __restrict__ token_log) {
+                         uint32_t* __restrict__ token_log, uint32_t row = 0, uint32_t rows = 1) {
   const uint32_t k = min(step->top_k, (uint32_t)kCandidates);
   const bool use_top_p = step->top_p < 1.0f;
   const float temperature = step->temperature;
@@ -167,7 +177,7 @@ __device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __
     }
   }
   // Philox4x32-10 at counter (position + tokens, 0, 0, 0), key = seed.
-  uint32_t c0 = step->position + step->tokens, c1 = 0, c2 = 0, c3 = 0;
+  uint32_t c0 = step->position + (step->variants ? 1u : step->tokens), c1 = 0, c2 = 0, c3 = 0;
   uint32_t k0 = step->seed[0], k1 = step->seed[1];
   for (int r = 0; r < 10; ++r) {
     const uint32_t hi0 = mulhi16(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
@@ -217,8 +227,9 @@ __device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __
   sampled[2] = float_to_bits(u);
   sampled[3] = 0u;
   if (token_log) {
-    token_log[2 * step->drawn] = token;
-    token_log[2 * step->drawn + 1] = failed ? 1u : 0u;
+    const size_t at = 2 * ((size_t)step->drawn * rows + row);
+    token_log[at] = token;
+    token_log[at + 1] = failed ? 1u : 0u;
   }
 }
 
@@ -242,13 +253,29 @@ __global__ void advance_kernel(DevStep* step) {
   if (threadIdx.x == 0) advance_one(step);
 }
 
+// A variants step's advance: the next position, every row fed.
+__global__ void advance_rows_kernel(DevStep* step) {
+  if (threadIdx.x == 0) {
+    step->position += 1;
+    step->fed = 1;
+    step->logits = 1;
+    step->drawn += 1;
+  }
+}
+
 // The last merge (at most kListsPerMerge lists), the draw from its list and,
 // for a fed decode step, the advance.
+// Row y of the grid (rows of a variants step) merges in + y * stride and
+// draws into record y.
 __global__ __launch_bounds__(64 * kMergeWaves) void topk_draw_kernel(
     const uint32_t* __restrict__ in, int lists, uint32_t* __restrict__ cand, DevStep* step,
-    uint32_t* __restrict__ sampled, uint32_t* __restrict__ token_log, int advance) {
+    uint32_t* __restrict__ sampled, uint32_t* __restrict__ token_log, int advance,
+    size_t stride) {
   __shared__ uint64_t shared[kMergeWaves][64];
   __shared__ uint32_t final_list[2 * kCandidates];
+  const uint32_t row = blockIdx.y;
+  in += row * stride;
+  cand += 2 * kCandidates * row;
   const uint64_t top = merge_lists(in, lists, shared);
   if (threadIdx.x < 64) {
     store_entry(cand, threadIdx.x, top);
@@ -256,46 +283,52 @@ __global__ __launch_bounds__(64 * kMergeWaves) void topk_draw_kernel(
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    draw_one(step, final_list, sampled, token_log);
+    draw_one(step, final_list, sampled + 4 * row, token_log, row, gridDim.y);
     if (advance) advance_one(step);
   }
 }
 
 // Pass one into scratch, then merges of kListsPerMerge lists a workgroup
 // until one list is left; `last` launches the final merge.
-template <typename Last>
-hipError_t select_passes(hipStream_t s, const float* logits, int count, uint32_t* scratch,
-                         Last last) {
-  if (count < kCandidates) return hipErrorInvalidValue;
-  int lists = (count + kSelectionTile - 1) / kSelectionTile;
-  uint32_t* bufs[2] = {scratch, scratch + 2 * kCandidates * lists};
-  hipLaunchKernelGGL(topk_tile_kernel, dim3(lists), dim3(kTileThreads), 0, s,
-                     reinterpret_cast<const uint32_t*>(logits), count, bufs[0]);
-  hipError_t e = hipGetLastError();
-  int at = 0;
-  while (e == hipSuccess && lists > kListsPerMerge) {
-    const int groups = (lists + kListsPerMerge - 1) / kListsPerMerge;
-    hipLaunchKernelGGL(topk_merge_kernel, dim3(groups), dim3(64 * kMergeWaves), 0, s, bufs[at],
-                       lists, bufs[at ^ 1]);
-    e = hipGetLastError();
-    lists = groups;
-    at ^= 1;
-  }
-  return e == hipSuccess ? last(bufs[at], lists) : e;
-}
-
-}  // namespace
-
-size_t topk_scratch_words(int count) {
+size_t scratch_words(int count) {
   const int lists = (count + kSelectionTile - 1) / kSelectionTile;
   return (size_t)2 * kCandidates * (lists + (lists + kListsPerMerge - 1) / kListsPerMerge);
 }
 
+// `rows` rows of `count` logits, each with its own scratch_words(count)
+// words of scratch.
+template <typename Last>
+hipError_t select_passes(hipStream_t s, const float* logits, int count, int rows,
+                         uint32_t* scratch, Last last) {
+  if (count < kCandidates || rows < 1) return hipErrorInvalidValue;
+  int lists = (count + kSelectionTile - 1) / kSelectionTile;
+  const size_t stride = scratch_words(count);
+  uint32_t* bufs[2] = {scratch, scratch + 2 * kCandidates * lists};
+  hipLaunchKernelGGL(topk_tile_kernel, dim3(lists, rows), dim3(kTileThreads), 0, s,
+                     reinterpret_cast<const uint32_t*>(logits), count, bufs[0], (size_t)count,
+                     stride);
+  hipError_t e = hipGetLastError();
+  int at = 0;
+  while (e == hipSuccess && lists > kListsPerMerge) {
+    const int groups = (lists + kListsPerMerge - 1) / kListsPerMerge;
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(groups, rows), dim3(64 * kMergeWaves), 0, s,
+                       bufs[at], lists, bufs[at ^ 1], stride);
+    e = hipGetLastError();
+    lists = groups;
+    at ^= 1;
+  }
+  return e == hipSuccess ? last(bufs[at], lists, stride) : e;
+}
+
+}  // namespace
+
+size_t topk_scratch_words(int count) { return scratch_words(count); }
+
 hipError_t launch_topk(hipStream_t s, const float* logits, int count,
                        uint32_t* scratch, uint32_t* candidates) {
-  return select_passes(s, logits, count, scratch, [&](const uint32_t* in, int lists) {
+  return select_passes(s, logits, count, 1, scratch, [&](const uint32_t* in, int lists, size_t) {
     hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(64 * kMergeWaves), 0, s, in, lists,
-                       candidates);
+                       candidates, (size_t)0);
     return hipGetLastError();
   });
 }
@@ -303,11 +336,25 @@ hipError_t launch_topk(hipStream_t s, const float* logits, int count,
 hipError_t launch_select(hipStream_t s, DevStep* step, const float* logits, int count,
                          uint32_t* scratch, uint32_t* candidates, uint32_t* sampled,
                          uint32_t* token_log, bool advance) {
-  return select_passes(s, logits, count, scratch, [&](const uint32_t* in, int lists) {
+  return select_passes(s, logits, count, 1, scratch, [&](const uint32_t* in, int lists, size_t) {
     hipLaunchKernelGGL(topk_draw_kernel, dim3(1), dim3(64 * kMergeWaves), 0, s, in, lists,
-                       candidates, step, sampled, token_log, advance ? 1 : 0);
+                       candidates, step, sampled, token_log, advance ? 1 : 0, (size_t)0);
     return hipGetLastError();
   });
+}
+
+hipError_t launch_select_rows(hipStream_t s, DevStep* step, const float* logits, int count,
+                              int rows, uint32_t* scratch, uint32_t* candidates,
+                              uint32_t* sampled, uint32_t* token_log) {
+  hipError_t e = select_passes(
+      s, logits, count, rows, scratch, [&](const uint32_t* in, int lists, size_t stride) {
+        hipLaunchKernelGGL(topk_draw_kernel, dim3(1, rows), dim3(64 * kMergeWaves), 0, s, in,
+                           lists, candidates, step, sampled, token_log, 0, stride);
+        return hipGetLastError();
+      });
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(advance_rows_kernel, dim3(1), dim3(64), 0, s, step);
+  return hipGetLastError();
 }
 
 hipError_t launch_draw(hipStream_t s, const DevStep* step, const uint32_t* candidates,

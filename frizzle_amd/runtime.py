@@ -317,6 +317,42 @@ class Model:
                                     len(stop_ids), out.ctypes.data, byref(drawn)))
         return out[:drawn.value].copy()
 
+    def generate_variants(self, prompt, variants, samp=None, max_tokens=16, stop_ids=(),
+                          residuals=False):
+        """Many replies to one prompt decoded together: variants is a list of
+        Edit lists (ranges in steps), one a variant. Returns a list of token
+        arrays (each what generate() gives for that variant's edits) and,
+        with residuals, a [max_tokens, layers, variants, hidden] array of the
+        residual entering each layer at each step."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        tables = []
+        for edits in variants:
+            edits = list(edits)
+            if edits:
+                err, idx = edit_check(edits, self.cfg.layers, self.cfg.ffn)
+                if err != EditError.OK:
+                    raise ValueError(f"edit {idx} refused: {err.name}")
+                tables.append(edit_table(edits, self.cfg.layers, 0))
+            else:
+                tables.append(np.zeros(2 * self.cfg.layers, dtype=np.uint32))
+        words = max(t.size for t in tables)
+        packed = np.zeros((len(tables), words), dtype=np.uint32)
+        for i, t in enumerate(tables):
+            packed[i, :t.size] = t
+        n = len(tables)
+        stops = np.ascontiguousarray(list(stop_ids) or [0], dtype=np.uint32)
+        out = np.zeros((n, max_tokens), dtype=np.uint32)
+        drawn = np.zeros(n, dtype=np.uint32)
+        res = (np.empty((max_tokens, self.cfg.layers, n, self.cfg.hidden), dtype=np.float32)
+               if residuals else None)
+        s = samp or sampling()
+        check(self.lib.frz_generate_variants(
+            self.handle, prompt.ctypes.data, prompt.size, n, packed.ctypes.data, words, byref(s),
+            max_tokens, stops.ctypes.data, len(stop_ids), out.ctypes.data, drawn.ctypes.data,
+            res.ctypes.data if residuals else None))
+        replies = [out[v, :drawn[v]].copy() for v in range(n)]
+        return (replies, res) if residuals else replies
+
     def paired(self, prompt, edits, samp=None, max_tokens=16, stop_ids=()):
         """The native tool's paired runs (tools/frizzle/main.cpp:53-55): the
         original reply, then the steered one from the same seed, sharing the

@@ -365,6 +365,31 @@ int frz_generate(frz_model* model, const uint32_t* prompt, uint32_t prompt_len,
                  const frz_sampling* sampling, uint32_t max_tokens,
                  const uint32_t* stop_ids, uint32_t stops,
                  uint32_t* tokens_out, uint32_t* drawn);
+/* Many continuations of one prompt at once: an original and steered
+ * variants of it from one seed, decoded as one batch. The reference runs
+ * such replies one at a time (the paired runs of tools/frizzle/main.cpp:
+ * 53-55 through runtime/engine.h:60-139); this runs them together. Variant
+ * v runs under its own edit table,
+ * edit_tables + v * table_words words in frz_edit_table's layout with
+ * ranges in steps, placed at the prompt's last position as frz_generate
+ * places one; all share `sampling`. The prompt but its last token is
+ * computed once, through the model's own caches (and reused as frz_generate
+ * reuses it); each variant then gets a copy of those caches, and every step
+ * runs one token of every variant through each product together. Variant
+ * v's tokens are the ones frz_generate gives for its table alone, bit for
+ * bit, ending likewise at a stop token or a failed draw:
+ * tokens_out[v * max_tokens ...], drawn_out[v] of them. residuals_out, when
+ * not null, receives [max_tokens][layers][variants][hidden] floats: at each
+ * step, the residual entering each layer (the hidden row after the add of
+ * the layer's first norm; layer 0's is the embedding row), as the capture
+ * store defines it (src/core/capture/capture.h:15-17). 1 to 64 variants. */
+int frz_generate_variants(frz_model* model, const uint32_t* prompt,
+                          uint32_t prompt_len, uint32_t variants,
+                          const uint32_t* edit_tables, uint32_t table_words,
+                          const frz_sampling* sampling, uint32_t max_tokens,
+                          const uint32_t* stop_ids, uint32_t stops,
+                          uint32_t* tokens_out, uint32_t* drawn_out,
+                          float* residuals_out);
 
 /* ---- GGUF files (replaces the reference's gguf::read_index and the
  *      Gemma 3 load, src/core/gguf/reader.h:12-107, index.h,

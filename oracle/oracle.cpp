@@ -694,6 +694,7 @@ struct orc_model {
   std::vector<std::vector<float>> turns;
   std::vector<uint32_t> edits;
   std::vector<float> hidden, normed, output, q, k, v, attn, act;
+  std::vector<float> residuals;  // [layers][hidden]: the last token's
 };
 
 orc_model* orc_model_create(const orc_config* config,
@@ -727,6 +728,7 @@ orc_model* orc_model_create(const orc_config* config,
   m->v.resize(kvw);
   m->attn.resize(c.query_heads * c.head_dim);
   m->act.resize(c.ffn);
+  m->residuals.resize(static_cast<size_t>(c.layers) * c.hidden);
   return m;
 }
 
@@ -759,6 +761,10 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
     orc_norm_row(w.attn_norm, pending, pending != nullptr, pending != nullptr,
                  1.0f, c.epsilon, H, m->hidden.data(), m->output.data(),
                  m->normed.data());
+    // The residual entering layer l: X after the add its first norm makes
+    // (capture.h:15-17), layer 0's the embedding row.
+    std::copy(m->hidden.begin(), m->hidden.end(),
+              m->residuals.begin() + static_cast<size_t>(l) * H);
     orc_gemv(w.q, qw, H, m->normed.data(), m->q.data());
     orc_gemv(w.k, kvw, H, m->normed.data(), m->k.data());
     orc_gemv(w.v, kvw, H, m->normed.data(), m->v.data());
@@ -785,6 +791,7 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
 }
 
 const float* orc_model_normed(const orc_model* m) { return m->normed.data(); }
+const float* orc_model_residuals(const orc_model* m) { return m->residuals.data(); }
 const uint16_t* orc_model_key_cache(const orc_model* m, int layer) {
   return m->kcache[layer].data();
 }

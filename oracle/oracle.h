@@ -175,6 +175,9 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
                      float* logits);
 /* The last layer's output row after the final norm (hidden floats). */
 const float* orc_model_normed(const orc_model* m);
+/* [layers][hidden]: for the last token, the residual entering each layer
+ * (X after the add of the layer's first norm; layer 0's is the embedding). */
+const float* orc_model_residuals(const orc_model* m);
 /* Read access to layer l's F16 key and value cache, slots x kv x head_dim. */
 const uint16_t* orc_model_key_cache(const orc_model* m, int layer);
 const uint16_t* orc_model_value_cache(const orc_model* m, int layer);

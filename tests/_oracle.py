@@ -69,6 +69,7 @@ _SIGS = {
     "orc_model_set_edits": (None, [_P, _P, c_int]),
     "orc_model_token": (None, [_P, c_uint32, c_int, _P]),
     "orc_model_normed": (c_void_p, [_P]),
+    "orc_model_residuals": (c_void_p, [_P]),
     "orc_model_key_cache": (c_void_p, [_P, c_int]),
     "orc_model_value_cache": (c_void_p, [_P, c_int]),
     "orc_model_slots": (c_int, [_P, c_int]),
@@ -249,6 +250,13 @@ class OracleModel:
     def normed(self):
         ptr = lib().orc_model_normed(self.handle)
         return np.ctypeslib.as_array((c_float * self.cfg.hidden).from_address(ptr)).copy()
+
+    def residuals(self):
+        """[layers][hidden]: the last token's residual entering each layer."""
+        ptr = lib().orc_model_residuals(self.handle)
+        n = self.cfg.layers * self.cfg.hidden
+        return np.ctypeslib.as_array((c_float * n).from_address(ptr)).copy().reshape(
+            self.cfg.layers, self.cfg.hidden)
 
     def close(self):
         if self.handle:
