@@ -64,6 +64,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--parity-tokens", type=int, default=256)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-steered", action="store_true",
+                   help="skip the batch of 16 steered variants")
+    p.add_argument("--steered-only", action="store_true",
+                   help="only the batch of 16 steered variants (one JSON line)")
     p.add_argument("--no-pinned", action="store_true",
                    help="skip the decode over the pinned file's Q8_0/Q4_1 formats")
     p.add_argument("--eager", action="store_true",
@@ -220,6 +224,46 @@ def pinned_formats(fz, model, cfg, seed):
         model.set_tensor(layer, "down", blocks(cfg.hidden, cfg.ffn, fz.Q4_1), fz.Q4_1)
 
 
+def steered_batch(fz, model, dev, cfg, seed, prompt_len=1024, variants=16, tokens=128):
+    """One original and variants - 1 steered replies to one seeded prompt,
+    decoded as one batch at temperature 1 from one seed; each steered variant
+    pins 1 to 32 seeded neurons of seeded layers to values in [-20, 20]. The
+    second run reuses the cached prompt, so it times the cache copies and
+    the batched decode; the residual capture ([tokens][layers][variants]
+    [hidden] floats) is written in one run and copied to the host."""
+    rng = np.random.default_rng(seed + 9)
+    prompt = rng.integers(0, cfg.vocab, prompt_len).astype(np.uint32)
+    sets = [[]]
+    for _ in range(variants - 1):
+        pins = {}
+        for _ in range(int(rng.integers(1, 33))):
+            layer, neuron = int(rng.integers(0, cfg.layers)), int(rng.integers(0, cfg.ffn))
+            pins[(layer, neuron)] = fz.Edit(layer, neuron, fz.EditKind.SET,
+                                            float(rng.uniform(-20, 20)))
+        sets.append(list(pins.values()))
+    samp = fz.sampling(temperature=1.0, top_k=64, top_p=1.0, min_p=0.0, seed=0x5EED)
+    model.generate_variants(prompt, sets, samp=samp, max_tokens=tokens)  # prompt, warm-up
+    dev.sync()
+    t0 = time.perf_counter()
+    replies = model.generate_variants(prompt, sets, samp=samp, max_tokens=tokens)
+    dev.sync()
+    plain = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    replies_r, res = model.generate_variants(prompt, sets, samp=samp, max_tokens=tokens,
+                                             residuals=True)
+    dev.sync()
+    captured = time.perf_counter() - t0
+    same = all(np.array_equal(a, b) for a, b in zip(replies, replies_r))
+    drawn = sum(len(r) for r in replies)
+    return {"workload": f"1 original + {variants - 1} steered variants of one {prompt_len}-token "
+                        f"seeded prompt, {tokens} tokens each at temperature 1.0 from one seed, "
+                        "decoded as one batch (1-32 seeded pins in [-20, 20] a variant)",
+            "tok_per_s": drawn / plain, "ms_per_step": plain * 1e3 / tokens,
+            "tok_per_s_with_residuals": drawn / captured,
+            "residual_bytes": int(res.nbytes), "tokens": drawn,
+            "replies_identical_with_capture": bool(same)}
+
+
 def timed_decode(model, dev, prompt, warmup, steps, greedy):
     """The prompt in 512-token steps, `warmup` decode steps, then `steps`
     timed ones: (prefill seconds, wall seconds, µs/step by HIP events)."""
@@ -279,6 +323,12 @@ def main():
         model.set_graphs(False)
     greedy = fz.sampling()
 
+    if args.steered_only:
+        out = steered_batch(fz, model, dev, cfg, args.seed)
+        model.close()
+        dev.close()
+        print(json.dumps({"steered_only": True, **out}))
+        return
     if args.prefill_only:
         args.no_cpu = True
     # Full-size parity sample: the oracle decodes from a short prompt on the
@@ -340,6 +390,14 @@ def main():
     log(f"decode {args.steps} steps: {ms_per_step * 1000:.1f} us/step wall, "
         f"{us_events:.1f} us/step events")
 
+    # Config 5: the batch of steered variants.
+    steered = None
+    if not args.no_steered:
+        steered = steered_batch(fz, model, dev, cfg, args.seed)
+        log(f"steered batch: {steered['tok_per_s']:.0f} tok/s, "
+            f"{steered['ms_per_step']:.2f} ms a step; with residuals "
+            f"{steered['tok_per_s_with_residuals']:.0f} tok/s")
+
     # The same workload over the pinned file's formats (reported beside the
     # Q4_0 figure, which is the metric's).
     pinned = None
@@ -384,6 +442,7 @@ def main():
         "cpu_baseline": cpu_baseline,
         "parity": parity,
         "pinned_formats": pinned,
+        "steered_batch": steered,
         "prefill": {"workload": f"Gemma-3-1B Q4_0 prefill of {PREFILL_TOKENS} seeded ids in "
                                 "512-token steps, logits at the last position",
                     "seconds": prefill_2048, "flop": PREFILL_FLOP,

@@ -214,6 +214,7 @@ struct Schedule {
   int steps;
   uint32_t flags[kMaxSteps / 8];  // 4 bits per step
   uint32_t word[kMaxSteps * kWords];
+  int16_t pass_start[kRanges / NB + 1];  // first step of pass p; steps at the end
 };
 
 // One step's schedule words, read ahead into scalar registers.
@@ -390,6 +391,24 @@ __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepI
   wave_sync();
 }
 
+// A pass's range sums kept apart, when the passes of a tile are split over
+// the workgroup's waves: range NB p + b's sum for output (row, token) at
+// sums[(NB p + b) D^2 + row D + token].
+template <int NB>
+__device__ __forceinline__ void store_pass(typename Mfma<NB>::Acc& acc, float* sums, int pass) {
+  using M = Mfma<NB>;
+  constexpr int S = M::kSlots, D = M::kDim;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int o = 0; o < S; ++o)
+      sums[(NB * pass + b) * D * D + M::slot_row(lane, o) * D + lane % D] = acc[S * b + o];
+  }
+#pragma unroll
+  for (int i = 0; i < NB * S; ++i) acc[i] = 0.0f;
+}
+
 // A pass's range sums join the totals in range order.
 template <int NB>
 __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
@@ -406,27 +425,44 @@ __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
 
 // Step t, with the schedule of steps t .. t + 2 in hand; starts reading
 // step t + 3's (first used a step later, so its wait costs nothing).
-template <int NB, bool GATED, int F>
+template <int NB, bool GATED, int F, bool SPLIT>
 __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedule<NB>& S, int t,
                                          StepInfo<NB> (&I)[4], float4 (&G)[8],
                                          const Weights<GATED, F>& W, Weights<GATED, F>& W_next,
                                          typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
-                                         float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
+                                         float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots],
+                                         float* sums, int& pass) {
+  constexpr int D2 = Mfma<NB>::kDim * Mfma<NB>::kDim;
   I[3] = step_info(S, t + 3);
   chain_step<NB, GATED, F>(T, I[1], I[2], G, W, W_next, acc);
   if (I[0].flags & kCloses) {
 #pragma unroll
-    for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
+    for (int m = 0; m < (GATED ? 2 : 1); ++m) {
+      if constexpr (SPLIT) {
+        store_pass<NB>(acc[m], sums + m * kRanges * D2, pass);
+      } else {
+        close_pass<NB>(acc[m], total[m]);
+      }
+    }
+    ++pass;
   }
   I[0] = I[1];
   I[1] = I[2];
   I[2] = I[3];
 }
 
-// Grid: x = D-row tiles, y = groups of kTileWaves x D tokens. Rows and
-// tokens past the ends are read clamped and not stored.
-template <int NB, bool GATED, int F = kQ4_0>
-__global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
+// Waves of a workgroup that split a tile's passes: one pass (four ranges)
+// a wave.
+constexpr int kSplitWaves = 8;
+
+// Grid: x = D-row tiles, y = groups of kTileWaves x D tokens, a wave's own
+// D tokens. SPLIT (one token tile, of a step of D tokens at most): y = the
+// token tile, and the workgroup's kSplitWaves waves share it, wave w taking
+// the passes from w (kRanges / NB) / kSplitWaves on; their range sums meet
+// in LDS and are added in range order, the same sums in the same order.
+// Rows and tokens past the ends are read clamped and not stored.
+template <int NB, bool GATED, int F = kQ4_0, bool SPLIT = false>
+__global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_ranges(
     const DevStep* __restrict__ step, QMatrix w, QMatrix up,
     const float* __restrict__ x, int x_stride, uint32_t x_bytes, float* __restrict__ y,
     int y_stride, const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride,
@@ -435,11 +471,16 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   constexpr int D = M::kDim;
   constexpr int SL = M::kSlots;
   constexpr int kMats = GATED ? 2 : 1;
-  __shared__ float4 staged[kTileWaves][kXBuf];
+  constexpr int kWaves = SPLIT ? kSplitWaves : kTileWaves;
+  constexpr int kPassesPerWave = (kRanges / NB) / kSplitWaves;
+  static_assert(!SPLIT || (NB == 4 && kPassesPerWave >= 1), "split tiles are 16 x 16");
+  __shared__ float4 staged[kWaves][kXBuf];
+  __shared__ float sums[SPLIT ? kMats * kRanges * D * D : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tokens = (int)step->tokens;
-  const int token0 = (blockIdx.y * kTileWaves + wave) * D;
-  if (token0 >= tokens) return;  // whole waves; the kernel has no barriers
+  const int token0 = SPLIT ? (int)blockIdx.y * D : (int)(blockIdx.y * kTileWaves + wave) * D;
+  // Whole waves (whole workgroups when SPLIT) leave, before any barrier.
+  if (token0 >= tokens) return;
   const int groups = w.cols >> 5;
 
   Tile<NB, GATED> T;
@@ -473,11 +514,15 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
     for (int o = 0; o < SL; ++o) total[m][o] = 0.0f;
   }
 
-  // Step 0 staged; step 1's inputs and step 0's weights in registers.
+  // This wave's steps: all of them, or its passes' when SPLIT.
+  int pass = SPLIT ? wave * kPassesPerWave : 0;
+  const int t0 = SPLIT ? S.pass_start[pass] : 0;
+  const int t1 = SPLIT ? S.pass_start[pass + kPassesPerWave] : S.steps;
+  // Step t0 staged; step t0 + 1's inputs and step t0's weights in registers.
   StepInfo<NB> I[4];
-  I[0] = step_info(S, 0);
-  I[1] = step_info(S, 1);
-  I[2] = step_info(S, 2);
+  I[0] = step_info(S, t0);
+  I[1] = step_info(S, t0 + 1);
+  I[2] = step_info(S, t0 + 2);
   float4 G[8];
   load_inputs(T, I[0], G);
   stage_inputs(T, I[0], G);
@@ -485,10 +530,39 @@ __global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
   Weights<GATED, F> W0, W1;
   load_weights(T, I[0], W0);
   wave_sync();
-  for (int t = 0; t < S.steps; t += 2) {
-    run_step<NB, GATED, F>(T, S, t, I, G, W0, W1, acc, total);
-    if (t + 1 >= S.steps) break;
-    run_step<NB, GATED, F>(T, S, t + 1, I, G, W1, W0, acc, total);
+  for (int t = t0; t < t1; t += 2) {
+    run_step<NB, GATED, F, SPLIT>(T, S, t, I, G, W0, W1, acc, total, sums, pass);
+    if (t + 1 >= t1) break;
+    run_step<NB, GATED, F, SPLIT>(T, S, t + 1, I, G, W1, W0, acc, total, sums, pass);
+  }
+
+  if constexpr (SPLIT) {
+    // Output i of the tile (row i / D, token i % D): its 32 range sums in
+    // range order from +0, as the unsplit close adds them.
+    __syncthreads();
+    if (threadIdx.x >= D * D) return;
+    const int i = threadIdx.x;
+    const int tk = token0 + i % D, n = (int)blockIdx.x * D + i / D;
+    if (tk >= tokens || n >= w.rows) return;
+    float tot[kMats];
+#pragma unroll
+    for (int m = 0; m < kMats; ++m) {
+      tot[m] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kRanges; ++r) tot[m] = tot[m] + sums[(m * kRanges + r) * D * D + i];
+    }
+    float* yr = y + (size_t)tk * y_stride;
+    if (!GATED) {
+      yr[n] = tot[0];
+    } else {
+      const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tk);
+      const uint32_t* table =
+          edits && step->variants ? edits + (size_t)tk * edit_stride : edits;
+      float v = gelu_tanh(tot[0]) * tot[kMats - 1];
+      if (table) v = apply_edits(table, layer, (uint32_t)n, position, v);
+      yr[n] = v;
+    }
+    return;
   }
 
   const int tok = token0 + lane % D;
@@ -520,6 +594,7 @@ bool build_schedule(int groups, Schedule<NB>& S) {
   S = Schedule<NB>{};
   int t = 0;
   for (int p = 0; p < kRanges / NB; ++p) {
+    S.pass_start[p] = (int16_t)t;
     int lo[NB], len[NB], steps = 0;
     for (int b = 0; b < NB; ++b) {
       const int r = NB * p + b;
@@ -541,10 +616,11 @@ bool build_schedule(int groups, Schedule<NB>& S) {
     }
   }
   S.steps = t;
+  S.pass_start[kRanges / NB] = (int16_t)t;
   return t > 0;
 }
 
-template <int NB, bool GATED, int F = kQ4_0>
+template <int NB, bool GATED, int F = kQ4_0, bool SPLIT = false>
 hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
                          const float* x, int x_stride, float* y, int y_stride, int max_tokens,
                          const uint32_t* edits, int layer, uint32_t edit_stride = 0) {
@@ -557,10 +633,21 @@ hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix 
       !build_schedule<NB>(groups, S)) {
     return hipErrorInvalidValue;
   }
-  const dim3 grid((w.rows + D - 1) / D, (max_tokens + kTileWaves * D - 1) / (kTileWaves * D));
-  hipLaunchKernelGGL((gemm_ranges<NB, GATED, F>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
-                     x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, S);
+  // Split passes need every pass to hold work: a range of a group at least.
+  if (SPLIT && groups < kRanges) return hipErrorInvalidValue;
+  const int token_span = SPLIT ? D : kTileWaves * D;
+  const dim3 grid((w.rows + D - 1) / D, (max_tokens + token_span - 1) / token_span);
+  hipLaunchKernelGGL((gemm_ranges<NB, GATED, F, SPLIT>), grid,
+                     dim3((SPLIT ? kSplitWaves : kTileWaves) * 64), 0, s, step, w, up, x,
+                     x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, S);
   return hipGetLastError();
+}
+
+// A step of at most 16 rows over K of 32 groups or more (a batch of variants)
+// fills few waves with one 16 x 16 tile each; such a step splits each tile's
+// passes over a workgroup's waves.
+bool split_passes(const QMatrix& w, int max_tokens) {
+  return max_tokens <= Mfma<4>::kDim && (w.cols >> 5) >= kRanges;
 }
 
 }  // namespace
@@ -578,6 +665,21 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
   // most of the chip's 1,024 SIMDs; else 16 x 16 tiles (four ranges), four
   // times as many.
   const bool wide = (size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024;
+  if (split_passes(w, max_tokens)) {
+    switch (w.format) {
+      case kQ4_0:
+        return launch_ranges<4, false, kQ4_0, true>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
+      case kQ4_1:
+        return launch_ranges<4, false, kQ4_1, true>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
+      case kQ8_0:
+        return launch_ranges<4, false, kQ8_0, true>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
   switch (w.format) {
     case kQ4_0:
       if (wide)
@@ -612,6 +714,10 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
     GemvInput in{};
     in.x = x;
     return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
+  }
+  if (split_passes(gate, max_tokens)) {
+    return launch_ranges<4, true, kQ4_0, true>(s, step, gate, up, x, gate.cols, act, gate.rows,
+                                               max_tokens, edits, layer, edit_stride);
   }
   return launch_ranges<2, true>(s, step, gate, up, x, gate.cols, act, gate.rows, max_tokens, edits,
                                layer, edit_stride);

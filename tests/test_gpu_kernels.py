@@ -105,6 +105,25 @@ def test_gemv_tiled_is_decode_bits(device, rows, cols, tokens):
         assert_same_bits(got[t], orc.gemv(w, rows, cols, x[t]), f"token {t}")
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [(1152, 6912, 16), (1152, 1024, 2), (100, 1152, 1),
+                                               (16384 + 40, 1152, 16), (1536, 1152, 9)])
+def test_gemv_split_passes_bit_exact(device, rows, cols, tokens):
+    # Steps of at most 16 rows split each tile's passes over a workgroup's
+    # waves; the range sums meet in LDS and are added in range order. The
+    # tokens = 1 case is the decode form (last_token).
+    rng = np.random.default_rng(rows + 3 * tokens)
+    w = q4_blocks(rng, rows, cols)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    codes, scales = _q4_dev(device, w)
+    dx = device.array(x)
+    dy = device.empty((tokens, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gemv(device.handle, codes.ptr, scales.ptr, rows, cols,
+                                        dx.ptr, cols, dy.ptr, rows, tokens, 0))
+    got = dy.numpy()
+    for t in range(tokens):
+        assert_same_bits(got[t], orc.gemv(w, rows, cols, x[t]), f"token {t}")
+
+
 def test_gemv_tiled_subnormal_products(device):
     # Products and sums below f32's normal range: the prefill's chains keep
     # subnormals exactly as the reference's fma does.
@@ -166,6 +185,7 @@ def test_gemv_format_decode_bit_exact(device, fmt, rows, cols):
 
 
 @pytest.mark.parametrize("fmt,rows,cols,tokens", [(3, 1152, 6912, 37), (8, 1152, 6912, 37),
+                                                  (3, 1152, 6912, 16), (8, 4096, 1152, 16),
                                                   (3, 200, 96, 3), (8, 200, 96, 3),
                                                   (3, 1600, 1152, 512), (8, 1600, 1152, 512)])
 def test_gemv_format_tiled_bit_exact(device, fmt, rows, cols, tokens):
@@ -213,7 +233,7 @@ def test_gather_q8_0_bit_exact(device):
                          f"row {i}")
 
 
-@pytest.mark.parametrize("tokens", [1, 6, 37])
+@pytest.mark.parametrize("tokens", [1, 6, 16, 37])
 def test_gated_with_pins_bit_exact(device, tokens):
     rng = np.random.default_rng(11 + tokens)
     rows, cols, layers, layer = 6912, 1152, 3, 1
