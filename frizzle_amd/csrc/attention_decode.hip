@@ -15,7 +15,12 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
     const DevStep* __restrict__ step, DecodeAttentionArgs a) {
   __shared__ ChunkShared S;
   __shared__ float cosines[D / 2], sines[D / 2];
-  const int h = blockIdx.y, t = threadIdx.x;
+  const int h = blockIdx.y, t = threadIdx.x, row = blockIdx.z;
+  if (row > 0) {  // a variants step's row: its own token and caches
+    a.qkv += (size_t)row * a.qkv_stride;
+    a.key_cache += (size_t)row * a.cache_stride;
+    a.value_cache += (size_t)row * a.cache_stride;
+  }
   // Rope lanes, 32 a head: the query head h, then the key and the value.
   // Their loads and the turns go first (none depends on the position), the
   // cached rows' after, so the rope waits only for the former.
@@ -73,17 +78,18 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
 #pragma unroll
     for (int m = 0; m < kKeyLoads; ++m) kr[m] = src[m];
   }
-  const size_t slot = (size_t)blockIdx.x * QH + h;
+  const size_t slot = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
   chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
 }
 
 }  // namespace
 
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
-                                   const DecodeAttentionArgs& a) {
-  if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.max_chunks, QH), dim3(kThreads), 0, s, step,
-                     a);
+                                   const DecodeAttentionArgs& a, int rows) {
+  if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1 || rows < 1)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_decode_kernel, dim3(a.max_chunks, QH, rows), dim3(kThreads), 0, s,
+                     step, a);
   return hipGetLastError();
 }
 

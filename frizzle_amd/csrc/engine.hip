@@ -263,18 +263,37 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     e = launch_norm(s, m->step, attn_norm, max_tokens);
     if (e == hipSuccess)
       e = launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens, false);
-    if (e == hipSuccess) {
-      RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     m->qkv + qw,
-                 m->qkv + qw + kvw, qkv_stride, qkv_stride, kcache, vcache,
-                 L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon, cache_stride};
-      e = launch_rope(s, m->step, r, max_tokens);
-    }
-    if (e == hipSuccess) {
-      AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
-                      m->partials, m->partials + m->partial_floats, L.slots, L.window,
-                      c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
-                      cache_stride};
-      e = launch_attention(s, m->step, a, max_tokens);
+    if (v) {
+      // Each variant's row is one decode token: the fused rope and attention
+      // a (chunk, head, row), then each row's fold.
+      if (e == hipSuccess) {
+        DecodeAttentionArgs d{m->qkv,      L.turns,  L.gains[1],  L.gains[2], kcache,
+                              vcache,      m->partials, m->partials + m->partial_floats,
+                              L.slots,     L.window, c.head_dim, c.query_heads, c.kv_heads,
+                              L.max_chunks, c.epsilon, scale_log2e, qkv_stride, cache_stride};
+        e = launch_attention_decode(s, m->step, d, max_tokens);
+      }
+      if (e == hipSuccess) {
+        e = launch_attention_fold(
+            s, m->step,
+            FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window,
+                     L.max_chunks},
+            max_tokens);
+      }
+    } else {
+      if (e == hipSuccess) {
+        RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     m->qkv + qw,
+                   m->qkv + qw + kvw, qkv_stride, qkv_stride, kcache, vcache,
+                   L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon, cache_stride};
+        e = launch_rope(s, m->step, r, max_tokens);
+      }
+      if (e == hipSuccess) {
+        AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
+                        m->partials, m->partials + m->partial_floats, L.slots, L.window,
+                        c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
+                        cache_stride};
+        e = launch_attention(s, m->step, a, max_tokens);
+      }
     }
     if (e == hipSuccess)
       e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);

@@ -645,9 +645,11 @@ hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix 
 
 // A step of at most 16 rows over K of 32 groups or more (a batch of variants)
 // fills few waves with one 16 x 16 tile each; such a step splits each tile's
-// passes over a workgroup's waves.
+// passes over a workgroup's waves, unless the product has tiles enough to
+// fill the chip without (the 262,144-row head has 16,384).
 bool split_passes(const QMatrix& w, int max_tokens) {
-  return max_tokens <= Mfma<4>::kDim && (w.cols >> 5) >= kRanges;
+  return max_tokens <= Mfma<4>::kDim && (w.cols >> 5) >= kRanges &&
+         w.rows <= 2048 * Mfma<4>::kDim;
 }
 
 }  // namespace
@@ -664,7 +666,9 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
   // Tiles of 32 x 32 (two ranges in flight) when they are enough to cover
   // most of the chip's 1,024 SIMDs; else 16 x 16 tiles (four ranges), four
   // times as many.
-  const bool wide = (size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024;
+  // 32 x 32 tiles waste half their columns on 16 tokens or fewer.
+  const bool wide = (size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024 &&
+                    max_tokens > Mfma<4>::kDim;
   if (split_passes(w, max_tokens)) {
     switch (w.format) {
       case kQ4_0:

@@ -187,9 +187,14 @@ struct DecodeAttentionArgs {
   int max_chunks;
   float epsilon;
   float scale_log2e;
+  // A variants step's rows (grid z): row r's q, k, v at qkv + r * qkv_stride,
+  // its caches cache_stride elements on, its chunk states after row r - 1's
+  // max_chunks (the fold's layout).
+  int qkv_stride = 0;
+  size_t cache_stride = 0;
 };
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
-                                   const DecodeAttentionArgs& a);
+                                   const DecodeAttentionArgs& a, int rows = 1);
 
 // Each row's chunk states folded in chunk order into out[row][heads * d].
 struct FoldArgs {

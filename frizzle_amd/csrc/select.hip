@@ -149,33 +149,40 @@ __device__ __forceinline__ uint32_t mulhi16(uint32_t a, uint32_t b) {
   return p11 + (p01 >> 16) + (p10 >> 16) + (mid >> 16);
 }
 
-// The draw (draw.wgsl:77-170), by one lane: every sum the reference takes
-// runs in candidate order on one invocation there too, and the per-candidate
-// exponentials are independent, so one lane gives the same bits.
+// The draw (draw.wgsl:77-170). The per-candidate exponentials are
+// independent: candidate i's by thread i, into LDS. Every sum the reference
+// takes runs in candidate order on one invocation there too, so thread 0
+// takes them in that order and gives the same bits. Every thread of the
+// workgroup calls it (it holds a barrier).
 // Row `row` of `rows`: a variants step's rows are sequences at one position,
 // each drawing as its own one-token step would.
 __device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __restrict__ sampled,
                          uint32_t* __restrict__ token_log, uint32_t row = 0, uint32_t rows = 1) {
+  __shared__ float weight[kCandidates], tempered[kCandidates], running[kCandidates];
+  __shared__ uint32_t above[kCandidates];
   const uint32_t k = min(step->top_k, (uint32_t)kCandidates);
   const bool use_top_p = step->top_p < 1.0f;
   const float temperature = step->temperature;
   const uint32_t first_bits = cand[0];
   const bool failed = (first_bits & 0x7F800000u) == 0x7F800000u;
-  float weight[kCandidates], tempered[kCandidates], running[kCandidates];
-  uint32_t above[kCandidates];
   const float first = bits_to_float(first_bits);
-  for (uint32_t i = 0; i < k; ++i) {
-    weight[i] = 0.0f;
-    tempered[i] = 0.0f;
-    above[i] = 0u;
+  if (threadIdx.x < k) {
+    const uint32_t i = threadIdx.x;
+    float w = 0.0f, te = 0.0f;
+    uint32_t ab = 0u;
     const uint32_t mine_bits = cand[2 * i];
     if (!failed && mine_bits != 0xFF800000u) {
       const float mine = bits_to_float(mine_bits);
-      if (use_top_p) weight[i] = exp_nonpositive(mine - first);
-      if (temperature > 0.0f) tempered[i] = exp_nonpositive((mine - first) / temperature);
-      above[i] = (step->min_p == 0.0f || mine >= first + step->log_min_p) ? 1u : 0u;
+      if (use_top_p) w = exp_nonpositive(mine - first);
+      if (temperature > 0.0f) te = exp_nonpositive((mine - first) / temperature);
+      ab = (step->min_p == 0.0f || mine >= first + step->log_min_p) ? 1u : 0u;
     }
+    weight[i] = w;
+    tempered[i] = te;
+    above[i] = ab;
   }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
   // Philox4x32-10 at counter (position + tokens, 0, 0, 0), key = seed.
   uint32_t c0 = step->position + (step->variants ? 1u : step->tokens), c1 = 0, c2 = 0, c3 = 0;
   uint32_t k0 = step->seed[0], k1 = step->seed[1];
@@ -246,7 +253,7 @@ __global__ __launch_bounds__(64) void draw_kernel(const DevStep* __restrict__ st
                                                   const uint32_t* __restrict__ cand,
                                                   uint32_t* __restrict__ sampled,
                                                   uint32_t* __restrict__ token_log) {
-  if (threadIdx.x == 0) draw_one(step, cand, sampled, token_log);
+  draw_one(step, cand, sampled, token_log);
 }
 
 __global__ void advance_kernel(DevStep* step) {
@@ -282,10 +289,10 @@ __global__ __launch_bounds__(64 * kMergeWaves) void topk_draw_kernel(
     store_entry(final_list, threadIdx.x, top);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    draw_one(step, final_list, sampled + 4 * row, token_log, row, gridDim.y);
-    if (advance) advance_one(step);
-  }
+  draw_one(step, final_list, sampled + 4 * row, token_log, row, gridDim.y);
+  // Thread 0 drew (the others left draw_one); its writes to the step come
+  // after its own reads of it.
+  if (threadIdx.x == 0 && advance) advance_one(step);
 }
 
 // Pass one into scratch, then merges of kListsPerMerge lists a workgroup
