@@ -60,6 +60,17 @@ class GgufTensor(ctypes.Structure):
                 ("bytes", c_uint64)]
 
 
+class CaptureSlot(ctypes.Structure):
+    _fields_ = [("first", c_uint32), ("width", c_uint32)]
+
+
+class CaptureSlots(ctypes.Structure):
+    _fields_ = [(n, CaptureSlot) for n in (
+        "neurons", "residual", "attention_added", "mlp_added", "query", "weights", "stats",
+        "readout")] + [(n, c_uint32) for n in ("keys", "query_heads", "window",
+                                                 "full_attention")]
+
+
 _P = c_void_p
 _S = ctypes.c_char_p
 _SIGS = {
@@ -137,6 +148,10 @@ _SIGS = {
     "frz_generate": (c_int, [_P, _P, c_uint32, _P, c_uint32, POINTER(Sampling),
                              c_uint32, _P, c_uint32, _P, POINTER(c_uint32)]),
     "frz_model_get_config": (c_int, [_P, POINTER(ModelConfig)]),
+    "frz_capture_words": (c_uint64, [POINTER(ModelConfig), POINTER(c_uint64)]),
+    "frz_model_set_capture": (c_int, [_P, c_int]),
+    "frz_model_read_capture": (c_int, [_P, _P, c_uint64]),
+    "frz_capture_layer": (c_int, [POINTER(ModelConfig), c_int, POINTER(CaptureSlots)]),
     "frz_generate_variants": (c_int, [_P, _P, c_uint32, c_uint32, _P, c_uint32,
                                       POINTER(Sampling), c_uint32, _P, c_uint32, _P, _P, _P]),
     "frz_gguf_read": (c_int, [_P, c_uint64, c_uint64, POINTER(c_void_p), POINTER(c_uint64)]),

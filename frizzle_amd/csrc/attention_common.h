@@ -142,11 +142,14 @@ __device__ __forceinline__ float add_quad_dots(float s, const float (&d)[2 * kKe
 
 // The chunk's unnormalized output (D values) and (m, l, live, 0) for one
 // head, from its staged query and values in S and each lane's key part in
-// k (rows past k_end zeros). Every thread of the workgroup calls it.
+// k (rows past k_end zeros). Every thread of the workgroup calls it. With
+// `scores`, each live key j's score is also written at scores[j - earliest].
 __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKeyLoads], int p,
                                             int window, const ChunkRange& r,
                                             float* __restrict__ partial,
-                                            float* __restrict__ stats) {
+                                            float* __restrict__ stats,
+                                            float* __restrict__ scores = nullptr,
+                                            int earliest = 0) {
   const int t = threadIdx.x, jj = t >> 2, u = t & 3, j = r.k_begin + jj;
   const bool live = jj < r.n_tiles * kTileKeys && j < r.k_end && j <= p && j + window > p;
   // Dimension t of every staged value row, read now so the reads complete
@@ -171,6 +174,7 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   s = add_quad_dots<1>(s, d);
   s = add_quad_dots<2>(s, d);
   s = add_quad_dots<3>(s, d);
+  if (scores && live && u == 0) scores[j - earliest] = s;
   // A tile is 8 keys, 32 lanes.
   float top = live ? s : -__builtin_inff();
   int seen = live ? 1 : 0;

@@ -32,7 +32,11 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
   value_store(S, vr, r, -1);
   __syncthreads();
   const size_t slot = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
-  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
+  // The last row's scores, for the capture store: keys earliest .. p.
+  const bool store = a.store_scores && row == (int)step->tokens - 1;
+  const int earliest = p + 1 - min(p + 1, a.keys);
+  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4,
+              store ? a.store_scores + (size_t)h * a.keys : nullptr, earliest);
 }
 
 // ---- fold ------------------------------------------------------------------
@@ -142,6 +146,14 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
       live = live || st[c].z != 0.0f;
     }
     f.out[(size_t)row * QH * D + h * D + dim0 + t] = live ? o / l : 0.0f;
+    // The last row's (m, l), for the capture store: m as the last chunk's
+    // fold leaves it.
+    if (f.store_stats && t == 0 && dim0 == 0 && row == (int)step->tokens - 1) {
+      const Fold g = fold_factors(lb[count - 1] != 0, mb[count - 1], st[count - 1].z != 0.0f,
+                                  st[count - 1].x);
+      f.store_stats[2 * h] = g.m;
+      f.store_stats[2 * h + 1] = l;
+    }
   }
 }
 
@@ -163,8 +175,9 @@ hipError_t launch_attention(hipStream_t s, const DevStep* step, const AttentionA
                      s, step, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_attention_fold(s, step, FoldArgs{a.partials, a.stats, a.out, a.window, a.max_chunks},
-                               max_tokens);
+  return launch_attention_fold(
+      s, step, FoldArgs{a.partials, a.stats, a.out, a.window, a.max_chunks, a.store_stats},
+      max_tokens);
 }
 
 }  // namespace frz

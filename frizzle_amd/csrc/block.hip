@@ -94,6 +94,16 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
       if (k < per && q < vec4s) st4(cap + 4 * q, x[k]);
     }
   }
+  if (row == tokens - 1 && (a.store_x || a.store_added)) {
+#pragma unroll
+    for (int k = 0; k < kNormMaxVec4; ++k) {
+      const int q = i + k * kNormThreads;
+      if (k < per && q < vec4s) {
+        if (a.store_x) st4(a.store_x + 4 * q, x[k]);
+        if (a.store_added && a.post_gain) st4(a.store_added + 4 * q, y[k]);
+      }
+    }
+  }
   float squares = 0.0f;
 #pragma unroll
   for (int k = 0; k < kNormMaxVec4; ++k) {
@@ -203,6 +213,31 @@ __global__ __launch_bounds__(256) void gather_kernel(const DevStep* __restrict__
   }
 }
 
+// ---- the capture store's copy (capture.wgsl) ----------------------------------
+__global__ __launch_bounds__(256) void capture_copy_kernel(const DevStep* __restrict__ step,
+                                                           const uint32_t* __restrict__ src,
+                                                           size_t row_stride, int width,
+                                                           uint32_t* __restrict__ dst) {
+  const uint32_t* row = src + (size_t)(step->tokens - 1) * row_stride;
+  for (int i = threadIdx.x; i < width; i += blockDim.x) dst[i] = row[i];
+}
+
+// The last row's scores into attention weights (weights.wgsl), a workgroup
+// a query head: weight i = exp2(s_i - m) / l for the keys p read, earliest
+// + i; zero past them.
+__global__ __launch_bounds__(256) void capture_weights_kernel(const DevStep* __restrict__ step,
+                                                              float* __restrict__ weights,
+                                                              const float* __restrict__ stats,
+                                                              int keys) {
+  const int h = blockIdx.x;
+  const uint32_t p = step->position + step->tokens - 1;
+  const uint32_t read = min(p + 1, (uint32_t)keys);  // keys p's query read
+  const float m = stats[2 * h], l = stats[2 * h + 1];
+  float* w = weights + (size_t)h * keys;
+  for (int i = threadIdx.x; i < keys; i += blockDim.x)
+    w[i] = (uint32_t)i < read ? exp2f_fixed(w[i] - m) / l : 0.0f;
+}
+
 // ---- pins (edit.wgsl:55-76) ----------------------------------------------------
 __global__ __launch_bounds__(64) void edit_kernel(const DevStep* __restrict__ step,
                                                   const uint32_t* __restrict__ table,
@@ -249,6 +284,22 @@ hipError_t launch_gather(hipStream_t s, const DevStep* step, QMatrix table,
   if (table.format != kQ4_0 && table.format != kQ8_0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(gather_kernel, dim3(max_tokens), dim3(256), 0, s, step, table, sampled,
                      hidden, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_capture_copy(hipStream_t s, const DevStep* step, const void* src,
+                               size_t row_stride, int width, void* dst) {
+  hipLaunchKernelGGL(capture_copy_kernel, dim3(1), dim3(256), 0, s, step,
+                     static_cast<const uint32_t*>(src), row_stride, width,
+                     static_cast<uint32_t*>(dst));
+  return hipGetLastError();
+}
+
+hipError_t launch_capture_weights(hipStream_t s, const DevStep* step, float* weights,
+                                  const float* stats, int keys, int query_heads) {
+  if (keys <= 0 || query_heads <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(capture_weights_kernel, dim3(query_heads), dim3(256), 0, s, step, weights,
+                     stats, keys);
   return hipGetLastError();
 }
 

@@ -130,6 +130,14 @@ struct frz_model {
     uint32_t *scratch = nullptr, *candidates = nullptr, *sampled = nullptr, *token_log = nullptr,
              *edits = nullptr;
   } variants;
+  // The capture store (frz_model_set_capture): written by the step that ends
+  // a prompt while capture_on; the readouts' own norm, logits and selection.
+  bool capture_on = false;
+  float* store = nullptr;
+  uint64_t store_words = 0;
+  std::vector<frz_capture_slots> slots;
+  float *ro_normed = nullptr, *ro_logits = nullptr;
+  uint32_t* ro_scratch = nullptr;
 };
 
 namespace {
@@ -230,6 +238,32 @@ float scale_log2e_of(const frz_model_config& c) {
   return (float)((double)(1.0f / std::sqrt((float)c.head_dim)) * 1.4426950408889634);
 }
 
+// The capture store's readouts (capture.h:28-34): the last layer's is the
+// step's own candidates; layer l's (l below it) is the residual entering
+// layer l + 1, already in the store, through the final norm, the head and
+// the selection. Run after the step's own output, into buffers of their own.
+hipError_t enqueue_readouts(frz_model* m) {
+  const frz_model_config& c = m->c;
+  hipStream_t s = m->dev->stream;
+  auto slot = [m](int l, frz_capture_slot frz_capture_slots::*field) {
+    return m->store + (m->slots[l].*field).first;
+  };
+  hipError_t e = launch_capture_copy(s, m->step, m->candidates, 0, 2 * kCandidates,
+                                     slot(c.layers - 1, &frz_capture_slots::readout));
+  for (int l = 0; l + 1 < c.layers && e == hipSuccess; ++l) {
+    NormArgs n{m->output_norm, nullptr, nullptr, slot(l + 1, &frz_capture_slots::residual),
+               m->ro_normed, c.epsilon, c.hidden, false};
+    e = launch_norm(s, m->step, n, 1);
+    if (e == hipSuccess)
+      e = launch_gemv(s, m->step, m->embedding, m->ro_normed, c.hidden, m->ro_logits, c.vocab,
+                      1, false);
+    if (e == hipSuccess)
+      e = launch_topk(s, m->ro_logits, c.vocab, m->ro_scratch,
+                      reinterpret_cast<uint32_t*>(slot(l, &frz_capture_slots::readout)));
+  }
+  return e;
+}
+
 // A step of several rows, in the graph's order (graph.cpp:290-470): the
 // embedding; per layer the attention norm (adding the last block's
 // post-normed output), Q/K/V, rope and the cache append, attention, O; the
@@ -247,11 +281,20 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   const float scale_log2e = scale_log2e_of(c);
   hipError_t e = launch_gather(s, m->step, m->embedding, v ? v->sampled : m->sampled, m->hidden,
                                std::sqrt((float)H), max_tokens);
+  // The step that ends a prompt fills the capture store, when it is on.
+  const bool cap = !v && logits && m->capture_on;
+  auto slot = [m](int l, frz_capture_slot frz_capture_slots::*field) {
+    return m->store + (m->slots[l].*field).first;
+  };
   const float* pending = nullptr;
   for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
     const Layer& L = m->layers[l];
     NormArgs attn_norm{L.gains[0], pending, m->output, m->hidden, m->normed,
                        c.epsilon, H, false};
+    if (cap) {
+      attn_norm.store_x = slot(l, &frz_capture_slots::residual);
+      if (l > 0) attn_norm.store_added = slot(l - 1, &frz_capture_slots::mlp_added);
+    }
     if (v && v->capture) {
       // [step][layer][row][hidden] for this step's rows
       attn_norm.capture = v->residuals + (size_t)l * max_tokens * H;
@@ -287,12 +330,25 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                    L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon, cache_stride};
         e = launch_rope(s, m->step, r, max_tokens);
       }
+      if (cap && e == hipSuccess) {
+        e = launch_capture_copy(s, m->step, m->qkv, qkv_stride, qw,
+                                slot(l, &frz_capture_slots::query));
+      }
       if (e == hipSuccess) {
         AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
                         m->partials, m->partials + m->partial_floats, L.slots, L.window,
                         c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
                         cache_stride};
+        if (cap) {
+          a.store_scores = slot(l, &frz_capture_slots::weights);
+          a.store_stats = slot(l, &frz_capture_slots::stats);
+          a.keys = (int)m->slots[l].keys;
+        }
         e = launch_attention(s, m->step, a, max_tokens);
+        if (cap && e == hipSuccess) {
+          e = launch_capture_weights(s, m->step, a.store_scores, a.store_stats, a.keys,
+                                     c.query_heads);
+        }
       }
     }
     if (e == hipSuccess)
@@ -300,11 +356,16 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     if (e == hipSuccess) {
       NormArgs ffn_norm{L.gains[4], L.gains[3], m->output, m->hidden, m->normed,
                         c.epsilon, H, false};
+      if (cap) ffn_norm.store_added = slot(l, &frz_capture_slots::attention_added);
       e = launch_norm(s, m->step, ffn_norm, max_tokens);
     }
     if (e == hipSuccess)
       e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens,
                        v ? v->edits : m->edits, l, v ? v->edit_stride : 0);
+    if (cap && e == hipSuccess) {
+      e = launch_capture_copy(s, m->step, m->act, c.ffn, c.ffn,
+                              slot(l, &frz_capture_slots::neurons));
+    }
     if (e == hipSuccess)
       e = launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
     pending = L.gains[5];
@@ -312,11 +373,13 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden, m->normed,
                         c.epsilon, H, v == nullptr};
+    if (cap) final_norm.store_added = slot(c.layers - 1, &frz_capture_slots::mlp_added);
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
   if (logits && e == hipSuccess) {
     if (!v) {
       e = enqueue_output(m, max_tokens, false);
+      if (cap && e == hipSuccess) e = enqueue_readouts(m);
     } else {
       e = launch_gemv(s, m->step, m->embedding, m->normed, H, v->logits, c.vocab, max_tokens,
                       false);
@@ -406,8 +469,13 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
 // `advance`: a fed decode step (logits drawn), whose last kernel advances
 // the step parameters for the next.
 int enqueue_step(frz_model* m, int max_tokens, bool logits, bool advance = false) {
-  return max_tokens == 1 ? enqueue_decode(m, logits, advance)
-                         : enqueue_rows(m, max_tokens, logits, nullptr);
+  // A one-token step that ends a prompt (logits, not a fed decode step that
+  // advances) takes the rows path when the capture store is on: its kernels
+  // write the store, and the bits are the same either way.
+  const bool ends_prompt = logits && !advance;
+  return max_tokens == 1 && !(ends_prompt && m->capture_on)
+             ? enqueue_decode(m, logits, advance)
+             : enqueue_rows(m, max_tokens, logits, nullptr);
 }
 
 int build_decode_graph(frz_model* m) {
@@ -725,6 +793,41 @@ int frz_model_synthesize(frz_model* m, uint64_t seed) {
   }
   if (int rc = one(-1, FRZ_ROLE_EMBEDDING)) return rc;
   return one(-1, FRZ_ROLE_OUTPUT_NORM);
+}
+
+int frz_model_set_capture(frz_model* m, int enabled) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_capture: null model");
+  const frz_model_config& c = m->c;
+  if (enabled && !m->store) {
+    const uint64_t words = frz_capture_words(&c, nullptr);
+    if (words == 0) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_capture: store too large");
+    std::vector<frz_capture_slots> slots(c.layers);
+    for (int l = 0; l < c.layers; ++l) {
+      if (int rc = frz_capture_layer(&c, l, &slots[l])) return rc;
+    }
+    if (int rc = alloc(m, &m->store, words * 4)) return rc;
+    if (int rc = alloc(m, &m->ro_normed, (size_t)c.hidden * 4)) return rc;
+    if (int rc = alloc(m, &m->ro_logits, (size_t)c.vocab * 4)) return rc;
+    if (int rc = alloc(m, &m->ro_scratch, topk_scratch_words(c.vocab) * 4)) return rc;
+    if (int rc = check_hip(hipMemsetAsync(m->store, 0, words * 4, m->dev->stream), "store"))
+      return rc;
+    m->store_words = words;
+    m->slots = std::move(slots);
+  }
+  m->capture_on = enabled != 0;
+  return check_hip(hipStreamSynchronize(m->dev->stream), "capture sync");
+}
+
+int frz_model_read_capture(frz_model* m, uint32_t* out, uint64_t words) {
+  if (!m || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_read_capture: null argument");
+  if (!m->store || words > m->store_words) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_read_capture: no store, or more words than it has");
+  }
+  if (int rc = check_hip(hipMemcpyAsync(out, m->store, words * 4, hipMemcpyDeviceToHost,
+                                        m->dev->stream),
+                         "read capture"))
+    return rc;
+  return check_hip(hipStreamSynchronize(m->dev->stream), "read capture sync");
 }
 
 int frz_model_set_graphs(frz_model* m, int enabled) {

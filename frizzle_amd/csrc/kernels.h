@@ -123,6 +123,10 @@ struct NormArgs {
   // written to capture + step.drawn * capture_step + row * width.
   float* capture = nullptr;
   size_t capture_step = 0;
+  // Not null: the last row's hidden after the add, and what was added
+  // (the block's output after its post-norm), written there too.
+  float* store_x = nullptr;
+  float* store_added = nullptr;
 };
 hipError_t launch_norm(hipStream_t s, const DevStep* step, const NormArgs& a,
                        int max_tokens);
@@ -164,6 +168,12 @@ struct AttentionArgs {
   int max_chunks;             // chunks a row may reach: the grid's width
   float scale_log2e;
   size_t cache_stride = 0;    // elements from one variant's cache to the next
+  // Not null: the last row's scores (log2 units) of the keys it reads, head h
+  // key earliest + i at store_scores[h * keys + i]; and each head's final
+  // (m, l) at store_stats[2 h], [2 h + 1].
+  float* store_scores = nullptr;
+  float* store_stats = nullptr;
+  int keys = 0;
 };
 hipError_t launch_attention(hipStream_t s, const DevStep* step,
                             const AttentionArgs& a, int max_tokens);
@@ -203,10 +213,20 @@ struct FoldArgs {
   float* out;
   int window;
   int max_chunks;
+  float* store_stats = nullptr;  // the last row's (m, l) a head, when not null
 };
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens);
 constexpr int kMaxFoldChunks = 224;  // chunk states a fold stages in LDS: 14,272 keys
+
+// The capture store's copies at the step that ends the prompt: the last row
+// of src (rows row_stride words apart) into dst, word for word
+// (capture.wgsl); and the last row's scores turned into attention weights
+// exp2(s - m) / l in place, zeros past the keys read (weights.wgsl).
+hipError_t launch_capture_copy(hipStream_t s, const DevStep* step, const void* src,
+                               size_t row_stride, int width, void* dst);
+hipError_t launch_capture_weights(hipStream_t s, const DevStep* step, float* weights,
+                                  const float* stats, int keys, int query_heads);
 
 hipError_t launch_gather(hipStream_t s, const DevStep* step, QMatrix table,
                          const uint32_t* sampled, float* hidden, float scale,

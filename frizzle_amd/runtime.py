@@ -137,6 +137,29 @@ def block_split(fmt, blocks):
     return codes, scales
 
 
+CAPTURE_SLOTS = ("neurons", "residual", "attention_added", "mlp_added", "query", "weights",
+                 "stats", "readout")
+
+
+def capture_words(cfg):
+    """The capture store's size in words (0 for shapes it cannot hold)."""
+    return int(load().frz_capture_words(byref(cfg), None))
+
+
+def capture_layout(cfg):
+    """Each layer's slots of the capture store: {name: (first word, width)},
+    plus keys, query_heads, window and full_attention."""
+    out = []
+    for layer in range(cfg.layers):
+        s = _lib.CaptureSlots()
+        check(load().frz_capture_layer(byref(cfg), layer, byref(s)))
+        d = {n: (getattr(s, n).first, getattr(s, n).width) for n in CAPTURE_SLOTS}
+        d.update(keys=s.keys, query_heads=s.query_heads, window=s.window,
+                 full_attention=bool(s.full_attention))
+        out.append(d)
+    return out
+
+
 def rope_turns(base, head_dim):
     out = (ctypes.c_float * (head_dim // 2))()
     load().frz_rope_turns(base, head_dim, out)
@@ -233,6 +256,20 @@ class Model:
         else:
             check(self.lib.frz_model_set_tensor_format(self.handle, layer, _lib.ROLE[role], fmt,
                                                        a.ctypes.data, a.nbytes))
+
+    def set_capture(self, on=True):
+        """The capture store on or off: while on, the step that ends a
+        prompt writes it."""
+        check(self.lib.frz_model_set_capture(self.handle, int(on)))
+
+    def capture(self):
+        """The capture store as uint32 words, and its per-layer slots
+        ({slot: (first, width)} a layer, with keys and window)."""
+        layout = capture_layout(self.cfg)
+        words = capture_words(self.cfg)
+        out = np.empty(words, dtype=np.uint32)
+        check(self.lib.frz_model_read_capture(self.handle, out.ctypes.data, words))
+        return out, layout
 
     def load_gguf(self, path):
         """Every tensor of a Gemma 3 GGUF file of this model's shapes."""

@@ -296,6 +296,38 @@ uint64_t frz_tensor_bytes(const frz_model_config* config, int role);
 int frz_synth_tensor(const frz_model_config* config, uint64_t seed, int layer,
                      int role, void* out, uint64_t bytes);
 
+/* ---- the capture store (src/core/capture/capture.h:43-75) ---------------
+ * What the model used at the last position of the step that ends the prompt,
+ * layer by layer, in one store of 32-bit words. Region 1: every layer's
+ * neurons (the gated activation after the layer's pins, as the down product
+ * reads it), in layer order. Region 2, layer by layer: the residual entering
+ * the layer (the hidden row after its first norm's add; layer 0's is the
+ * embedding row), what the attention block and the MLP block add to the
+ * residual (their outputs after their post-norms), the query after QK-norm
+ * and rope, the attention weights over the keys the query read, the
+ * softmax statistics (m, l) of each head, and the readout: the top-64
+ * (logit bits, token) pairs of the residual as the layer leaves it through
+ * the final norm and the head (the last layer's: the step's own). */
+typedef struct frz_capture_slot {
+  uint32_t first;  /* word offset in the store */
+  uint32_t width;  /* words */
+} frz_capture_slot;
+typedef struct frz_capture_slots {
+  frz_capture_slot neurons, residual, attention_added, mlp_added, query,
+      weights, stats, readout;
+  uint32_t keys;   /* min(window, context): a head's weights */
+  uint32_t query_heads;
+  uint32_t window;
+  uint32_t full_attention; /* window >= context */
+} frz_capture_slots;
+/* The store's words for a model of these shapes (0 for bad shapes), and
+ * region 1's in *neuron_words when not null. */
+uint64_t frz_capture_words(const frz_model_config* config,
+                           uint64_t* neuron_words);
+/* One layer's slots (capture.h: layout()). */
+int frz_capture_layer(const frz_model_config* config, int layer,
+                      frz_capture_slots* out);
+
 typedef struct frz_model frz_model;
 
 int frz_model_create(frz_device* dev, const frz_model_config* config,
@@ -315,6 +347,15 @@ int frz_model_set_tensor_format(frz_model* model, int layer, int role,
 int frz_model_synthesize(frz_model* model, uint64_t seed);
 /* The shapes the model was created with. */
 int frz_model_get_config(const frz_model* model, frz_model_config* out);
+/* The capture store on or off (off when created). While on, the step that
+ * ends a prompt (a step asking for logits that is not a fed decode step)
+ * writes every word of the store at its last row: Engine::inspect's and a
+ * run's captures (src/core/capture/capture.h:15-34, :77-101), the store
+ * laid out as frz_capture_layer says. It costs that step a head product,
+ * a norm and a selection a layer for the readouts. */
+int frz_model_set_capture(frz_model* model, int enabled);
+/* The store's first `words` words, after the stream's work. */
+int frz_model_read_capture(frz_model* model, uint32_t* out, uint64_t words);
 /* The edit table, u32 words in the reference's layout (src/core/edit/
  * edit.h: per layer [first, count], then [neuron, kind, value bits, first
  * position, end position] per edit), used by every later step. */

@@ -338,6 +338,16 @@ float norm_squares(const float* v, int width) {
 void orc_norm_row(const float* gain, const float* post_gain, int add,
                   int post_norm, float post_scale, float epsilon, int width,
                   float* hidden, const float* output, float* normed) {
+  orc_norm_row_added(gain, post_gain, add, post_norm, post_scale, epsilon, width, hidden, output,
+                     normed, nullptr);
+}
+
+// The same, also giving the vector the add added (the block's output after
+// its post-norm) when `added` is not null: the capture store's additions
+// (capture.h:18-21).
+void orc_norm_row_added(const float* gain, const float* post_gain, int add,
+                        int post_norm, float post_scale, float epsilon, int width,
+                        float* hidden, const float* output, float* normed, float* added) {
   const float n = static_cast<float>(width);
   if (add) {
     std::vector<float> y(output, output + width);
@@ -347,6 +357,7 @@ void orc_norm_row(const float* gain, const float* post_gain, int add,
       for (int i = 0; i < width; ++i) y[i] = ((y[i] * r) * post_gain[i]) * post_scale;
     }
     for (int i = 0; i < width; ++i) hidden[i] = hidden[i] + y[i];
+    if (added) std::copy(y.begin(), y.end(), added);
   }
   const float r = orc_inverse_sqrt(norm_squares(hidden, width) / n + epsilon);
   for (int i = 0; i < width; ++i) normed[i] = (hidden[i] * r) * gain[i];
@@ -445,7 +456,21 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
                        int query_heads, int kv_heads, float scale_log2e,
                        const float* query, const uint16_t* key_cache,
                        const uint16_t* value_cache, float* out) {
+  orc_attention_row_scores(position, window, slots, head_dim, query_heads, kv_heads, scale_log2e,
+                           query, key_cache, value_cache, out, nullptr, 0, nullptr);
+}
+
+// The same, also giving each head's scores of the keys it reads (key
+// earliest + i at scores[h * keys + i], earliest = p + 1 - min(p + 1, keys))
+// and its final (m, l) at stats[2 h], stats[2 h + 1], when not null: the
+// capture store's scores and statistics (weights.h:12-21).
+void orc_attention_row_scores(int position, int window, int slots, int head_dim,
+                              int query_heads, int kv_heads, float scale_log2e,
+                              const float* query, const uint16_t* key_cache,
+                              const uint16_t* value_cache, float* out, float* scores,
+                              int keys, float* stats) {
   const int p = position;
+  const int score0 = p + 1 - std::min(p + 1, keys);
   const int group = query_heads / kv_heads;
   const int earliest = p + 1 > window ? p + 1 - window : 0;
   std::vector<float> q(head_dim), o_run(head_dim), o_chunk(head_dim),
@@ -478,6 +503,7 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
             float acc = 0.0f;
             for (int w = 0; w < head_dim / 4; ++w) acc += orc_dot4(q.data() + 4 * w, kf.data() + 4 * w);
             s[b] = acc;
+            if (scores) scores[static_cast<size_t>(h) * keys + (j - score0)] = acc;
             top_tile = seen ? std::max(top_tile, acc) : acc;
             seen = true;
           }
@@ -519,6 +545,10 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
       run_live = run_live || chunk_live;
     }
     for (int i = 0; i < head_dim; ++i) out[h * head_dim + i] = run_live ? o_run[i] / run_l : 0.0f;
+    if (stats) {
+      stats[2 * h] = run_m;
+      stats[2 * h + 1] = run_l;
+    }
   }
 }
 
@@ -695,7 +725,18 @@ struct orc_model {
   std::vector<uint32_t> edits;
   std::vector<float> hidden, normed, output, q, k, v, attn, act;
   std::vector<float> residuals;  // [layers][hidden]: the last token's
+  bool capture = false;
+  std::vector<std::vector<uint32_t>> cap;  // [layer * 8 + slot]: the last token's
 };
+
+namespace {
+// A captured value's words (floats as their bits), for layer l's slot.
+void put_words(orc_model* m, int layer, int slot, const float* v, int n) {
+  std::vector<uint32_t>& out = m->cap[static_cast<size_t>(layer) * 8 + slot];
+  out.resize(n);
+  std::memcpy(out.data(), v, static_cast<size_t>(n) * 4);
+}
+}  // namespace
 
 orc_model* orc_model_create(const orc_config* config,
                             const orc_layer_weights* layers,
@@ -758,13 +799,18 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
       1.4426950408889634);
   for (int l = 0; l < c.layers; ++l) {
     const orc_layer_weights& w = m->w[l];
-    orc_norm_row(w.attn_norm, pending, pending != nullptr, pending != nullptr,
-                 1.0f, c.epsilon, H, m->hidden.data(), m->output.data(),
-                 m->normed.data());
+    std::vector<float> added(H);
+    orc_norm_row_added(w.attn_norm, pending, pending != nullptr, pending != nullptr,
+                       1.0f, c.epsilon, H, m->hidden.data(), m->output.data(),
+                       m->normed.data(), added.data());
     // The residual entering layer l: X after the add its first norm makes
     // (capture.h:15-17), layer 0's the embedding row.
     std::copy(m->hidden.begin(), m->hidden.end(),
               m->residuals.begin() + static_cast<size_t>(l) * H);
+    if (m->capture) {
+      put_words(m, l, 1, m->hidden.data(), H);
+      if (l > 0) put_words(m, l - 1, 3, added.data(), H);
+    }
     orc_gemv(w.q, qw, H, m->normed.data(), m->q.data());
     orc_gemv(w.k, kvw, H, m->normed.data(), m->k.data());
     orc_gemv(w.v, kvw, H, m->normed.data(), m->v.data());
@@ -772,22 +818,82 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
                  c.epsilon, m->turns[l].data(), w.q_norm, w.k_norm,
                  m->q.data(), m->k.data(), m->v.data(), m->kcache[l].data(),
                  m->vcache[l].data());
-    orc_attention_row(position, m->windows[l], m->slots[l], c.head_dim,
-                      c.query_heads, c.kv_heads, scale_log2e, m->q.data(),
-                      m->kcache[l].data(), m->vcache[l].data(),
-                      m->attn.data());
+    if (m->capture) {
+      // Q after rope; each head's scores turned into weights by the fold's
+      // (m, l), zeros past the keys read (weights.h:29-40).
+      put_words(m, l, 4, m->q.data(), qw);
+      const int keys = std::min(m->windows[l], c.context);
+      std::vector<float> wts(static_cast<size_t>(c.query_heads) * keys, 0.0f);
+      std::vector<float> st(2 * c.query_heads);
+      orc_attention_row_scores(position, m->windows[l], m->slots[l], c.head_dim, c.query_heads,
+                               c.kv_heads, scale_log2e, m->q.data(), m->kcache[l].data(),
+                               m->vcache[l].data(), m->attn.data(), wts.data(), keys, st.data());
+      const int read = std::min(position + 1, keys);
+      for (int h = 0; h < c.query_heads; ++h) {
+        for (int i = 0; i < keys; ++i) {
+          float& x = wts[static_cast<size_t>(h) * keys + i];
+          x = i < read ? orc_exp2(x - st[2 * h]) / st[2 * h + 1] : 0.0f;
+        }
+      }
+      put_words(m, l, 5, wts.data(), static_cast<int>(wts.size()));
+      put_words(m, l, 6, st.data(), 2 * c.query_heads);
+    } else {
+      orc_attention_row(position, m->windows[l], m->slots[l], c.head_dim,
+                        c.query_heads, c.kv_heads, scale_log2e, m->q.data(),
+                        m->kcache[l].data(), m->vcache[l].data(),
+                        m->attn.data());
+    }
     orc_gemv(w.o, H, qw, m->attn.data(), m->output.data());
-    orc_norm_row(w.ffn_norm, w.post_attn_norm, 1, 1, 1.0f, c.epsilon, H,
-                 m->hidden.data(), m->output.data(), m->normed.data());
+    orc_norm_row_added(w.ffn_norm, w.post_attn_norm, 1, 1, 1.0f, c.epsilon, H,
+                       m->hidden.data(), m->output.data(), m->normed.data(), added.data());
+    if (m->capture) put_words(m, l, 2, added.data(), H);
     orc_gated(w.gate, w.up, c.ffn, H, m->normed.data(), m->act.data());
     orc_edit_row(m->edits.data(), l, static_cast<uint32_t>(position), c.ffn,
                  m->act.data());
+    if (m->capture) put_words(m, l, 0, m->act.data(), c.ffn);
     orc_gemv_format(w.down_format, w.down, H, c.ffn, m->act.data(), m->output.data());
     pending = w.post_ffn_norm;
   }
-  orc_norm_row(m->output_norm, pending, 1, 1, 1.0f, c.epsilon, H,
-               m->hidden.data(), m->output.data(), m->normed.data());
+  std::vector<float> added(H);
+  orc_norm_row_added(m->output_norm, pending, 1, 1, 1.0f, c.epsilon, H,
+                     m->hidden.data(), m->output.data(), m->normed.data(), added.data());
+  if (m->capture) put_words(m, c.layers - 1, 3, added.data(), H);
   if (logits) orc_gemv_format(c.embedding_format, m->embedding, c.vocab, H, m->normed.data(), logits);
+  if (m->capture) {
+    // Readouts (capture.h:28-34): the residual entering layer l + 1 through
+    // the final norm, the head and the selection; the last layer's is the
+    // token's own selection.
+    std::vector<float> x(H), nrm(H), lg(c.vocab);
+    std::vector<uint32_t> bits(kCandidates), ids(kCandidates), pairs(2 * kCandidates);
+    for (int l = 0; l < c.layers; ++l) {
+      if (l + 1 < c.layers) {
+        std::copy(m->residuals.begin() + static_cast<size_t>(l + 1) * H,
+                  m->residuals.begin() + static_cast<size_t>(l + 2) * H, x.begin());
+        orc_norm_row(m->output_norm, nullptr, 0, 0, 1.0f, c.epsilon, H, x.data(), nullptr,
+                     nrm.data());
+      } else {
+        nrm = m->normed;
+      }
+      orc_gemv_format(c.embedding_format, m->embedding, c.vocab, H, nrm.data(), lg.data());
+      orc_topk(lg.data(), c.vocab, bits.data(), ids.data());
+      for (int i = 0; i < kCandidates; ++i) {
+        pairs[2 * i] = bits[i];
+        pairs[2 * i + 1] = ids[i];
+      }
+      m->cap[static_cast<size_t>(l) * 8 + 7] = pairs;
+    }
+  }
+}
+
+void orc_model_set_capture(orc_model* m, int on) {
+  m->capture = on != 0;
+  m->cap.assign(static_cast<size_t>(m->c.layers) * 8, {});
+}
+
+const uint32_t* orc_model_capture(const orc_model* m, int layer, int slot, int* words) {
+  const std::vector<uint32_t>& v = m->cap[static_cast<size_t>(layer) * 8 + slot];
+  *words = static_cast<int>(v.size());
+  return v.data();
 }
 
 const float* orc_model_normed(const orc_model* m) { return m->normed.data(); }

@@ -95,6 +95,11 @@ void orc_gated(const uint8_t* gate, const uint8_t* up, int rows, int cols,
 void orc_norm_row(const float* gain, const float* post_gain, int add,
                   int post_norm, float post_scale, float epsilon, int width,
                   float* hidden, const float* output, float* normed);
+/* orc_norm_row, also giving the vector the add added (when added is not
+ * null and add is set). */
+void orc_norm_row_added(const float* gain, const float* post_gain, int add,
+                        int post_norm, float post_scale, float epsilon, int width,
+                        float* hidden, const float* output, float* normed, float* added);
 void orc_rope_turns(float base, int head_dim, float* turns);
 void orc_rope_row(int position, int slots, int head_dim, int query_heads,
                   int kv_heads, float epsilon, const float* turns,
@@ -105,6 +110,14 @@ void orc_attention_row(int position, int window, int slots, int head_dim,
                        int query_heads, int kv_heads, float scale_log2e,
                        const float* query, const uint16_t* key_cache,
                        const uint16_t* value_cache, float* out);
+/* orc_attention_row, also giving each head's scores of the keys its query
+ * reads (key earliest + i at scores[h * keys + i], earliest =
+ * p + 1 - min(p + 1, keys)) and its final (m, l) at stats[2h], [2h + 1]. */
+void orc_attention_row_scores(int position, int window, int slots, int head_dim,
+                              int query_heads, int kv_heads, float scale_log2e,
+                              const float* query, const uint16_t* key_cache,
+                              const uint16_t* value_cache, float* out, float* scores,
+                              int keys, float* stats);
 void orc_gather_row(const uint8_t* table, int width, uint32_t token,
                     float scale, float* hidden);
 void orc_gather_row_format(int format, const uint8_t* table, int width,
@@ -178,6 +191,12 @@ const float* orc_model_normed(const orc_model* m);
 /* [layers][hidden]: for the last token, the residual entering each layer
  * (X after the add of the layer's first norm; layer 0's is the embedding). */
 const float* orc_model_residuals(const orc_model* m);
+/* The capture store's values for the last token, kept while capture is on
+ * (src/core/capture/capture.h:12-34): slot 0 neurons, 1 residual,
+ * 2 attention_added, 3 mlp_added, 4 query, 5 weights, 6 stats, 7 readout,
+ * as 32-bit words; *words gets the slot's width. */
+void orc_model_set_capture(orc_model* m, int on);
+const uint32_t* orc_model_capture(const orc_model* m, int layer, int slot, int* words);
 /* Read access to layer l's F16 key and value cache, slots x kv x head_dim. */
 const uint16_t* orc_model_key_cache(const orc_model* m, int layer);
 const uint16_t* orc_model_value_cache(const orc_model* m, int layer);

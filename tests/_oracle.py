@@ -70,6 +70,8 @@ _SIGS = {
     "orc_model_token": (None, [_P, c_uint32, c_int, _P]),
     "orc_model_normed": (c_void_p, [_P]),
     "orc_model_residuals": (c_void_p, [_P]),
+    "orc_model_set_capture": (None, [_P, c_int]),
+    "orc_model_capture": (c_void_p, [_P, c_int, c_int, POINTER(c_int)]),
     "orc_model_key_cache": (c_void_p, [_P, c_int]),
     "orc_model_value_cache": (c_void_p, [_P, c_int]),
     "orc_model_slots": (c_int, [_P, c_int]),
@@ -250,6 +252,20 @@ class OracleModel:
     def normed(self):
         ptr = lib().orc_model_normed(self.handle)
         return np.ctypeslib.as_array((c_float * self.cfg.hidden).from_address(ptr)).copy()
+
+    SLOTS = ("neurons", "residual", "attention_added", "mlp_added", "query", "weights",
+             "stats", "readout")
+
+    def set_capture(self, on=True):
+        lib().orc_model_set_capture(self.handle, int(on))
+
+    def capture(self, layer, slot):
+        """The last token's captured words (uint32) of one layer's slot."""
+        n = c_int()
+        ptr = lib().orc_model_capture(self.handle, layer, self.SLOTS.index(slot), ctypes.byref(n))
+        if n.value == 0:
+            return np.zeros(0, dtype=np.uint32)
+        return np.ctypeslib.as_array((c_uint32 * n.value).from_address(ptr)).copy()
 
     def residuals(self):
         """[layers][hidden]: the last token's residual entering each layer."""
