@@ -42,6 +42,15 @@
  *                     fixture-style blocks their generator states
  *   orc_gemv_format   Q4_0 equal to orc_gemv; exact integer results for
  *                     Q8_0 and Q4_1 (the order is orc_gemv's, pinned above)
+ *   orc_norm_row_added  hidden after = hidden before + added, bit for bit;
+ *                     added against the f64 post-norm within 2^-18
+ *   orc_attention_row_scores  the output is orc_attention_row's bit for
+ *                     bit; scores against f64 dots, m their maximum, l the
+ *                     f64 sum of exp2(s - m); untouched past the keys read
+ *   orc_model_residuals, orc_model_capture  the model's own intermediates
+ *                     (pinned through the functions above and the model's
+ *                     logits); the capture store's layout is pinned by the
+ *                     reference's counts in tests/test_capture.py
  *   orc_edit_row      the edit kernel contract (edit_kernel_test.cpp:1-21)
  *   orc_topk          brute-force stable sort in the total order
  *   orc_philox        Random123 known answers; orc_mulhi against 64-bit

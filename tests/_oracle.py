@@ -53,6 +53,10 @@ _SIGS = {
     "orc_rope_turns": (None, [c_float, c_int, _P]),
     "orc_rope_row": (None, [c_int, c_int, c_int, c_int, c_int, c_float, _P, _P,
                             _P, _P, _P, _P, _P, _P]),
+    "orc_norm_row_added": (None, [_P, _P, c_int, c_int, c_float, c_float, c_int, _P,
+                                  _P, _P, _P]),
+    "orc_attention_row_scores": (None, [c_int, c_int, c_int, c_int, c_int, c_int, c_float,
+                                        _P, _P, _P, _P, _P, c_int, _P]),
     "orc_attention_row": (None, [c_int, c_int, c_int, c_int, c_int, c_int,
                                  c_float, _P, _P, _P, _P]),
     "orc_gather_row": (None, [_P, c_int, c_uint32, c_float, _P]),

@@ -83,6 +83,26 @@ def test_capture_at_a_one_token_prompt_end_and_every_word_rewritten(device):
     model.close()
 
 
+def test_inspection_captures_what_a_run_does(device):
+    # An inspection (max_tokens 0) draws nothing and captures the whole
+    # store, equal to a run's from the same prompt and edits
+    # (replay_test.cpp, 7).
+    cfg = small_config()
+    model, _ = build_pair(device, cfg, seed=67)
+    prompt = np.random.default_rng(68).integers(0, cfg.vocab, 50).astype(np.uint32)
+    edits = [fz.Edit(0, 9, fz.EditKind.ZERO, 0.0)]
+    model.set_capture(True)
+    assert model.generate(prompt, edits, max_tokens=0).size == 0
+    inspected, _ = model.capture()
+    fresh, _ = build_pair(device, cfg, seed=67)
+    fresh.set_capture(True)
+    fresh.generate(prompt, edits, max_tokens=6)
+    ran, _ = fresh.capture()
+    assert np.array_equal(inspected, ran)
+    fresh.close()
+    model.close()
+
+
 def test_readouts_see_the_residual_where_each_layer_leaves_it(device):
     # A pin at layer 1 leaves the readouts below it bit for bit and changes
     # its own (replay_test.cpp, 9).

@@ -378,6 +378,65 @@ def test_attention_against_f64_softmax(pos, window, slots):
         assert np.max(np.abs(out[h * d:(h + 1) * d] - want)) < 2.0 ** -14 * (1 + np.abs(V).max())
 
 
+def test_norm_added_is_what_the_add_added():
+    # The capture store's addition is the vector the norm adds: hidden after
+    # equals hidden before plus it, each element one f32 add, and it is the
+    # post-normed block output (f64 within the 2^-18 margin).
+    rng = np.random.default_rng(19)
+    n = 1152
+    for trial in range(10):
+        hidden = rng.normal(0, 3, n).astype(np.float32)
+        out = rng.normal(0, 10, n).astype(np.float32)
+        gain = (1 + 0.1 * rng.normal(0, 1, n)).astype(np.float32)
+        pg = (1 + 0.1 * rng.normal(0, 1, n)).astype(np.float32)
+        h = hidden.copy()
+        normed = np.empty(n, np.float32)
+        added = np.empty(n, np.float32)
+        orc.lib().orc_norm_row_added(gain.ctypes.data, pg.ctypes.data, 1, 1, 1.0, 1e-6, n,
+                                     h.ctypes.data, out.ctypes.data, normed.ctypes.data,
+                                     added.ctypes.data)
+        assert np.array_equal(bits(h), bits(hidden + added))
+        h2, normed2 = orc.norm_row(gain, hidden, out, pg)
+        assert np.array_equal(bits(h), bits(h2)) and np.array_equal(bits(normed), bits(normed2))
+        o = out.astype(np.float64)
+        want = o / np.sqrt(np.mean(o * o) + 1e-6) * pg
+        assert np.max(np.abs(added - want) / (np.abs(want) + 1e-30)) < 2.0 ** -18
+
+
+@pytest.mark.parametrize("pos,window,slots", [(700, 512, 640), (40, 512, 640), (300, 64, 640)])
+def test_attention_scores_and_statistics(pos, window, slots):
+    # The capture store's scores are the query's dots with the keys it reads
+    # (log2 units), m their maximum and l the sum of exp2(s - m); the output
+    # is orc_attention_row's, bit for bit; slots past the keys read stay.
+    rng = np.random.default_rng(pos + slots)
+    d, qh = 256, 4
+    kc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16)
+    vc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16)
+    q = rng.normal(0, 0.5, qh * d).astype(np.float32)
+    sc = np.float32(0.0625 * 1.4426950408889634)
+    keys = window
+    out, out2 = np.empty(qh * d, np.float32), np.empty(qh * d, np.float32)
+    scores = np.full(qh * keys, -7.0, np.float32)
+    stats = np.empty(2 * qh, np.float32)
+    args = (pos, window, slots, d, qh, 1, float(sc), q.ctypes.data, kc.view(np.uint16).ctypes.data,
+            vc.view(np.uint16).ctypes.data)
+    orc.lib().orc_attention_row_scores(*args, out.ctypes.data, scores.ctypes.data, keys,
+                                       stats.ctypes.data)
+    orc.lib().orc_attention_row(*args, out2.ctypes.data)
+    assert np.array_equal(bits(out), bits(out2))
+    earliest = pos + 1 - min(pos + 1, keys)
+    read = pos - earliest + 1
+    K = np.stack([kc[(j % slots) * d:(j % slots + 1) * d] for j in range(earliest, pos + 1)])
+    for h in range(qh):
+        s = scores[h * keys:h * keys + read]
+        want = K.astype(np.float64) @ (q[h * d:(h + 1) * d] * sc).astype(np.float64)
+        assert np.max(np.abs(s - want)) < 2.0 ** -18 * (1 + np.abs(want).max())
+        assert (scores[h * keys + read:(h + 1) * keys] == -7.0).all()
+        assert stats[2 * h] == s.max()
+        l64 = np.exp2(s.astype(np.float64) - np.float64(s.max())).sum()
+        assert abs(stats[2 * h + 1] - l64) < 2.0 ** -18 * l64
+
+
 def test_attention_ignores_keys_outside_the_window():
     # Keys at or before p - W, and slots not yet written, never count: make
     # them huge and the output must not move.
