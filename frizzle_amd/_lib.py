@@ -150,6 +150,7 @@ _SIGS = {
     "frz_model_get_config": (c_int, [_P, POINTER(ModelConfig)]),
     "frz_capture_words": (c_uint64, [POINTER(ModelConfig), POINTER(c_uint64)]),
     "frz_model_set_capture": (c_int, [_P, c_int]),
+    "frz_model_reused": (c_uint32, [_P]),
     "frz_model_read_capture": (c_int, [_P, _P, c_uint64]),
     "frz_capture_layer": (c_int, [POINTER(ModelConfig), c_int, POINTER(CaptureSlots)]),
     "frz_generate_variants": (c_int, [_P, _P, c_uint32, c_uint32, _P, c_uint32,

@@ -115,6 +115,7 @@ struct frz_model {
   std::vector<uint32_t> cached;
   std::vector<uint32_t> cached_edits;
   uint64_t written_end = 0;  // one past the last position any step wrote
+  uint32_t reused = 0;       // prompt tokens the last generation took from the caches
   std::vector<uint32_t> edit_words;
   // Buffers of a variants step (frz_generate_variants), grown on demand:
   // each layer's caches once per variant, `rows` rows of logits and
@@ -830,6 +831,8 @@ int frz_model_read_capture(frz_model* m, uint32_t* out, uint64_t words) {
   return check_hip(hipStreamSynchronize(m->dev->stream), "read capture sync");
 }
 
+uint32_t frz_model_reused(const frz_model* m) { return m ? m->reused : 0; }
+
 int frz_model_set_graphs(frz_model* m, int enabled) {
   if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_graphs: null model");
   m->use_graphs = enabled != 0;
@@ -1035,6 +1038,15 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   if ((uint64_t)prompt_len + max_tokens > (uint64_t)c.context) {
     return fail(FRZ_ERR_ARGUMENT, "frz_generate: prompt and reply exceed the context");
   }
+  // A token past the vocabulary is refused before anything runs, by its
+  // index (runtime.h: TurnFailure::Kept).
+  for (uint32_t i = 0; i < prompt_len; ++i) {
+    if (prompt[i] >= (uint32_t)c.vocab) {
+      return fail(FRZ_ERR_ARGUMENT, "frz_generate: prompt token " + std::to_string(i) +
+                                        " (id " + std::to_string(prompt[i]) +
+                                        ") is past the vocabulary");
+    }
+  }
   const uint32_t origin = prompt_len - 1;
   std::vector<uint32_t> placed =
       place_table(c, edit_table ? edit_table : nullptr, edit_table ? edit_words : 0, origin);
@@ -1049,6 +1061,7 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   common = std::min(common, prompt_len - 1);
   // A sliding layer's ring must still hold the window before the resume.
   if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
+  m->reused = common;
   uint32_t pos = common;
   while (pos < prompt_len) {
     const uint32_t n = std::min<uint32_t>(kPrefillBlock, prompt_len - pos);
@@ -1183,6 +1196,7 @@ int frz_generate_variants(frz_model* m, const uint32_t* prompt, uint32_t prompt_
     ++common;
   common = std::min(common, first_edit_difference(c, m->cached_edits, none));
   if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
+  m->reused = common;
   for (uint32_t pos = common; pos < origin;) {
     const uint32_t n = std::min<uint32_t>(kPrefillBlock, origin - pos);
     if (int rc = model_step(m, pos, n, prompt + pos, 0, sampling)) return rc;

@@ -257,6 +257,11 @@ class Model:
             check(self.lib.frz_model_set_tensor_format(self.handle, layer, _lib.ROLE[role], fmt,
                                                        a.ctypes.data, a.nbytes))
 
+    @property
+    def reused(self):
+        """Prompt tokens the last generate() took from the caches."""
+        return int(self.lib.frz_model_reused(self.handle))
+
     def set_capture(self, on=True):
         """The capture store on or off: while on, the step that ends a
         prompt writes it."""

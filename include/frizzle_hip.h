@@ -347,6 +347,10 @@ int frz_model_set_tensor_format(frz_model* model, int layer, int role,
 int frz_model_synthesize(frz_model* model, uint64_t seed);
 /* The shapes the model was created with. */
 int frz_model_get_config(const frz_model* model, frz_model_config* out);
+/* Prompt tokens the last frz_generate (or frz_generate_variants) took from
+ * the caches rather than computing them (the reference's Reply::reused,
+ * runtime/runtime.h; the reuse rule of cache/prefix.h:87-94). */
+uint32_t frz_model_reused(const frz_model* model);
 /* The capture store on or off (off when created). While on, the step that
  * ends a prompt (a step asking for logits that is not a fed decode step)
  * writes every word of the store at its last row: Engine::inspect's and a
