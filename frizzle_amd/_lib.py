@@ -150,6 +150,16 @@ _SIGS = {
     "frz_model_get_config": (c_int, [_P, POINTER(ModelConfig)]),
     "frz_capture_words": (c_uint64, [POINTER(ModelConfig), POINTER(c_uint64)]),
     "frz_model_set_capture": (c_int, [_P, c_int]),
+    "frz_tokenizer_open": (c_int, [_S, POINTER(c_void_p)]),
+    "frz_tokenizer_free": (None, [_P]),
+    "frz_tokenizer_size": (c_uint32, [_P]),
+    "frz_tokenizer_longest_cover": (c_uint32, [_P]),
+    "frz_tokenizer_token": (c_int, [_P, c_uint32, POINTER(_S), POINTER(c_uint32),
+                                    POINTER(ctypes.c_int32), POINTER(c_float)]),
+    "frz_tokenizer_encode": (c_int, [_P, _S, c_uint64, c_uint32, _P, c_uint64, POINTER(c_uint64),
+                                     _P]),
+    "frz_tokenizer_decode": (c_int, [_P, _P, c_uint32, _P, c_uint64, POINTER(c_uint64)]),
+    "frz_tokenizer_texts": (c_int, [_P, _P, c_uint32, _P, c_uint64, POINTER(c_uint64), _P]),
     "frz_model_reused": (c_uint32, [_P]),
     "frz_model_read_capture": (c_int, [_P, _P, c_uint64]),
     "frz_capture_layer": (c_int, [POINTER(ModelConfig), c_int, POINTER(CaptureSlots)]),

@@ -297,4 +297,38 @@ int read_index(const uint8_t* front, uint64_t resident, uint64_t size, Index& ou
   return kOk;
 }
 
+File::~File() {
+  if (f) std::fclose(f);
+}
+
+bool File::open(const char* path) {
+  f = std::fopen(path, "rb");
+  if (!f || fseeko(f, 0, SEEK_END) != 0) return false;
+  const off_t end = ftello(f);
+  if (end < 0) return false;
+  size = (uint64_t)end;
+  return true;
+}
+
+bool File::read(uint64_t offset, void* out, uint64_t bytes) {
+  return fseeko(f, (off_t)offset, SEEK_SET) == 0 && std::fread(out, 1, bytes, f) == bytes;
+}
+
+int read_file(File& file, Index& out) {
+  std::vector<uint8_t> front;
+  uint64_t resident = 0;
+  uint64_t want = std::min<uint64_t>(file.size, 16ull << 20);
+  for (;;) {
+    if (want > resident) {
+      front.resize(want);
+      if (!file.read(resident, front.data() + resident, want - resident)) return -1;
+      resident = want;
+    }
+    uint64_t needed = 0;
+    const int e = read_index(front.data(), resident, file.size, out, &needed);
+    if (e != kNeedMoreBytes) return e;
+    want = std::min<uint64_t>(file.size, std::max<uint64_t>(needed, 2 * resident));
+  }
+}
+
 }  // namespace frz::gguf

@@ -16,6 +16,7 @@
 #pragma once
 
 #include <cstdint>
+#include <cstdio>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -115,5 +116,22 @@ struct Index {
 // `needed` is set with kNeedMoreBytes.
 int read_index(const uint8_t* front, uint64_t resident, uint64_t size, Index& out,
                uint64_t* needed);
+
+// A file read by offset.
+struct File {
+  std::FILE* f = nullptr;
+  uint64_t size = 0;
+  File() = default;
+  File(const File&) = delete;
+  File& operator=(const File&) = delete;
+  ~File();
+  bool open(const char* path);
+  bool read(uint64_t offset, void* out, uint64_t bytes);
+};
+
+// The index of a whole file, its front read as the reader asks for it (at
+// least doubling a round). -1 when the file cannot be read, else read_index's
+// result.
+int read_file(File& file, Index& out);
 
 }  // namespace frz::gguf

@@ -56,45 +56,6 @@ bool as_u32(const Meta& m, uint32_t* out) {
   }
 }
 
-struct File {
-  std::FILE* f = nullptr;
-  uint64_t size = 0;
-  ~File() {
-    if (f) std::fclose(f);
-  }
-  bool open(const char* path) {
-    f = std::fopen(path, "rb");
-    if (!f || fseeko(f, 0, SEEK_END) != 0) return false;
-    const off_t end = ftello(f);
-    if (end < 0) return false;
-    size = (uint64_t)end;
-    return true;
-  }
-  bool read(uint64_t offset, void* out, uint64_t bytes) {
-    return fseeko(f, (off_t)offset, SEEK_SET) == 0 &&
-           std::fread(out, 1, bytes, f) == bytes;
-  }
-};
-
-// Reads the index from the file's front, growing the front as the reader
-// asks (it asks one field at a time, so the front at least doubles a round).
-int read_file_index(File& file, Index& out) {
-  std::vector<uint8_t> front;
-  uint64_t resident = 0;
-  uint64_t want = std::min<uint64_t>(file.size, 16ull << 20);
-  for (;;) {
-    if (want > resident) {
-      front.resize(want);
-      if (!file.read(resident, front.data() + resident, want - resident)) return -1;
-      resident = want;
-    }
-    uint64_t needed = 0;
-    const int e = frz::gguf::read_index(front.data(), resident, file.size, out, &needed);
-    if (e != frz::gguf::kNeedMoreBytes) return e;
-    want = std::min<uint64_t>(file.size, std::max<uint64_t>(needed, 2 * resident));
-  }
-}
-
 struct RoleName {
   int role;
   const char* name;
@@ -153,10 +114,10 @@ int frz_gguf_read(const void* front, uint64_t resident, uint64_t file_size, frz_
 
 int frz_gguf_open(const char* path, frz_gguf** out) {
   if (!path || !out) return -1;
-  File file;
+  frz::gguf::File file;
   if (!file.open(path)) return -1;
   auto g = std::make_unique<frz_gguf>();
-  const int e = read_file_index(file, g->index);
+  const int e = frz::gguf::read_file(file, g->index);
   if (e == frz::gguf::kOk) *out = g.release();
   return e;
 }
@@ -291,10 +252,10 @@ int frz_model_load_gguf(frz_model* model, const char* path) {
   if (!model || !path) return fail(FRZ_ERR_ARGUMENT, "frz_model_load_gguf: null argument");
   frz_model_config c;
   if (int rc = frz_model_get_config(model, &c)) return rc;
-  File file;
+  frz::gguf::File file;
   if (!file.open(path)) return fail(FRZ_ERR_ARGUMENT, std::string("cannot open ") + path);
   frz_gguf g;
-  if (int e = read_file_index(file, g.index)) {
+  if (int e = frz::gguf::read_file(file, g.index)) {
     return fail(FRZ_ERR_ARGUMENT, std::string(path) + ": " +
                                       (e < 0 ? "read failed" : frz::gguf::error_text(e)));
   }

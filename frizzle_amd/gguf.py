@@ -210,11 +210,12 @@ def _extents(cfg, role):
     }.get(role, [cfg.hidden])
 
 
-def write_gemma3(path, cfg, tensor, name="synthetic gemma3", formats=None):
+def write_gemma3(path, cfg, tensor, name="synthetic gemma3", formats=None, metadata=()):
     """A Gemma 3 GGUF file of cfg's shapes. tensor(layer, role) gives a
     role's bytes as the library's roles hold them (Q4_0 matrices, F32
     gains); layer -1 for "embedding" and "output_norm". `formats` may give a
-    tensor name another format number (to write files this backend refuses)."""
+    tensor name another format number (to write files this backend refuses);
+    `metadata` adds entries (key, value type, value), such as a tokenizer's."""
     formats = formats or {}
     md = [
         ("general.architecture", STRING, "gemma3"),
@@ -233,7 +234,7 @@ def write_gemma3(path, cfg, tensor, name="synthetic gemma3", formats=None):
         ("gemma3.rope.freq_base_swa", F32, cfg.rope_local),
         ("gemma3.attention.sliding_window", U32, cfg.window),
         ("gemma3.attention.sliding_window_pattern", U32, cfg.pattern),
-    ]
+    ] + list(metadata)
 
     def fmt(tname, role):
         return formats.get(tname, T_F32 if "norm" in role else T_Q4_0)

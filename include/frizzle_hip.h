@@ -328,6 +328,62 @@ uint64_t frz_capture_words(const frz_model_config* config,
 int frz_capture_layer(const frz_model_config* config, int layer,
                       frz_capture_slots* out);
 
+/* ---- the tokenizer (src/core/tokenizer/tokenizer.h:124-247,
+ *      bpe/sentencepiece_bpe.h:21-92) --------------------------------------
+ * Gemma 3's SentencePiece BPE ("llama" in tokenizer.ggml.model), loaded
+ * from a GGUF file's tokenizer.ggml.tokens, scores and token_type. Host
+ * only: no device is needed. Encoding turns rendered text into ids: each
+ * space becomes U+2581, control and user-defined tokens written as text
+ * become their single ids (longest match from the left), every other
+ * character its normal token or byte tokens, then adjacent normal symbols
+ * merge, the highest-scoring token first, the leftmost on a tie. Nothing is
+ * added: BOS is the template's text. Decoding gives each token's bytes (a
+ * normal token's U+2581 as a space, a byte token's byte, any other token's
+ * text as written). */
+typedef struct frz_tokenizer frz_tokenizer;
+enum frz_encode_error {
+  FRZ_ENCODE_OK = 0,
+  FRZ_ENCODE_INVALID_UTF8 = 1,
+  FRZ_ENCODE_TOO_MANY_TOKENS = 2, /* more, at least, than max_tokens */
+  FRZ_ENCODE_TOO_LONG = 3         /* past 512 KiB of normalized text */
+};
+#define FRZ_NO_TOKEN_LIMIT 0xFFFFFFFFu
+/* EncodeResult (tokenizer.h:194-201). */
+typedef struct frz_encode_result {
+  int error; /* frz_encode_error */
+  uint64_t least_tokens;
+  uint64_t normalized_bytes;
+  uint64_t raw_bytes;
+} frz_encode_result;
+/* Algorithm::load for the file's tokenizer; a refusal names its key. */
+int frz_tokenizer_open(const char* gguf_path, frz_tokenizer** out);
+void frz_tokenizer_free(frz_tokenizer* tokenizer);
+uint32_t frz_tokenizer_size(const frz_tokenizer* tokenizer);
+/* The longest token text, in bytes (tokenizer.h:70-72; 48 for Gemma 3). */
+uint32_t frz_tokenizer_longest_cover(const frz_tokenizer* tokenizer);
+/* A token's text as the file spells it, its type (1 normal, 2 unknown,
+ * 3 control, 4 user-defined, 5 unused, 6 byte) and score. */
+int frz_tokenizer_token(const frz_tokenizer* tokenizer, uint32_t id,
+                        const char** text, uint32_t* bytes, int32_t* type,
+                        float* score);
+/* Tokenizer::encode: *count gets the ids' count and the first min(count,
+ * cap) are written to ids; a refusal (result->error) writes none. */
+int frz_tokenizer_encode(const frz_tokenizer* tokenizer, const char* text,
+                         uint64_t bytes, uint32_t max_tokens, uint32_t* ids,
+                         uint64_t cap, uint64_t* count,
+                         frz_encode_result* result);
+/* Tokenizer::decode of each id in turn: their bytes, *bytes of them (the
+ * first cap written). */
+int frz_tokenizer_decode(const frz_tokenizer* tokenizer, const uint32_t* ids,
+                         uint32_t n, char* out, uint64_t cap, uint64_t* bytes);
+/* A turn's input as text (detokenizer.h: texts): each id's text as a fresh
+ * UTF-8 stream gives it, whole characters only, the last's with what ending
+ * the stream gives (U+FFFD where bytes were pending); token i's text is
+ * pool[offsets[i], offsets[i + 1]), n + 1 offsets. */
+int frz_tokenizer_texts(const frz_tokenizer* tokenizer, const uint32_t* ids,
+                        uint32_t n, char* pool, uint64_t cap,
+                        uint64_t* pool_bytes, uint64_t* offsets);
+
 typedef struct frz_model frz_model;
 
 int frz_model_create(frz_device* dev, const frz_model_config* config,
