@@ -264,6 +264,32 @@ def steered_batch(fz, model, dev, cfg, seed, prompt_len=1024, variants=16, token
             "replies_identical_with_capture": bool(same)}
 
 
+# One local layer's single-token decode (its five launches): algorithmic bytes
+# = its Q4_0 weights, its gains, its 512 keys and values read (F16), and the
+# activation rows its launches read and write.
+LAYER_WEIGHT_BYTES = 15_095_808
+LAYER_GAIN_BYTES = 4 * (4 * 1152 + 2 * 256)
+LAYER_KV_BYTES = 512 * 2 * 256 * 2
+LAYER_ACT_BYTES = 4 * (3 * 1152 + 1536 + 1024 + 3 * 1152 + 2 * 6912 + 1152)
+
+
+def one_layer(fz, model, cfg, seed, position, iters=500):
+    """Config 2: layer 0 (a sliding layer) decoding one token at `position`
+    over its 512-key window, with 8 seeded pins in [-10, 10]."""
+    rng = np.random.default_rng(seed + 11)
+    neurons = sorted(rng.choice(cfg.ffn, 8, replace=False).tolist())
+    pins = [fz.Edit(0, n, fz.EditKind.SET, float(rng.uniform(-10, 10))) for n in neurons]
+    model.set_edits(fz.edit_table(pins, cfg.layers, 0))
+    us = model.time_layer(0, position, iters)
+    total = LAYER_WEIGHT_BYTES + LAYER_GAIN_BYTES + LAYER_KV_BYTES + LAYER_ACT_BYTES
+    return {"workload": f"layer 0 (sliding, window 512) of the 26-layer model, one token at "
+                        f"position {position}, 8 seeded pins in [-10, 10], its 5 launches "
+                        "replayed as a graph",
+            "us_per_layer": us, "algorithmic_bytes": total,
+            "achieved_gbs": total / (us * 1e-6) / 1e9,
+            "frac": total / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def timed_decode(model, dev, prompt, warmup, steps, greedy):
     """The prompt in 512-token steps, `warmup` decode steps, then `steps`
     timed ones: (prefill seconds, wall seconds, µs/step by HIP events)."""
@@ -390,6 +416,10 @@ def main():
     log(f"decode {args.steps} steps: {ms_per_step * 1000:.1f} us/step wall, "
         f"{us_events:.1f} us/step events")
 
+    # Config 2: one local layer's decode, at the position the decode reached.
+    layer = one_layer(fz, model, cfg, args.seed, args.prompt + args.warmup + args.steps)
+    log(f"one layer: {layer['us_per_layer']:.2f} us, {layer['achieved_gbs']:.0f} GB/s")
+
     # Config 5: the batch of steered variants.
     steered = None
     if not args.no_steered:
@@ -441,6 +471,7 @@ def main():
                      "us_per_launch": us, "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,
         "parity": parity,
+        "one_layer": layer,
         "pinned_formats": pinned,
         "steered_batch": steered,
         "prefill": {"workload": f"Gemma-3-1B Q4_0 prefill of {PREFILL_TOKENS} seeded ids in "

@@ -161,6 +161,7 @@ _SIGS = {
     "frz_tokenizer_decode": (c_int, [_P, _P, c_uint32, _P, c_uint64, POINTER(c_uint64)]),
     "frz_tokenizer_texts": (c_int, [_P, _P, c_uint32, _P, c_uint64, POINTER(c_uint64), _P]),
     "frz_model_reused": (c_uint32, [_P]),
+    "frz_model_time_layer": (c_int, [_P, c_int, c_uint32, c_uint32, POINTER(c_double)]),
     "frz_model_read_capture": (c_int, [_P, _P, c_uint64]),
     "frz_capture_layer": (c_int, [POINTER(ModelConfig), c_int, POINTER(CaptureSlots)]),
     "frz_generate_variants": (c_int, [_P, _P, c_uint32, c_uint32, _P, c_uint32,

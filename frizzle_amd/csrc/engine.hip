@@ -393,6 +393,69 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   return check_hip(e, "enqueue_rows");
 }
 
+// One layer of a one-token step: Q/K/V with the attention norm in its
+// prologue (layer 0 gathering the embedding there), the fused rope and
+// attention, O (with the fold in its prologue for sliding layers), gate-up
+// with the feed-forward norm and the pins, down. `pending` is the last
+// layer's post-feed-forward gain (null at layer 0).
+hipError_t enqueue_decode_layer(frz_model* m, int l, const float* pending) {
+  const frz_model_config& c = m->c;
+  hipStream_t s = m->dev->stream;
+  const int H = c.hidden;
+  const Layer& L = m->layers[l];
+  GemvInput in{};
+  in.hidden = m->hidden_b;
+  in.output = m->output;
+  in.post_gain = pending;
+  in.gain = L.gains[0];
+  in.hidden_out = m->hidden;
+  in.table = m->embedding;
+  in.sampled = m->sampled;
+  in.scale = std::sqrt((float)H);
+  in.epsilon = c.epsilon;
+  hipError_t e = launch_gemv_decode(s, m->step, L.qkv, in, l == 0 ? 2 : 1, m->qkv);
+  if (e == hipSuccess) {
+    DecodeAttentionArgs d{m->qkv,      L.turns,  L.gains[1],  L.gains[2], L.kcache,
+                          L.vcache,    m->partials, m->partials + m->partial_floats, L.slots,
+                          L.window,    c.head_dim, c.query_heads, c.kv_heads, L.max_chunks,
+                          c.epsilon,   scale_log2e_of(c)};
+    e = launch_attention_decode(s, m->step, d);
+  }
+  // O: local layers fold their few chunks in the product's prologue.
+  if (e == hipSuccess) {
+    GemvInput x{};
+    if (L.max_chunks <= kFoldPrologueChunks) {
+      x.partials = m->partials;
+      x.stats = m->partials + m->partial_floats;
+      x.window = L.window;
+      e = launch_gemv_decode(s, m->step, L.o, x, 3, m->output);
+    } else {
+      e = launch_attention_fold(
+          s, m->step,
+          FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window, L.max_chunks},
+          1);
+      x.x = m->attn;
+      if (e == hipSuccess) e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+    }
+  }
+  if (e == hipSuccess) {
+    GemvInput g{};
+    g.hidden = m->hidden;
+    g.output = m->output;
+    g.post_gain = L.gains[3];
+    g.gain = L.gains[4];
+    g.hidden_out = m->hidden_b;
+    g.epsilon = c.epsilon;
+    e = launch_gated_decode(s, m->step, L.gate, L.up, g, 1, m->act, m->edits, l);
+  }
+  if (e == hipSuccess) {
+    GemvInput x{};
+    x.x = m->act;
+    e = launch_gemv_decode(s, m->step, L.down, x, 0, m->output);
+  }
+  return e;
+}
+
 // A step of one token: five launches a layer, each norm inside the product
 // that reads it. The hidden row alternates between two buffers: Q/K/V's
 // prologue reads hidden_b (layer 0: the embedding) and writes hidden;
@@ -400,67 +463,15 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
 int enqueue_decode(frz_model* m, bool logits, bool advance) {
   const frz_model_config& c = m->c;
   hipStream_t s = m->dev->stream;
-  const int H = c.hidden, qw = c.query_heads * c.head_dim;
-  const float scale_log2e = scale_log2e_of(c);
   hipError_t e = hipSuccess;
   const float* pending = nullptr;
   for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
-    const Layer& L = m->layers[l];
-    GemvInput in{};
-    in.hidden = m->hidden_b;
-    in.output = m->output;
-    in.post_gain = pending;
-    in.gain = L.gains[0];
-    in.hidden_out = m->hidden;
-    in.table = m->embedding;
-    in.sampled = m->sampled;
-    in.scale = std::sqrt((float)H);
-    in.epsilon = c.epsilon;
-    e = launch_gemv_decode(s, m->step, L.qkv, in, l == 0 ? 2 : 1, m->qkv);
-    if (e == hipSuccess) {
-      DecodeAttentionArgs d{m->qkv,      L.turns,  L.gains[1],  L.gains[2], L.kcache,
-                            L.vcache,    m->partials, m->partials + m->partial_floats, L.slots,
-                            L.window,    c.head_dim, c.query_heads, c.kv_heads, L.max_chunks,
-                            c.epsilon,   scale_log2e};
-      e = launch_attention_decode(s, m->step, d);
-    }
-    // O: local layers fold their few chunks in the product's prologue.
-    if (e == hipSuccess) {
-      GemvInput x{};
-      if (L.max_chunks <= kFoldPrologueChunks) {
-        x.partials = m->partials;
-        x.stats = m->partials + m->partial_floats;
-        x.window = L.window;
-        e = launch_gemv_decode(s, m->step, L.o, x, 3, m->output);
-      } else {
-        e = launch_attention_fold(
-            s, m->step,
-            FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window, L.max_chunks},
-            1);
-        x.x = m->attn;
-        if (e == hipSuccess) e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
-      }
-    }
-    if (e == hipSuccess) {
-      GemvInput g{};
-      g.hidden = m->hidden;
-      g.output = m->output;
-      g.post_gain = L.gains[3];
-      g.gain = L.gains[4];
-      g.hidden_out = m->hidden_b;
-      g.epsilon = c.epsilon;
-      e = launch_gated_decode(s, m->step, L.gate, L.up, g, 1, m->act, m->edits, l);
-    }
-    if (e == hipSuccess) {
-      GemvInput x{};
-      x.x = m->act;
-      e = launch_gemv_decode(s, m->step, L.down, x, 0, m->output);
-    }
-    pending = L.gains[5];
+    e = enqueue_decode_layer(m, l, pending);
+    pending = m->layers[l].gains[5];
   }
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden_b, m->normed,
-                        c.epsilon, H, true};
+                        c.epsilon, c.hidden, true};
     e = launch_norm(s, m->step, final_norm, 1);
   }
   if (logits && e == hipSuccess) e = enqueue_output(m, 1, advance);
@@ -988,6 +999,51 @@ int frz_model_time_decode(frz_model* m, uint32_t position, uint32_t steps,
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   *us_per_step = (double)ms * 1000.0 / steps;
+  return rc;
+}
+
+int frz_model_time_layer(frz_model* m, int layer, uint32_t position, uint32_t iters,
+                         double* us_per_layer) {
+  if (!m || !us_per_layer || iters == 0 || layer < 0 || layer >= m->c.layers ||
+      position >= (uint32_t)m->c.context) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_time_layer: bad argument");
+  }
+  DevStep& st = *m->step_host;
+  std::memset(&st, 0, sizeof st);
+  st.position = position;
+  st.tokens = 1;
+  st.fed = 1;
+  if (int rc = put_step(m)) return rc;
+  hipStream_t s = m->dev->stream;
+  // The layer's launches as one graph, replayed: each replay rewrites the
+  // same cache slot with the same key and value.
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  if (int rc = check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "capture"))
+    return rc;
+  const hipError_t e =
+      enqueue_decode_layer(m, layer, layer > 0 ? m->layers[layer - 1].gains[5] : nullptr);
+  const hipError_t end = hipStreamEndCapture(s, &graph);
+  int rc = check_hip(e != hipSuccess ? e : end, "frz_model_time_layer capture");
+  if (rc == FRZ_OK) rc = check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate");
+  hipEvent_t a = nullptr, b = nullptr;
+  if (rc == FRZ_OK) {
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    rc = check_hip(hipGraphLaunch(exec, s), "warm-up");
+    if (rc == FRZ_OK) (void)hipEventRecord(a, s);
+    for (uint32_t i = 0; i < iters && rc == FRZ_OK; ++i) rc = check_hip(hipGraphLaunch(exec, s), "replay");
+    if (rc == FRZ_OK) (void)hipEventRecord(b, s);
+    if (rc == FRZ_OK) rc = check_hip(hipEventSynchronize(b), "hipEventSynchronize");
+    float ms = 0.0f;
+    if (rc == FRZ_OK) (void)hipEventElapsedTime(&ms, a, b);
+    *us_per_layer = (double)ms * 1000.0 / iters;
+  }
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  forget_prefix(m);  // its caches' slot at `position` was rewritten
   return rc;
 }
 

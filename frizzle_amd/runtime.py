@@ -257,6 +257,12 @@ class Model:
             check(self.lib.frz_model_set_tensor_format(self.handle, layer, _lib.ROLE[role], fmt,
                                                        a.ctypes.data, a.nbytes))
 
+    def time_layer(self, layer, position, iters=200):
+        """µs of one layer's one-token decode launches, replayed as a graph."""
+        us = ctypes.c_double()
+        check(self.lib.frz_model_time_layer(self.handle, layer, position, iters, byref(us)))
+        return us.value
+
     @property
     def reused(self):
         """Prompt tokens the last generate() took from the caches."""

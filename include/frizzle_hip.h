@@ -403,6 +403,14 @@ int frz_model_set_tensor_format(frz_model* model, int layer, int role,
 int frz_model_synthesize(frz_model* model, uint64_t seed);
 /* The shapes the model was created with. */
 int frz_model_get_config(const frz_model* model, frz_model_config* out);
+/* One layer's launches of a one-token decode step at `position` (attention
+ * norm and Q/K/V, rope and attention, O, feed-forward norm and gate-up with
+ * the layer's pins, down), captured as one graph and replayed `iters` times,
+ * timed with HIP events on the model's stream: the per-layer decode time of
+ * the reference's one-layer decode configuration. The caches must hold the
+ * context; the layer's slot at `position` is rewritten. */
+int frz_model_time_layer(frz_model* model, int layer, uint32_t position,
+                         uint32_t iters, double* us_per_layer);
 /* Prompt tokens the last frz_generate (or frz_generate_variants) took from
  * the caches rather than computing them (the reference's Reply::reused,
  * runtime/runtime.h; the reuse rule of cache/prefix.h:87-94). */

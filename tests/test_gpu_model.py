@@ -171,6 +171,20 @@ def test_prompt_reuse_forgotten_after_direct_steps(device):
     model.close()
 
 
+def test_layer_timing_leaves_generation_exact(device):
+    # Timing a layer replays its launches at one position; the next
+    # generation starts over and is exact.
+    cfg = small_config()
+    model, oracle = build_pair(device, cfg, seed=19)
+    prompt = np.random.default_rng(20).integers(0, cfg.vocab, 70).astype(np.uint32)
+    model.generate(prompt, max_tokens=4)
+    for layer in range(cfg.layers):
+        assert model.time_layer(layer, len(prompt) + 2, iters=20) > 0
+    want, _ = oracle_run(oracle, prompt, 6, cfg)
+    assert np.array_equal(model.generate(prompt, max_tokens=6), want)
+    model.close()
+
+
 # ---- GGUF files -------------------------------------------------------------------
 
 def _synth_all(cfg, seed):
