@@ -12,19 +12,25 @@
 // The products keep the reference's order of addition (matmul.h:88-97):
 // range r of a row is groups floor(r G / 32) .. floor((r + 1) G / 32), its
 // products chained by fma from zero; the 32 range sums add in order to a
-// total from zero. Lane r of a half-wave takes range (r + j) mod 32 of the
-// half-wave's row j: the rotation spreads each row's longer ranges over
-// different lanes (at K = 1,152, four ranges of 32 hold two groups). A lane's
-// plan (which groups, where each range sum goes) is fixed for the kernel;
-// a tile only moves it by whole rows.
+// total from zero. Three lane layouts:
+//   one row a half-wave, lane r range r: the total is a DPP chain across
+//     the half-wave, with no LDS (the write products, K other than 1,152);
+//   K = 1,152 (`pair`): 18 lanes a row, each exactly two groups, so no lane
+//     idles through a second group; sums meet in LDS;
+//   two rows a half-wave (the 262,144-row head) and the gated product: lane
+//     r takes range (r + j) mod 32 of row j, which spreads each row's longer
+//     ranges over different lanes; sums meet in LDS.
+// A lane's plan (which groups, where each range sum goes) is fixed for the
+// kernel; a tile only moves it by whole rows.
 //
 // Latency: a workgroup issues its input loads, then its weight loads, then
 // makes the input row while the weights are in flight. Loads return in issue
 // order, so every load is issued unconditionally (out-of-range indexes
 // clamped, values unused) and the code stays straight-line: a wait for the
-// input row is then a wait for its own loads only. After the input row is
-// staged, each half-wave works alone: it writes its range sums to LDS and
-// totals its own rows, with no workgroup barrier.
+// input row is then a wait for its own loads only. Where the input of a
+// lane's groups fits in registers it is read from LDS before the weights are
+// waited for. Totals read all 32 sums before adding, so one LDS round trip
+// precedes the serial adds.
 
 #include "attention_common.h"
 #include "kernels.h"
@@ -65,36 +71,82 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // One group's 32 products chained into acc, weights in order: the 16 low
 // nibbles (code byte j's low nibble is weight j), then the 16 high nibbles.
-// Weight j is (q_j - 8) d (q4_0.wgsl:71-83), formed exactly: the nibble goes
-// into the mantissa of the half 1024 + q, and fma(1024 + q, d, -1032 d) in
-// single precision is (q - 8) d before its one rounding, which is exact, as
-// is -1032 d (1032 = 8 * 129 needs 8 bits, d 11). Two nibbles make a half2
-// with one bitwise select, and the fma reads the half operands directly.
-__device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits, const float* xg) {
-  const _Float16 dh = __builtin_bit_cast(_Float16, dbits);
-  const float bias = -1032.0f * (float)dh;
+// Weight j is (q_j - 8) d (q4_0.wgsl:71-83), formed exactly in one mixed
+// fma whose half operand carries the nibble under the exponent of 1024:
+//   a low nibble, masked in place, is the half 1024 + q, and
+//     fma(1024 + q, d, -1032 d) = (q - 8) d;
+//   a high nibble, masked in place, is 1024 + 16 q, and
+//     fma(1024 + 16 q, d / 16, -72 d) = 64 d + q d - 72 d = (q - 8) d.
+// Each is rounded once and exact, since (q - 8) d needs 15 bits; d / 16,
+// -72 d and -1032 d are exact in single precision. One bitwise select makes
+// two halves (bytes 0 and 2, or 1 and 3, of a word), so a word's 8 weights
+// take 1 shift and 4 selects. `x(i)` is vec4 i of the group's input.
+template <class X>
+__device__ __forceinline__ float chain_q4_0(float acc, uint4 c, uint16_t dbits, X x) {
+  const float d = (float)__builtin_bit_cast(_Float16, dbits);
+  const float bias_lo = -1032.0f * d;
+  const float d16 = d * 0.0625f;
+  const float bias_hi = -72.0f * d;
   const uint32_t words[4] = {c.x, c.y, c.z, c.w};
-  constexpr uint32_t kMask = 0x000F000Fu;
   // The exponent bits come from a register the compiler cannot see into, so
   // that (s & mask) | (exp & ~mask) stays one bitfield insert.
   uint32_t kExp;
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
+  constexpr uint32_t kLo = 0x000F000Fu, kHi = 0x00F000F0u;
+  half2v lo_a[4], lo_b[4], hi_a[4], hi_b[4];
 #pragma unroll
-  for (int hi = 0; hi < 2; ++hi) {
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t s = words[w], s8 = words[w] >> 8;
+    lo_a[w] = __builtin_bit_cast(half2v, (s & kLo) | (kExp & ~kLo));    // weights 4w, 4w + 2
+    lo_b[w] = __builtin_bit_cast(half2v, (s8 & kLo) | (kExp & ~kLo));   // 4w + 1, 4w + 3
+    hi_a[w] = __builtin_bit_cast(half2v, (s & kHi) | (kExp & ~kHi));    // 4w + 16, 4w + 18
+    hi_b[w] = __builtin_bit_cast(half2v, (s8 & kHi) | (kExp & ~kHi));   // 4w + 17, 4w + 19
+  }
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float4 x = *reinterpret_cast<const float4*>(xg + 16 * hi + 4 * w);
-      const uint32_t s = words[w] >> (4 * hi);
-      // a: bytes 0 and 2 of the word; b: bytes 1 and 3.
-      const half2v a = __builtin_bit_cast(half2v, (s & kMask) | (kExp & ~kMask));
-      const half2v b = __builtin_bit_cast(half2v, ((s >> 8) & kMask) | (kExp & ~kMask));
-      acc = fmaf_(__builtin_fmaf((float)a.x, (float)dh, bias), x.x, acc);
-      acc = fmaf_(__builtin_fmaf((float)b.x, (float)dh, bias), x.y, acc);
-      acc = fmaf_(__builtin_fmaf((float)a.y, (float)dh, bias), x.z, acc);
-      acc = fmaf_(__builtin_fmaf((float)b.y, (float)dh, bias), x.w, acc);
-    }
+  for (int w = 0; w < 4; ++w) {
+    const float4 v = x(w);
+    acc = fmaf_(__builtin_fmaf((float)lo_a[w].x, d, bias_lo), v.x, acc);
+    acc = fmaf_(__builtin_fmaf((float)lo_b[w].x, d, bias_lo), v.y, acc);
+    acc = fmaf_(__builtin_fmaf((float)lo_a[w].y, d, bias_lo), v.z, acc);
+    acc = fmaf_(__builtin_fmaf((float)lo_b[w].y, d, bias_lo), v.w, acc);
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 v = x(4 + w);
+    acc = fmaf_(__builtin_fmaf((float)hi_a[w].x, d16, bias_hi), v.x, acc);
+    acc = fmaf_(__builtin_fmaf((float)hi_b[w].x, d16, bias_hi), v.y, acc);
+    acc = fmaf_(__builtin_fmaf((float)hi_a[w].y, d16, bias_hi), v.z, acc);
+    acc = fmaf_(__builtin_fmaf((float)hi_b[w].y, d16, bias_hi), v.w, acc);
   }
   return acc;
+}
+
+// The group's input staged in LDS at xg.
+__device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits, const float* xg) {
+  return chain_q4_0(acc, c, dbits, [xg](int i) { return ld4(xg + 4 * i); });
+}
+
+// The group's input held in registers.
+__device__ __forceinline__ float chain_group(float acc, uint4 c, uint16_t dbits,
+                                             const float4 (&xv)[8]) {
+  return chain_q4_0(acc, c, dbits, [&xv](int i) { return xv[i]; });
+}
+
+// The in-order total of each half-wave's 32 lane values, ((0 + s0) + s1) ...
+// + s31 (matmul.h:88-97), without LDS: step k moves every lane's running
+// value one lane up (DPP wave_shr:1) and adds the lane's own, so after step
+// k lane i holds ((0 + s[i-k]) + ...) + s[i]. Lanes 31 and 63 end with their
+// half-waves' totals; the running value stays first operand, as in a serial
+// sum.
+__device__ __forceinline__ float half_wave_total(float s) {
+  float t = 0.0f + s;
+#pragma unroll
+  for (int k = 1; k < 32; ++k) {
+    const float prev = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x138, 0xF, 0xF, false));
+    t = prev + s;
+  }
+  return t;
 }
 
 // Q8_0: weight k = qs[k] d (q8_0.wgsl:12-24), qs signed. A code flipped to
@@ -548,6 +600,19 @@ __device__ __forceinline__ void load_neuron(LaneWeights<MAXI>& W, const LanePlan
   }
 }
 
+// Item it's group chained into acc, in the weights' format.
+template <int MAXI, int F>
+__device__ __forceinline__ float lane_chain_item(float acc, const LaneWeights<MAXI, F>& W, int it,
+                                                 const float* xg) {
+  if constexpr (F == kQ8_0) {
+    return chain_group_q8_0(acc, W.codes[2 * it], W.codes[2 * it + 1], W.scale[it], xg);
+  } else if constexpr (F == kQ4_1) {
+    return chain_group_q4_1(acc, W.codes[it], W.scale[it], xg);
+  } else {
+    return chain_group(acc, W.codes[it], W.scale[it], xg);
+  }
+}
+
 // The lane's chains; each range's sum goes to its parts entry.
 template <int RH, int MAXI, int F = kQ4_0>
 __device__ __forceinline__ void lane_chains(const LaneWeights<MAXI, F>& W,
@@ -561,14 +626,7 @@ __device__ __forceinline__ void lane_chains(const LaneWeights<MAXI, F>& W,
 #pragma unroll
   for (int it = 0; it < MAXI; ++it) {
     if (P.xoff[it] >= 0) {
-      if constexpr (F == kQ8_0) {
-        acc = chain_group_q8_0(acc, W.codes[2 * it], W.codes[2 * it + 1], W.scale[it],
-                               xs + P.xoff[it]);
-      } else if constexpr (F == kQ4_1) {
-        acc = chain_group_q4_1(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
-      } else {
-        acc = chain_group(acc, W.codes[it], W.scale[it], xs + P.xoff[it]);
-      }
+      acc = lane_chain_item<MAXI, F>(acc, W, it, xs + P.xoff[it]);
       if (P.dest[it] >= 0) {
         parts[P.dest[it]] = acc;
         acc = 0.0f;
@@ -649,6 +707,38 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* _
   load_rows<RH, MAXI, F>(buf[0], plan, w, tile_of(0) * kRows + slot0);
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
+  if constexpr (RH == 1) {
+    // One row a half-wave, lane r its range r: the lane's chain is the range
+    // sum (0 for an empty range, which leaves a total unchanged) and the
+    // total is a DPP chain, with no LDS round trip. Up to two items take
+    // their input into registers before the weights are waited for.
+    static_assert(TPW == 1, "one tile a workgroup");
+    float acc = 0.0f;
+    if constexpr (F == kQ4_0 && MAXI <= 2) {
+      float4 xv[MAXI][8];
+#pragma unroll
+      for (int it = 0; it < MAXI; ++it) {
+        const int xo = max(plan.xoff[it], 0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xv[it][q] = ld4(xs + xo + 4 * q);
+      }
+#pragma unroll
+      for (int it = 0; it < MAXI; ++it) {
+        if (plan.xoff[it] >= 0) acc = chain_group(acc, buf[0].codes[it], buf[0].scale[it], xv[it]);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < MAXI; ++it) {
+        if (plan.xoff[it] >= 0) acc = lane_chain_item<MAXI, F>(acc, buf[0], it, xs + plan.xoff[it]);
+      }
+    }
+    const float total = half_wave_total(acc);
+    if (r == 31) {
+      const int row = tile_of(0) * kRows + slot0;
+      if (row < w.rows) y[row] = total;
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < TPW; ++k) {
     if (k + 1 < TPW) load_rows<RH, MAXI, F>(buf[(k + 1) & 1], plan, w, tile_of(k + 1) * kRows + slot0);
@@ -660,6 +750,117 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* _
     }
     wave_sync();
   }
+}
+
+// ---- K = 1,152: every lane two groups --------------------------------------
+// At K = 1,152 a row's 36 groups make 32 ranges, of which ranges 8p + 7
+// (p < 4) hold two groups (9p + 7, 9p + 8) and the other 28 one each (range
+// r starts at group r + r / 8). With a lane a range, lanes of a two-group
+// range set every wave's length and half the lanes idle through the second
+// group. Here 18 lanes take a row, each exactly two groups:
+//   position p < 4: two-group range 8p + 7, one chain over both groups;
+//   position p >= 4: the one-group ranges i and i + 1 of the 28 in order,
+//     i = 2 (p - 4), two chains from zero (range of the i-th: i + i / 7).
+// The range sums meet in LDS, row-major, and one thread a row adds its 32 in
+// order.
+namespace pair {
+constexpr int kCols = 1152;
+constexpr int kGroups = kCols / 32;
+constexpr int kLanes = 18;   // lanes a row
+constexpr int kStride = 36;  // a row's range sums in LDS (16-byte rows)
+
+struct Plan {
+  int g0, g1;  // the lane's groups
+  int r0, r1;  // their ranges (r0 = -1: one chain over both)
+};
+
+__device__ __forceinline__ Plan plan(int p) {
+  Plan P;
+  if (p < 4) {
+    P.r0 = -1;
+    P.r1 = 8 * p + 7;
+    P.g0 = 9 * p + 7;
+    P.g1 = P.g0 + 1;
+  } else {
+    const int i0 = 2 * (p - 4), i1 = i0 + 1;
+    P.r0 = i0 + i0 / 7;
+    P.r1 = i1 + i1 / 7;
+    P.g0 = P.r0 + (P.r0 >> 3);
+    P.g1 = P.r1 + (P.r1 >> 3);
+  }
+  return P;
+}
+
+template <int T>
+constexpr int rows() { return T / kLanes; }
+
+// Bytes of LDS a workgroup of T threads takes.
+template <int T>
+constexpr size_t lds_bytes() {
+  return (size_t)(rows<T>() * kStride + kRedFloats + kGroups * kXStride) * 4;
+}
+
+// The lane's two chains from its groups and staged input: the range sums
+// (s0 for r0, s1 for r1).
+__device__ __forceinline__ void chains(const Plan& P, uint4 c0, uint16_t d0, uint4 c1, uint16_t d1,
+                                       const float* xs, float& s0, float& s1) {
+  float4 x0[8], x1[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    x0[q] = ld4(xs + P.g0 * kXStride + 4 * q);
+    x1[q] = ld4(xs + P.g1 * kXStride + 4 * q);
+  }
+  s0 = chain_group(0.0f, c0, d0, x0);
+  s1 = chain_group(P.r0 < 0 ? s0 : 0.0f, c1, d1, x1);
+}
+
+// Row `local`'s total from its 32 range sums at sums[local * kStride].
+__device__ __forceinline__ float row_total(const float* sums, int local) {
+  float4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = ld4(sums + local * kStride + 4 * k);
+  float t = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) t = (((t + v[k].x) + v[k].y) + v[k].z) + v[k].w;
+  return t;
+}
+}  // namespace pair
+
+template <int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_pair_kernel(const DevStep* __restrict__ step,
+                                                               QMatrix w, GemvInput in,
+                                                               float* __restrict__ y) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int T = 64 * WAVES;
+  constexpr int kRows = pair::rows<T>();
+  constexpr int X4 = plain_vec4s<1, 2, T>();
+  float* sums = smem;
+  float* red = sums + kRows * pair::kStride;
+  float* xs = red + kRedFloats;
+  const int t = threadIdx.x;
+  const int local = t / pair::kLanes, p = t - local * pair::kLanes;
+  const int row = blockIdx.x * kRows + local;
+  const bool live = local < kRows && row < w.rows;
+  const pair::Plan P = pair::plan(p);
+  Prologue<T, X4> pro;
+  prologue_load<MODE, T, X4>(pro, in, step, w.cols);
+  // Lanes past the rows load row 0's blocks, unused.
+  const int base = live ? row * pair::kGroups : 0;
+  const uint4 c0 = reinterpret_cast<const uint4*>(w.codes)[base + P.g0];
+  const uint16_t d0 = w.scales[base + P.g0];
+  const uint4 c1 = reinterpret_cast<const uint4*>(w.codes)[base + P.g1];
+  const uint16_t d1 = w.scales[base + P.g1];
+  prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
+  __syncthreads();
+  float s0, s1;
+  pair::chains(P, c0, d0, c1, d1, xs, s0, s1);
+  if (live) {
+    if (P.r0 >= 0) sums[local * pair::kStride + P.r0] = s0;
+    sums[local * pair::kStride + P.r1] = s1;
+  }
+  __syncthreads();
+  if (t < kRows && blockIdx.x * kRows + t < w.rows)
+    y[blockIdx.x * kRows + t] = pair::row_total(sums, t);
 }
 
 // Gated product: each half-wave one neuron n, its gate row and its up row
@@ -736,6 +937,15 @@ hipError_t launch_write(hipStream_t s, const DevStep* step, const QMatrix& w, co
   return hipGetLastError();
 }
 
+template <int MODE, int WAVES>
+hipError_t launch_pair(hipStream_t s, const DevStep* step, const QMatrix& w, const GemvInput& in,
+                       float* y) {
+  constexpr int T = 64 * WAVES, kRows = pair::rows<T>();
+  hipLaunchKernelGGL((gemv_pair_kernel<MODE, WAVES>), dim3((w.rows + kRows - 1) / kRows), dim3(T),
+                     pair::lds_bytes<T>(), s, step, w, in, y);
+  return hipGetLastError();
+}
+
 template <int MODE, int F = kQ4_0>
 hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
                           const GemvInput& in, float* y) {
@@ -744,6 +954,14 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
   // Many rows: two rows a half-wave, ranges rotated, where that balances.
   if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536)
     return launch_write<2, 3, MODE, kHeadTilesPerGroup, 2, F>(s, step, w, in, y);
+  // K = 1,152 in Q4_0: two groups every lane; four waves (14 rows) share an
+  // input row where there are thousands of rows, two (7 rows) below.
+  if constexpr (F == kQ4_0 && MODE != 3) {
+    if (w.cols == pair::kCols) {
+      return w.rows >= 4096 ? launch_pair<MODE, 4>(s, step, w, in, y)
+                            : launch_pair<MODE, 2>(s, step, w, in, y);
+    }
+  }
   if (items1 <= 1) return launch_write<1, 1, MODE, 1, 2, F>(s, step, w, in, y);
   if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2, F>(s, step, w, in, y);
   if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2, F>(s, step, w, in, y);
