@@ -908,6 +908,64 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   }
 }
 
+// Gated product at K = 1,152: a neuron takes 36 lanes, 18 for its gate row
+// and 18 for its up row, each lane two groups as in the pair layout; then
+// gelu_tanh(gate) * up and the layer's pins.
+template <int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
+    const DevStep* __restrict__ step, QMatrix gate, QMatrix up, GemvInput in,
+    float* __restrict__ act, const uint32_t* __restrict__ edits, int layer) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int T = 64 * WAVES;
+  constexpr int kNeurons = T / (2 * pair::kLanes);
+  static_assert(2 * kNeurons <= 64, "the totals sit in the first wave");
+  constexpr int X4 = plain_vec4s<1, 2, T>();
+  float* sums = smem;  // [neuron][gate, up][pair::kStride]
+  float* red = sums + 2 * kNeurons * pair::kStride;
+  float* xs = red + kRedFloats;
+  const int t = threadIdx.x;
+  const int local = t / (2 * pair::kLanes);
+  const int q = t - local * 2 * pair::kLanes;
+  const int which = q >= pair::kLanes ? 1 : 0;
+  const int n = blockIdx.x * kNeurons + local;
+  const bool live = local < kNeurons && n < gate.rows;
+  uint32_t pin_first = 0, pin_count = 0;
+  if (edits) {
+    pin_first = edits[2 * layer];
+    pin_count = edits[2 * layer + 1];
+  }
+  const pair::Plan P = pair::plan(q - which * pair::kLanes);
+  Prologue<T, X4> pro;
+  prologue_load<MODE, T, X4>(pro, in, step, gate.cols);
+  const QMatrix& m = which ? up : gate;
+  const int base = live ? n * pair::kGroups : 0;
+  const uint4 c0 = reinterpret_cast<const uint4*>(m.codes)[base + P.g0];
+  const uint16_t d0 = m.scales[base + P.g0];
+  const uint4 c1 = reinterpret_cast<const uint4*>(m.codes)[base + P.g1];
+  const uint16_t d1 = m.scales[base + P.g1];
+  prologue_finish<MODE, T, X4>(xs, red, pro, in, step, gate.cols);
+  __syncthreads();
+  float s0, s1;
+  pair::chains(P, c0, d0, c1, d1, xs, s0, s1);
+  const int slot = 2 * local + which;
+  if (live) {
+    if (P.r0 >= 0) sums[slot * pair::kStride + P.r0] = s0;
+    sums[slot * pair::kStride + P.r1] = s1;
+  }
+  __syncthreads();
+  if (t < 64) {
+    // Thread 2k totals neuron k's gate row, thread 2k + 1 its up row.
+    const float total = t < 2 * kNeurons ? pair::row_total(sums, t) : 0.0f;
+    const float u = __shfl_down(total, 1, 64);
+    const int nn = blockIdx.x * kNeurons + (t >> 1);
+    if ((t & 1) == 0 && t < 2 * kNeurons && nn < gate.rows) {
+      float v = gelu_tanh(total) * u;
+      if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)nn, step->position, v);
+      act[nn] = v;
+    }
+  }
+}
+
 int max_items(int cols, int rh) {
   const int groups = cols / 32;
   int most = 0;
@@ -1016,6 +1074,19 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix&
   }
 }
 
+template <int MODE, int WAVES>
+hipError_t launch_gated_pair(hipStream_t s, const DevStep* step, const QMatrix& gate,
+                             const QMatrix& up, const GemvInput& in, float* act,
+                             const uint32_t* edits, int layer) {
+  constexpr int T = 64 * WAVES, kNeurons = T / (2 * pair::kLanes);
+  const size_t lds = (size_t)(2 * kNeurons * pair::kStride + kRedFloats +
+                              pair::kGroups * kXStride) * 4;
+  hipLaunchKernelGGL((gemv_gated_pair_kernel<MODE, WAVES>),
+                     dim3((gate.rows + kNeurons - 1) / kNeurons), dim3(T), lds, s, step, gate, up,
+                     in, act, edits, layer);
+  return hipGetLastError();
+}
+
 hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix& gate,
                                const QMatrix& up, const GemvInput& in, int mode, float* act,
                                const uint32_t* edits, int layer) {
@@ -1024,6 +1095,11 @@ hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix
       gate.cols > kNormMaxCols || (long long)gate.rows * (gate.cols / 32) >= (1ll << 31) ||
       (mode != 0 && mode != 1) || gate.format != kQ4_0 || up.format != kQ4_0) {
     return hipErrorInvalidValue;
+  }
+  // K = 1,152: two groups every lane, 7 neurons a 4-wave workgroup.
+  if (gate.cols == pair::kCols) {
+    return mode == 0 ? launch_gated_pair<0, 4>(s, step, gate, up, in, act, edits, layer)
+                     : launch_gated_pair<1, 4>(s, step, gate, up, in, act, edits, layer);
   }
   const int items = max_items(gate.cols, 2);
   if (items <= 3) {

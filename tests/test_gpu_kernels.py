@@ -87,6 +87,50 @@ def test_gemv_decode_bit_exact(device, rows, cols):
     assert_same_bits(dy.numpy(), orc.gemv(w, rows, cols, x), f"gemv {rows}x{cols}")
 
 
+def _every_scale_blocks(rng, rows, cols):
+    """rows x cols Q4_0 blocks whose scales run through every finite f16
+    (subnormals, zeros and negatives included; repeated to fill), codes
+    uniform."""
+    finite = np.concatenate([np.arange(0x0000, 0x7C00), np.arange(0x8000, 0xFC00)]).astype(np.uint16)
+    n = rows * cols // 32
+    out = np.empty((n, 18), dtype=np.uint8)
+    out[:, 0:2] = np.resize(finite, n).view(np.uint8).reshape(n, 2)
+    out[:, 2:] = rng.integers(0, 256, size=(n, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+# The decode forms of the weight (low nibble 1024 + q with d, high nibble
+# 1024 + 16 q with d / 16) against the oracle's (q - 8) d, over every finite
+# scale: the two-groups-a-lane layout (7 and 14 rows a workgroup) and the
+# lane-a-range layout.
+@pytest.mark.parametrize("rows,cols", [(1764, 1152), (4200, 1152), (1984, 1024)])
+def test_gemv_decode_every_scale_bit_exact(device, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    w = _every_scale_blocks(rng, rows, cols)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    codes, scales = _q4_dev(device, w)
+    dx = device.array(x)
+    dy = device.empty((rows,), np.float32)
+    fz._lib.check(fz.load().frz_op_gemv(device.handle, codes.ptr, scales.ptr, rows, cols,
+                                        dx.ptr, cols, dy.ptr, rows, 1, 0))
+    assert_same_bits(dy.numpy(), orc.gemv(w, rows, cols, x), f"gemv {rows}x{cols}")
+
+
+def test_gated_every_scale_bit_exact(device):
+    rng = np.random.default_rng(77)
+    rows, cols = 1764, 1152
+    g = _every_scale_blocks(rng, rows, cols)
+    u = np.roll(_every_scale_blocks(rng, rows, cols).reshape(-1, 18), 1000, axis=0).reshape(-1)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    gc, gs = _q4_dev(device, g)
+    uc, us = _q4_dev(device, u)
+    dx = device.array(x)
+    da = device.empty((1, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gated(device.handle, gc.ptr, gs.ptr, uc.ptr, us.ptr, rows,
+                                         cols, dx.ptr, da.ptr, 1, 0, None, 0))
+    assert_same_bits(da.numpy()[0], orc.gated(g, u, rows, cols, x), "gated")
+
+
 @pytest.mark.parametrize("rows,cols,tokens", [(1536, 1152, 5), (1152, 6912, 37),
                                                (1152, 1024, 64), (200, 96, 3)])
 def test_gemv_tiled_is_decode_bits(device, rows, cols, tokens):
