@@ -467,7 +467,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": committed_traffic(),
-                     "kernel": "Q4_0 decode GEMV 6912x1152 (gemv_decode<1>)",
+                     "kernel": "Q4_0 decode GEMV 6912x1152 (gemv_pair_kernel<0, 4>: 18 lanes a row, 14 rows a workgroup)",
                      "us_per_launch": us, "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,
         "parity": parity,

@@ -726,6 +726,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_write_kernel(const DevStep* _
       for (int it = 0; it < MAXI; ++it) {
         if (plan.xoff[it] >= 0) acc = chain_group(acc, buf[0].codes[it], buf[0].scale[it], xv[it]);
       }
+    } else if constexpr (F == kQ4_0) {
+      // Longer chains (K = 6,912: 6 or 7 groups) run about one wave a SIMD,
+      // which cannot hide LDS latency: the next group's input is read into
+      // the other register buffer while this group's chain runs.
+      float4 xa[8], xb[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xa[q] = ld4(xs + max(plan.xoff[0], 0) + 4 * q);
+#pragma unroll
+      for (int it = 0; it < MAXI; ++it) {
+        float4 (&cur)[8] = (it & 1) ? xb : xa;
+        float4 (&nxt)[8] = (it & 1) ? xa : xb;
+        if (it + 1 < MAXI) {
+          const int xo = max(plan.xoff[it + 1 < MAXI ? it + 1 : it], 0);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) nxt[q] = ld4(xs + xo + 4 * q);
+        }
+        if (plan.xoff[it] >= 0) acc = chain_group(acc, buf[0].codes[it], buf[0].scale[it], cur);
+      }
     } else {
 #pragma unroll
       for (int it = 0; it < MAXI; ++it) {
@@ -1023,7 +1041,9 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
   if (items1 <= 1) return launch_write<1, 1, MODE, 1, 2, F>(s, step, w, in, y);
   if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2, F>(s, step, w, in, y);
   if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2, F>(s, step, w, in, y);
-  if (items1 <= 8) return launch_write<1, 8, MODE, 1, 2, F>(s, step, w, in, y);
+  // Up to 8 items (K to 8,192): four waves, so half as many workgroups stage
+  // the long input row.
+  if (items1 <= 8) return launch_write<1, 8, MODE, 1, 4, F>(s, step, w, in, y);
   return hipErrorInvalidValue;
 }
 
