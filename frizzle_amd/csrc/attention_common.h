@@ -38,9 +38,9 @@ struct ChunkShared {
   alignas(16) uint16_t v[kChunkKeys * D];  // value rows as stored
   alignas(16) uint16_t knew[D];        // the step's own key row, when the chunk holds it
   alignas(16) float e[kChunkKeys];     // weights
-  float tile_top[kTiles];
-  int tile_seen[kTiles];
-  float tile_a[kTiles];
+  alignas(16) float tile_top[kTiles];
+  alignas(16) int tile_seen[kTiles];
+  alignas(16) float tile_a[kTiles];
 };
 
 __device__ __forceinline__ float h2f(uint32_t h) {
@@ -127,6 +127,22 @@ __device__ __forceinline__ void value_store(ChunkShared& S, const uint4 (&v)[kVa
   }
 }
 
+// Lane (l + N) mod 16 of the calling lane l's 16-lane row (DPP row_ror).
+template <int N>
+__device__ __forceinline__ int row_rotate_int(int x) {
+  return __builtin_amdgcn_mov_dpp(x, 0x120 + N, 0xF, 0xF, false);
+}
+template <int N>
+__device__ __forceinline__ float row_rotate(float x) {
+  return __builtin_bit_cast(float, row_rotate_int<N>(__builtin_bit_cast(int, x)));
+}
+
+// Lane l ^ 16 of the calling lane l's 32-lane group (ds_swizzle bit mode:
+// and-mask 31, or-mask 0, xor-mask 16).
+__device__ __forceinline__ int other_row(int x) {
+  return __builtin_amdgcn_ds_swizzle(x, (16 << 10) | 31);
+}
+
 // Lane UU of the calling lane's quad.
 template <int UU>
 __device__ __forceinline__ float quad_lane(float x) {
@@ -144,6 +160,7 @@ __device__ __forceinline__ float add_quad_dots(float s, const float (&d)[2 * kKe
 // head, from its staged query and values in S and each lane's key part in
 // k (rows past k_end zeros). Every thread of the workgroup calls it. With
 // `scores`, each live key j's score is also written at scores[j - earliest].
+template <bool kQueryFirst = false>
 __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKeyLoads], int p,
                                             int window, const ChunkRange& r,
                                             float* __restrict__ partial,
@@ -155,6 +172,19 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   // Dimension t of every staged value row, read now so the reads complete
   // under the scores and the softmax and the output chain finds them in
   // registers (rows past the chunk's tiles read as staged; their weight is 0).
+  // With kQueryFirst (a latency-bound launch of few workgroups) the 64 query
+  // values the lane's dots take are read before them: LDS reads complete in
+  // order, so the dots then do not wait for the 64 value reads. It costs 16
+  // registers, which a launch of many workgroups pays in occupancy.
+  float4 qv[2 * kKeyLoads];
+  if constexpr (kQueryFirst) {
+#pragma unroll
+    for (int m = 0; m < kKeyLoads; ++m) {
+      qv[2 * m] = ld4f(S.q + 64 * u + 8 * m);
+      qv[2 * m + 1] = ld4f(S.q + 64 * u + 8 * m + 4);
+    }
+    __asm__ volatile("" ::: "memory");
+  }
   uint16_t vt[kChunkKeys];
 #pragma unroll
   for (int key = 0; key < kChunkKeys; ++key) vt[key] = S.v[key * D + t];
@@ -162,7 +192,8 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   float d[2 * kKeyLoads];
 #pragma unroll
   for (int m = 0; m < kKeyLoads; ++m) {
-    const float4 qa = ld4f(S.q + 64 * u + 8 * m), qb = ld4f(S.q + 64 * u + 8 * m + 4);
+    const float4 qa = kQueryFirst ? qv[2 * m] : ld4f(S.q + 64 * u + 8 * m);
+    const float4 qb = kQueryFirst ? qv[2 * m + 1] : ld4f(S.q + 64 * u + 8 * m + 4);
     const uint4 w = k[m];
     d[2 * m] = dot4(qa.x, qa.y, qa.z, qa.w, h2f(w.x & 0xFFFFu), h2f(w.x >> 16),
                     h2f(w.y & 0xFFFFu), h2f(w.y >> 16));
@@ -175,28 +206,40 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   s = add_quad_dots<2>(s, d);
   s = add_quad_dots<3>(s, d);
   if (scores && live && u == 0) scores[j - earliest] = s;
-  // A tile is 8 keys, 32 lanes.
+  // A tile is 8 keys, 32 lanes: two DPP rows of 4 keys. Its maximum and
+  // whether any key is live, in every lane: within a row by rotations, then
+  // across the two rows by a swizzle (xor 16); a max is order-free.
   float top = live ? s : -__builtin_inff();
   int seen = live ? 1 : 0;
-#pragma unroll
-  for (int off = kKeyLanes; off < kKeyLanes * kTileKeys; off <<= 1) {
-    top = __builtin_fmaxf(top, __shfl_xor(top, off, 64));
-    seen |= __shfl_xor(seen, off, 64);
-  }
+  top = __builtin_fmaxf(top, row_rotate<4>(top));
+  seen |= row_rotate_int<4>(seen);
+  top = __builtin_fmaxf(top, row_rotate<8>(top));
+  seen |= row_rotate_int<8>(seen);
+  top = __builtin_fmaxf(top, __builtin_bit_cast(float, other_row(__builtin_bit_cast(int, top))));
+  seen |= other_row(seen);
   if ((t & 31) == 0) {
     S.tile_top[jj >> 3] = top;
     S.tile_seen[jj >> 3] = seen;
   }
   __syncthreads();
   // Each tile's running maximum and rescale factor, and each weight
-  // (attention.wgsl:304-340).
+  // (attention.wgsl:304-340), from all tiles' maxima read at once.
+  float tops[kTiles];
+  int seens[kTiles];
+#pragma unroll
+  for (int q4 = 0; q4 < kTiles / 4; ++q4) {
+    const float4 tv = ld4f(S.tile_top + 4 * q4);
+    const int4 sv = *reinterpret_cast<const int4*>(S.tile_seen + 4 * q4);
+    tops[4 * q4] = tv.x; tops[4 * q4 + 1] = tv.y; tops[4 * q4 + 2] = tv.z; tops[4 * q4 + 3] = tv.w;
+    seens[4 * q4] = sv.x; seens[4 * q4 + 1] = sv.y; seens[4 * q4 + 2] = sv.z; seens[4 * q4 + 3] = sv.w;
+  }
   const int tile = jj >> 3;
   bool chunk_live = false;
   float cm = 0.0f, my_old = 0.0f, my_top = 0.0f;
 #pragma unroll
   for (int tt = 0; tt < kTiles; ++tt) {
-    if (tt < r.n_tiles && S.tile_seen[tt]) {
-      const float top_tile = S.tile_top[tt];
+    if (tt < r.n_tiles && seens[tt]) {
+      const float top_tile = tops[tt];
       const float old = chunk_live ? cm : top_tile;
       chunk_live = true;
       const float next = __builtin_fmaxf(old, top_tile);
@@ -211,8 +254,7 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
   // first key: the two exponentials run side by side.
   if (u == 0) S.e[jj] = live ? exp2f_fixed(s - my_top) : 0.0f;
   if (u == 1 && (jj & 7) == 0 && tile < r.n_tiles) {
-    S.tile_a[tile] =
-        (S.tile_seen[tile] != 0 && my_old != my_top) ? exp2f_fixed(my_old - my_top) : 1.0f;
+    S.tile_a[tile] = (seens[tile] != 0 && my_old != my_top) ? exp2f_fixed(my_old - my_top) : 1.0f;
   }
   __syncthreads();
   // Each tile's weights summed in order, then l = l a + sum over the seen
@@ -223,14 +265,21 @@ __device__ __forceinline__ void chunk_state(ChunkShared& S, const uint4 (&k)[kKe
 #pragma unroll
       for (int b = 0; b < kTileKeys; ++b) sum += S.e[t * kTileKeys + b];
     }
-    float sums[kTiles];
+    float sums[kTiles], as[kTiles];
 #pragma unroll
-    for (int tt = 0; tt < kTiles; ++tt) sums[tt] = __shfl(sum, tt, 64);
+    for (int tt = 0; tt < kTiles; ++tt) {
+      sums[tt] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), tt));
+    }
+#pragma unroll
+    for (int q4 = 0; q4 < kTiles / 4; ++q4) {
+      const float4 av = ld4f(S.tile_a + 4 * q4);
+      as[4 * q4] = av.x; as[4 * q4 + 1] = av.y; as[4 * q4 + 2] = av.z; as[4 * q4 + 3] = av.w;
+    }
     if (t == 0) {
       float cl = 0.0f;
 #pragma unroll
       for (int tt = 0; tt < kTiles; ++tt) {
-        if (tt < r.n_tiles && S.tile_seen[tt]) cl = cl * S.tile_a[tt] + sums[tt];
+        if (tt < r.n_tiles && seens[tt]) cl = cl * as[tt] + sums[tt];
       }
       *reinterpret_cast<float4*>(stats) = make_float4(cm, cl, chunk_live ? 1.0f : 0.0f, 0.0f);
     }

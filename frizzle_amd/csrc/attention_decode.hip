@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
     for (int m = 0; m < kKeyLoads; ++m) kr[m] = src[m];
   }
   const size_t slot = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
-  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
+  chunk_state<true>(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4);
 }
 
 }  // namespace

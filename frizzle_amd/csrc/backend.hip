@@ -42,7 +42,7 @@ __global__ void numerics_kernel(int which, const float* in, float* out, int n) {
     case 3: r = inverse_sqrt(x); break;
     case 4: r = gelu_tanh(x); break;
     case 5: r = exp_nonpositive(x); break;
-    case 6: r = bits_to_float((uint32_t)f16_pack(x)); break;
+    case 6: r = bits_to_float((uint32_t)f16_pack_device(x)); break;
     case 7: r = __builtin_sqrtf(x); break;
     case 8: r = in[2 * (i / 2)] / in[2 * (i / 2) + 1]; break;
     default: break;

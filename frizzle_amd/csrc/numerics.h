@@ -148,6 +148,15 @@ FRZ_HD uint16_t f16_pack(float x) {
   return (uint16_t)(sign | h);
 }
 
+// f16_pack on the device: the same saturation, then the hardware's f32 to
+// f16 conversion, which rounds to nearest even and keeps f16 subnormals (the
+// kernels run with f16 denormals on); a NaN packs as 0x7E00.
+__device__ __forceinline__ uint16_t f16_pack_device(float x) {
+  if (x != x) return 0x7E00;
+  x = __builtin_fminf(__builtin_fmaxf(x, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
 // F16 to f32, exact, subnormals kept.
 FRZ_HD float f16_unpack(uint32_t h) {
   const uint32_t sign = (h & 0x8000u) << 16;

@@ -67,10 +67,10 @@ __device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum
 
 __device__ __forceinline__ ushort4 pack4_f16(float4 v) {
   ushort4 o;
-  o.x = f16_pack(v.x);
-  o.y = f16_pack(v.y);
-  o.z = f16_pack(v.z);
-  o.w = f16_pack(v.w);
+  o.x = f16_pack_device(v.x);
+  o.y = f16_pack_device(v.y);
+  o.z = f16_pack_device(v.z);
+  o.w = f16_pack_device(v.w);
   return o;
 }
 
