@@ -41,13 +41,49 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
 
 // ---- fold ------------------------------------------------------------------
 // A workgroup folds one row's chunks for 64 dimensions of one head. The
-// chunk states are staged into LDS; each chunk's factors (a, b) follow from
-// the running maximum and liveness before it, found by a prefix scan (a
-// running maximum is a max while no chunk maximum is NaN; with one, lane 0
-// replays the recursion itself); then each dimension's chain
-// o = o a + po b, and l's, run in chunk order.
+// chunk states are staged into LDS; the running maximum and liveness before
+// each chunk come from a wave-wide prefix scan (a maximum and an or, exact
+// in any order while no chunk maximum is NaN; with one, lane 0 replays the
+// recursion itself); each chunk's factors (a, b) follow in parallel; then
+// each dimension's chain o = o a + po b, and l's, run in chunk order. The
+// chains read a chunk's (a, b, l term, liveness) as one record, 8 chunks at
+// a time; the chunk count is padded to 8 with records (1, 0, 0, 0) and zero
+// outputs, which leave o, l and liveness as they are (o and l are never -0,
+// so adding 0 * 0 changes no bits).
 constexpr int kFoldDims = 64;
-constexpr int kFoldBatch = 8;  // staging loads a thread keeps in flight
+constexpr int kFoldBatch = 8;  // staging loads a thread keeps in flight; chunks a chain step reads
+
+__host__ __device__ constexpr int fold_padded(int chunks) {
+  return (chunks + kFoldBatch - 1) / kFoldBatch * kFoldBatch;
+}
+
+// Inclusive prefix maximum and or over the wave's 64 lanes: shifts within
+// each 16-lane row, then row 0's and 2's last lanes into the next row, then
+// lane 31 into rows 2 and 3 (DPP row_shr, row_bcast:15, row_bcast:31).
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_or_old(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ float wave_prefix_max(float v) {
+  const int ninf = __builtin_bit_cast(int, -__builtin_inff());
+  auto step = [&](int got) { v = __builtin_fmaxf(v, __builtin_bit_cast(float, got)); };
+  step(dpp_or_old<0x111>(ninf, __builtin_bit_cast(int, v)));
+  step(dpp_or_old<0x112>(ninf, __builtin_bit_cast(int, v)));
+  step(dpp_or_old<0x114>(ninf, __builtin_bit_cast(int, v)));
+  step(dpp_or_old<0x118>(ninf, __builtin_bit_cast(int, v)));
+  step(dpp_or_old<0x142, 0xA>(ninf, __builtin_bit_cast(int, v)));
+  step(dpp_or_old<0x143, 0xC>(ninf, __builtin_bit_cast(int, v)));
+  return v;
+}
+__device__ __forceinline__ int wave_prefix_or(int v) {
+  v |= dpp_or_old<0x111>(0, v);
+  v |= dpp_or_old<0x112>(0, v);
+  v |= dpp_or_old<0x114>(0, v);
+  v |= dpp_or_old<0x118>(0, v);
+  v |= dpp_or_old<0x142, 0xA>(0, v);
+  v |= dpp_or_old<0x143, 0xC>(0, v);
+  return v;
+}
 
 __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep* __restrict__ step,
                                                                   FoldArgs f) {
@@ -56,17 +92,21 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   if (row >= (int)step->tokens) return;
   const int p = (int)step->position + (step->variants ? 0 : row);
   const int count = chunk_range(p, f.window, 0).count;
+  const int padded = fold_padded(count);
+  const int cap = fold_padded(f.max_chunks);
   const int h = blockIdx.x / (D / kFoldDims), dim0 = (blockIdx.x % (D / kFoldDims)) * kFoldDims;
   const int t = threadIdx.x;
-  float* po = fold_smem;                                      // [count][64]
-  float4* st = reinterpret_cast<float4*>(po + f.max_chunks * kFoldDims);  // [count]
-  float* fa = reinterpret_cast<float*>(st + f.max_chunks);    // [count]
-  float* fb = fa + f.max_chunks;
-  float* mb = fb + f.max_chunks;                              // m before chunk c
-  int* lb = reinterpret_cast<int*>(mb + f.max_chunks);        // live before chunk c
+  float* po = fold_smem;                                       // [cap][64]
+  float4* st = reinterpret_cast<float4*>(po + cap * kFoldDims);  // [cap] (m, l, live, 0)
+  float4* rec = st + cap;                                      // [cap] (a, b, l, live)
+  float* mb = reinterpret_cast<float*>(rec + cap);             // m before chunk c
+  int* lb = reinterpret_cast<int*>(mb + cap);                  // live before chunk c
   const float* part = f.partials + (size_t)row * f.max_chunks * QH * D;
   const float* stats = f.stats + (size_t)row * f.max_chunks * QH * 4;
-  // Stage: uint4 i of the head's block is chunk i / 16, dims 4 (i % 16).
+  // Stage: the chunk states (one a thread: count <= 224), then uint4 i of the
+  // head's block, chunk i / 16, dims 4 (i % 16); the padding's outputs zero.
+  float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t < count) sv = ld4f(stats + ((size_t)t * QH + h) * 4);
   const int vec4s = count * (kFoldDims / 4);
   for (int base = 0; base < vec4s; base += kFoldBatch * kThreads) {
     float4 v[kFoldBatch];
@@ -81,7 +121,9 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
       if (i < vec4s) reinterpret_cast<float4*>(po)[i] = v[n];
     }
   }
-  for (int c = t; c < count; c += kThreads) st[c] = ld4f(stats + ((size_t)c * QH + h) * 4);
+  for (int i = vec4s + t; i < padded * (kFoldDims / 4); i += kThreads)
+    reinterpret_cast<float4*>(po)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (t < count) st[t] = sv;
   __syncthreads();
   if (t < 64) {
     bool carry_live = false, nan = false;
@@ -91,29 +133,18 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
       const float4 s4 = c < count ? st[c] : make_float4(0.f, 0.f, 0.f, 0.f);
       const bool cl = c < count && s4.z != 0.0f;
       nan = nan || (cl && s4.x != s4.x);
-      float v = cl ? s4.x : -__builtin_inff();
-      int lv = cl ? 1 : 0;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float ov = __shfl_up(v, off, 64);
-        const int ol = __shfl_up(lv, off, 64);
-        if (t >= off) {
-          v = __builtin_fmaxf(v, ov);
-          lv |= ol;
-        }
-      }
-      float ev = __shfl_up(v, 1, 64);
-      int el = __shfl_up(lv, 1, 64);
-      if (t == 0) {
-        ev = -__builtin_inff();
-        el = 0;
-      }
+      const float v = wave_prefix_max(cl ? s4.x : -__builtin_inff());
+      const int lv = wave_prefix_or(cl ? 1 : 0);
+      // Exclusive: lane c - 1's (lane 0: nothing before).
+      const float ev = __builtin_bit_cast(
+          float, dpp_or_old<0x138>(__builtin_bit_cast(int, -__builtin_inff()), __builtin_bit_cast(int, v)));
+      const int el = dpp_or_old<0x138>(0, lv);
       if (c < count) {
         lb[c] = carry_live || el;
         mb[c] = carry_live ? (el ? __builtin_fmaxf(carry_m, ev) : carry_m) : ev;
       }
-      const float last_v = __shfl(v, 63, 64);
-      const int last_l = __shfl(lv, 63, 64);
+      const float last_v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+      const int last_l = __builtin_amdgcn_readlane(lv, 63);
       carry_m = carry_live ? (last_l ? __builtin_fmaxf(carry_m, last_v) : carry_m) : last_v;
       carry_live = carry_live || last_l;
     }
@@ -130,20 +161,33 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
     }
   }
   __syncthreads();
-  for (int c = t; c < count; c += kThreads) {
-    const Fold g = fold_factors(lb[c] != 0, mb[c], st[c].z != 0.0f, st[c].x);
-    fa[c] = g.a;
-    fb[c] = g.b;
+  for (int c = t; c < padded; c += kThreads) {
+    if (c < count) {
+      const float4 s4 = st[c];
+      const Fold g = fold_factors(lb[c] != 0, mb[c], s4.z != 0.0f, s4.x);
+      rec[c] = make_float4(g.a, g.b, s4.y, s4.z);
+    } else {
+      rec[c] = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+    }
   }
   __syncthreads();
   if (t < kFoldDims) {
     bool live = false;
     float l = 0.0f, o = 0.0f;
-    for (int c = 0; c < count; ++c) {
-      const float a = fa[c], b = fb[c];
-      l = l * a + st[c].y * b;
-      o = o * a + po[c * kFoldDims + t] * b;
-      live = live || st[c].z != 0.0f;
+    for (int base = 0; base < padded; base += kFoldBatch) {
+      float4 r[kFoldBatch];
+      float v[kFoldBatch];
+#pragma unroll
+      for (int k = 0; k < kFoldBatch; ++k) {
+        r[k] = rec[base + k];
+        v[k] = po[(base + k) * kFoldDims + t];
+      }
+#pragma unroll
+      for (int k = 0; k < kFoldBatch; ++k) {
+        l = l * r[k].x + r[k].z * r[k].y;
+        o = o * r[k].x + v[k] * r[k].y;
+        live = live || r[k].w != 0.0f;
+      }
     }
     f.out[(size_t)row * QH * D + h * D + dim0 + t] = live ? o / l : 0.0f;
     // The last row's (m, l), for the capture store: m as the last chunk's
@@ -161,7 +205,8 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
 
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens) {
-  const size_t lds = (size_t)f.max_chunks * (kFoldDims * 4 + 16 + 4 * 4);
+  // po, st, rec, mb, lb for the chunk count padded to a batch.
+  const size_t lds = (size_t)fold_padded(f.max_chunks) * (kFoldDims * 4 + 16 + 16 + 4 + 4);
   if (f.max_chunks <= 0 || f.max_chunks > kMaxFoldChunks) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_fold_kernel, dim3(QH * (D / kFoldDims), max_tokens), dim3(kThreads),
                      lds, s, step, f);
