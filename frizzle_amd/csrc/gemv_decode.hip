@@ -323,8 +323,14 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
   uint32_t token = 0;
   if (MODE == 2) token = step->fed ? in.sampled[0] : step->ids[0];
   const int groups = width >> 5;
+  // A slot past the row for the wave's first lane is past it for the whole
+  // wave and is not loaded (the branch is uniform over the wave; at K =
+  // 1,152 it halves a workgroup's prologue loads). The loads skipped come
+  // after the ones kept and before the weights', so no wait counts them.
+  const int wave_first = (int)threadIdx.x & ~63;
 #pragma unroll
   for (int s = 0; s < Prologue<T, X4>::S; ++s) {
+    if (norm_vec4<T>(s >> 1, s & 1) - ((int)threadIdx.x - wave_first) >= vec4s) continue;
     const int q = min(norm_vec4<T>(s >> 1, s & 1), vec4s - 1);
     if (MODE == 1) {
       P.v[s] = ld4(in.hidden + 4 * q);
