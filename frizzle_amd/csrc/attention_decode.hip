@@ -44,10 +44,20 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(
   if (t < D / 2) rope_angle(turn, (uint32_t)p, &sines[t], &cosines[t]);
   if (!active) va = vb = make_float4(0.f, 0.f, 0.f, 0.f);
   // The head's sum of squares: the halving tree over its 32 lanes.
+  // Each 32-lane group's lane 0 ends with the total (level 16 by a swizzle
+  // within the group, lane l ^ 16; levels 8 to 1 within a row by DPP), which
+  // goes to the group's lanes.
   float sum = rope_lane_squares(va, vb);
-#pragma unroll
-  for (int stride = 16; stride > 0; stride >>= 1) sum = sum + __shfl_down(sum, stride, 32);
-  sum = __shfl(sum, 0, 32);
+  sum = sum + __builtin_bit_cast(float, other_row(__builtin_bit_cast(int, sum)));
+  sum = sum + row_shl<8>(sum);
+  sum = sum + row_shl<4>(sum);
+  sum = sum + row_shl<2>(sum);
+  sum = sum + row_shl<1>(sum);
+  {
+    const int b = __builtin_bit_cast(int, sum);
+    const int lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
+    sum = __builtin_bit_cast(float, (t & 32) ? hi : lo);
+  }
   __syncthreads();
   if (active) {
     if (role <= 1) {

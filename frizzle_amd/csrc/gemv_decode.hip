@@ -231,12 +231,6 @@ __device__ __forceinline__ bool norm_thread() {
 // remaining levels itself from LDS (levels 128 and 64 in registers, the last
 // six across the wave), so every thread gets the total with no second
 // barrier. `red` is 256 floats the call owns: a second tree uses another.
-// Lane l + N of the lane's 16-lane row (DPP row shift; out of the row: 0).
-template <int N>
-__device__ __forceinline__ float row_shl(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x100 + N, 0xF, 0xF, true));
-}
 
 // The halving tree's last six levels over a wave's 64 sums: lane l adds
 // lane l + stride for strides 32 .. 1; lane 0's total, broadcast.
@@ -924,7 +918,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   wave_sync();
   // Lane 0 totals the gate row while lane 1 totals the up row.
   const float total = r < 2 ? row_total(parts + (2 * local + r) * kPartStride) : 0.0f;
-  const float u = __shfl_down(total, 1, 64);
+  const float u = row_shl<1>(total);  // lane t + 1: even t stays in its row
   if (r == 0 && n < gate.rows) {
     float v = gelu_tanh(total) * u;
     if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)n, step->position, v);
@@ -980,7 +974,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
   if (t < 64) {
     // Thread 2k totals neuron k's gate row, thread 2k + 1 its up row.
     const float total = t < 2 * kNeurons ? pair::row_total(sums, t) : 0.0f;
-    const float u = __shfl_down(total, 1, 64);
+    const float u = row_shl<1>(total);  // lane t + 1: even t stays in its row
     const int nn = blockIdx.x * kNeurons + (t >> 1);
     if ((t & 1) == 0 && t < 2 * kNeurons && nn < gate.rows) {
       float v = gelu_tanh(total) * u;

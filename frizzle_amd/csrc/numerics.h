@@ -157,6 +157,14 @@ __device__ __forceinline__ uint16_t f16_pack_device(float x) {
   return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// Lane l + N of the calling lane l's 16-lane row, as a VALU operation (DPP
+// row_shl; lanes past the row get 0).
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x100 + N, 0xF, 0xF, true));
+}
+
 // F16 to f32, exact, subnormals kept.
 FRZ_HD float f16_unpack(uint32_t h) {
   const uint32_t sign = (h & 0x8000u) << 16;
