@@ -365,12 +365,18 @@ __device__ __forceinline__ void fold_prologue(float* xs, float* red, const Prolo
   __syncthreads();
   if (t < count * QH) {
     const int c = t / QH, h = t % QH;
+    // The head's states read at once, then the replay in registers.
+    float4 sv[kFoldPrologueChunks];
+#pragma unroll
+    for (int b = 0; b < kFoldPrologueChunks; ++b) sv[b] = st[min(b, count - 1) * QH + h];
     bool live = false;
     float m = 0.0f;
-    for (int b = 0; b < c; ++b) {
-      const float4 s = st[b * QH + h];
-      m = attn::fold_factors(live, m, s.z != 0.0f, s.x).m;
-      live = live || s.z != 0.0f;
+#pragma unroll
+    for (int b = 0; b < kFoldPrologueChunks; ++b) {
+      if (b < c) {
+        m = attn::fold_factors(live, m, sv[b].z != 0.0f, sv[b].x).m;
+        live = live || sv[b].z != 0.0f;
+      }
     }
     const attn::Fold f = attn::fold_factors(live, m, P.st.z != 0.0f, P.st.x);
     fa[t] = f.a;
