@@ -195,30 +195,32 @@ __device__ void draw_one(const DevStep* step, const uint32_t* cand, uint32_t* __
     k1 += 0xBB67AE85u;
   }
   const float u = (float)(c0 >> 9) * (1.0f / 8388608.0f) + (1.0f / 16777216.0f);
-  if (use_top_p) {
-    float sum = 0.0f;
-    for (uint32_t i = 0; i < k; ++i) sum = sum + weight[i];
-    if (!failed) {
-      for (uint32_t i = 0; i < k; ++i) weight[i] = weight[i] / sum;
-    }
-  }
-  uint32_t kept = k;
-  float cumulative = 0.0f, tempered_sum = 0.0f;
-  for (uint32_t i = 0; i < k; ++i) {
-    tempered_sum = tempered_sum + tempered[i];
-    running[i] = tempered_sum;
-    if (use_top_p) {
-      cumulative = cumulative + weight[i];
-      if (cumulative >= step->top_p) {
-        kept = i + 1;
-        break;
-      }
-    }
-  }
-  uint32_t survivors = 1;
-  while (survivors < kept && above[survivors] == 1u) ++survivors;
+  // The top-p cut, the min-p survivors and the running tempered sums decide
+  // only a tempered draw; greedy (temperature 0) takes candidate 0.
   uint32_t chosen = 0;
   if (temperature > 0.0f) {
+    if (use_top_p) {
+      float sum = 0.0f;
+      for (uint32_t i = 0; i < k; ++i) sum = sum + weight[i];
+      if (!failed) {
+        for (uint32_t i = 0; i < k; ++i) weight[i] = weight[i] / sum;
+      }
+    }
+    uint32_t kept = k;
+    float cumulative = 0.0f, tempered_sum = 0.0f;
+    for (uint32_t i = 0; i < k; ++i) {
+      tempered_sum = tempered_sum + tempered[i];
+      running[i] = tempered_sum;
+      if (use_top_p) {
+        cumulative = cumulative + weight[i];
+        if (cumulative >= step->top_p) {
+          kept = i + 1;
+          break;
+        }
+      }
+    }
+    uint32_t survivors = 1;
+    while (survivors < kept && above[survivors] == 1u) ++survivors;
     const float goal = u * running[survivors - 1];
     chosen = survivors - 1;
     for (uint32_t i = 0; i < survivors; ++i) {
