@@ -293,8 +293,14 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
                                               const DevStep* __restrict__ step, int width) {
   const int vec4s = width >> 2;
   if (MODE == 0) {
+    // A slot past the row for the wave's first lane is past it for the whole
+    // wave and is not loaded (the branch is uniform over the wave).
+    const int wave_first = (int)threadIdx.x & ~63;
 #pragma unroll
-    for (int j = 0; j < X4; ++j) P.plain[j] = ld4(in.x + 4 * min((int)threadIdx.x + j * T, vec4s - 1));
+    for (int j = 0; j < X4; ++j) {
+      if (wave_first + j * T >= vec4s) continue;
+      P.plain[j] = ld4(in.x + 4 * min((int)threadIdx.x + j * T, vec4s - 1));
+    }
     return;
   }
   if (MODE == 3) {
