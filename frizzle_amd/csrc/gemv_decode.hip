@@ -304,14 +304,18 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
     return;
   }
   if (MODE == 3) {
+    // Chunks past the window's count, and chunk states past the (chunk,
+    // head) pairs for a whole wave, are not loaded (the count is the same
+    // for every thread; the second test is uniform over the wave).
     const int count = window_chunks(step, in.window);
-    P.st = ld4(in.stats + 4 * min((int)threadIdx.x, count * attn::QH - 1));
+    if (((int)threadIdx.x & ~63) < count * attn::QH)
+      P.st = ld4(in.stats + 4 * min((int)threadIdx.x, count * attn::QH - 1));
 #pragma unroll
     for (int c = 0; c < kFoldPrologueChunks; ++c) {
-      const int cc = min(c, count - 1);
+      if (c >= count) continue;
 #pragma unroll
       for (int j = 0; j < Shape<T>::kFoldVec4s; ++j) {
-        P.po[c][j] = ld4(in.partials + cc * kFoldWidth + 4 * ((int)threadIdx.x + j * T));
+        P.po[c][j] = ld4(in.partials + c * kFoldWidth + 4 * ((int)threadIdx.x + j * T));
       }
     }
     return;
