@@ -16,8 +16,9 @@
 //   one row a half-wave, lane r range r: the total is a DPP chain across
 //     the half-wave, with no LDS (the write products, K other than 1,152);
 //   K = 1,152 (`pair`): 18 lanes a row, each exactly two groups, so no lane
-//     idles through a second group; sums meet in LDS;
-//   two rows a half-wave (the 262,144-row head) and the gated product: lane
+//     idles through a second group; sums meet in LDS. Many rows (the
+//     262,144-row head) take 8 tiles a workgroup (`gemv_pair_tiles_kernel`);
+//   two rows a half-wave (the Q8_0 head, other K of the gated product): lane
 //     r takes range (r + j) mod 32 of row j, which spreads each row's longer
 //     ranges over different lanes; sums meet in LDS.
 // A lane's plan (which groups, where each range sum goes) is fixed for the
@@ -897,6 +898,65 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_pair_kernel(const DevStep* __
     y[blockIdx.x * kRows + t] = pair::row_total(sums, t);
 }
 
+// The pair layout over many rows: a workgroup takes TPW tiles of kRows rows,
+// blockIdx.x + k gridDim.x (clamped to the last tile, which a workgroup past
+// the end recomputes with the same bits). The lane's two groups are the same
+// in every tile, so their input goes into registers once; the next tile's
+// weights load under this tile's chains; the range sums alternate between
+// two LDS areas, so one barrier a tile orders writers and readers.
+template <int MODE, int WAVES, int TPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_pair_tiles_kernel(
+    const DevStep* __restrict__ step, QMatrix w, GemvInput in, float* __restrict__ y) {
+  extern __shared__ __align__(16) float smem[];
+  constexpr int T = 64 * WAVES;
+  constexpr int kRows = pair::rows<T>();
+  constexpr int X4 = plain_vec4s<1, 2, T>();
+  float* sums = smem;  // [2][kRows][pair::kStride]
+  float* red = sums + 2 * kRows * pair::kStride;
+  float* xs = red + kRedFloats;
+  const int t = threadIdx.x;
+  const int local = t / pair::kLanes, p = t - local * pair::kLanes;
+  const int tiles = (w.rows + kRows - 1) / kRows;
+  auto tile_of = [&](int k) { return min((int)blockIdx.x + k * (int)gridDim.x, tiles - 1); };
+  const pair::Plan P = pair::plan(p);
+  Prologue<T, X4> pro;
+  prologue_load<MODE, T, X4>(pro, in, step, w.cols);
+  uint4 c[2][2];
+  uint16_t d[2][2];
+  auto load_tile = [&](int k, int b) {
+    const int row = tile_of(k) * kRows + local;
+    const int base = local < kRows && row < w.rows ? row * pair::kGroups : 0;
+    c[b][0] = reinterpret_cast<const uint4*>(w.codes)[base + P.g0];
+    d[b][0] = w.scales[base + P.g0];
+    c[b][1] = reinterpret_cast<const uint4*>(w.codes)[base + P.g1];
+    d[b][1] = w.scales[base + P.g1];
+  };
+  load_tile(0, 0);
+  prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
+  __syncthreads();
+  float4 x0[8], x1[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    x0[q] = ld4(xs + P.g0 * kXStride + 4 * q);
+    x1[q] = ld4(xs + P.g1 * kXStride + 4 * q);
+  }
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    if (k + 1 < TPW) load_tile(k + 1, (k + 1) & 1);
+    const float s0 = chain_group(0.0f, c[k & 1][0], d[k & 1][0], x0);
+    const float s1 = chain_group(P.r0 < 0 ? s0 : 0.0f, c[k & 1][1], d[k & 1][1], x1);
+    float* area = sums + (k & 1) * kRows * pair::kStride;
+    const int row = tile_of(k) * kRows + local;
+    if (local < kRows && row < w.rows) {
+      if (P.r0 >= 0) area[local * pair::kStride + P.r0] = s0;
+      area[local * pair::kStride + P.r1] = s1;
+    }
+    __syncthreads();
+    if (t < kRows && tile_of(k) * kRows + t < w.rows)
+      y[tile_of(k) * kRows + t] = pair::row_total(area, t);
+  }
+}
+
 // Gated product: each half-wave one neuron n, its gate row and its up row
 // (rotated ranges), then gelu_tanh(gate) * up and the layer's pins.
 template <int MAXI, int MODE, int WAVES>
@@ -1044,6 +1104,16 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
   const int items1 = max_items(w.cols, 1);
   const int items2 = max_items(w.cols, 2);
   // Many rows: two rows a half-wave, ranges rotated, where that balances.
+  if constexpr (F == kQ4_0 && MODE != 3) {
+    if (w.rows >= 16384 && w.cols == pair::kCols) {
+      constexpr int T = 256, kRows = pair::rows<T>(), TPW = kHeadTilesPerGroup;
+      const int tiles = (w.rows + kRows - 1) / kRows;
+      const size_t lds = (size_t)(2 * kRows * pair::kStride + kRedFloats + pair::kGroups * kXStride) * 4;
+      hipLaunchKernelGGL((gemv_pair_tiles_kernel<MODE, 4, TPW>), dim3((tiles + TPW - 1) / TPW),
+                         dim3(T), lds, s, step, w, in, y);
+      return hipGetLastError();
+    }
+  }
   if (w.rows >= 16384 && items2 <= 3 && w.cols < 1536)
     return launch_write<2, 3, MODE, kHeadTilesPerGroup, 2, F>(s, step, w, in, y);
   // K = 1,152 in Q4_0: two groups every lane; four waves (14 rows) share an
