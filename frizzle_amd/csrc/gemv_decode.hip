@@ -1005,7 +1005,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
 // Gated product at K = 1,152: a neuron takes 36 lanes, 18 for its gate row
 // and 18 for its up row, each lane two groups as in the pair layout; then
 // gelu_tanh(gate) * up and the layer's pins.
-template <int MODE, int WAVES>
+template <int MODE, int WAVES, int TPW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
     const DevStep* __restrict__ step, QMatrix gate, QMatrix up, GemvInput in,
     float* __restrict__ act, const uint32_t* __restrict__ edits, int layer) {
@@ -1014,15 +1014,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
   constexpr int kNeurons = T / (2 * pair::kLanes);
   static_assert(2 * kNeurons <= 64, "the totals sit in the first wave");
   constexpr int X4 = plain_vec4s<1, 2, T>();
-  float* sums = smem;  // [neuron][gate, up][pair::kStride]
-  float* red = sums + 2 * kNeurons * pair::kStride;
+  float* sums = smem;  // [2][neuron][gate, up][pair::kStride]
+  float* red = sums + 2 * 2 * kNeurons * pair::kStride;
   float* xs = red + kRedFloats;
   const int t = threadIdx.x;
   const int local = t / (2 * pair::kLanes);
   const int q = t - local * 2 * pair::kLanes;
   const int which = q >= pair::kLanes ? 1 : 0;
-  const int n = blockIdx.x * kNeurons + local;
-  const bool live = local < kNeurons && n < gate.rows;
+  const int tiles = (gate.rows + kNeurons - 1) / kNeurons;
+  auto tile_of = [&](int k) { return min((int)blockIdx.x * TPW + k, tiles - 1); };
   uint32_t pin_first = 0, pin_count = 0;
   if (edits) {
     pin_first = edits[2 * layer];
@@ -1032,30 +1032,48 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
   Prologue<T, X4> pro;
   prologue_load<MODE, T, X4>(pro, in, step, gate.cols);
   const QMatrix& m = which ? up : gate;
-  const int base = live ? n * pair::kGroups : 0;
-  const uint4 c0 = reinterpret_cast<const uint4*>(m.codes)[base + P.g0];
-  const uint16_t d0 = m.scales[base + P.g0];
-  const uint4 c1 = reinterpret_cast<const uint4*>(m.codes)[base + P.g1];
-  const uint16_t d1 = m.scales[base + P.g1];
+  uint4 c[2][2];
+  uint16_t d[2][2];
+  auto load_tile = [&](int k, int b) {
+    const int n = tile_of(k) * kNeurons + local;
+    const int base = local < kNeurons && n < gate.rows ? n * pair::kGroups : 0;
+    c[b][0] = reinterpret_cast<const uint4*>(m.codes)[base + P.g0];
+    d[b][0] = m.scales[base + P.g0];
+    c[b][1] = reinterpret_cast<const uint4*>(m.codes)[base + P.g1];
+    d[b][1] = m.scales[base + P.g1];
+  };
+  load_tile(0, 0);
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, gate.cols);
   __syncthreads();
-  float s0, s1;
-  pair::chains(P, c0, d0, c1, d1, xs, s0, s1);
-  const int slot = 2 * local + which;
-  if (live) {
-    if (P.r0 >= 0) sums[slot * pair::kStride + P.r0] = s0;
-    sums[slot * pair::kStride + P.r1] = s1;
+  float4 x0[8], x1[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x0[i] = ld4(xs + P.g0 * kXStride + 4 * i);
+    x1[i] = ld4(xs + P.g1 * kXStride + 4 * i);
   }
-  __syncthreads();
-  if (t < 64) {
-    // Thread 2k totals neuron k's gate row, thread 2k + 1 its up row.
-    const float total = t < 2 * kNeurons ? pair::row_total(sums, t) : 0.0f;
-    const float u = row_shl<1>(total);  // lane t + 1: even t stays in its row
-    const int nn = blockIdx.x * kNeurons + (t >> 1);
-    if ((t & 1) == 0 && t < 2 * kNeurons && nn < gate.rows) {
-      float v = gelu_tanh(total) * u;
-      if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)nn, step->position, v);
-      act[nn] = v;
+  const int slot = 2 * local + which;
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    if (k + 1 < TPW) load_tile(k + 1, (k + 1) & 1);
+    const float s0 = chain_group(0.0f, c[k & 1][0], d[k & 1][0], x0);
+    const float s1 = chain_group(P.r0 < 0 ? s0 : 0.0f, c[k & 1][1], d[k & 1][1], x1);
+    float* area = sums + (k & 1) * 2 * kNeurons * pair::kStride;
+    const int n = tile_of(k) * kNeurons + local;
+    if (local < kNeurons && n < gate.rows) {
+      if (P.r0 >= 0) area[slot * pair::kStride + P.r0] = s0;
+      area[slot * pair::kStride + P.r1] = s1;
+    }
+    __syncthreads();
+    if (t < 64) {
+      // Thread 2k totals neuron k's gate row, thread 2k + 1 its up row.
+      const float total = t < 2 * kNeurons ? pair::row_total(area, t) : 0.0f;
+      const float u = row_shl<1>(total);  // lane t + 1: even t stays in its row
+      const int nn = tile_of(k) * kNeurons + (t >> 1);
+      if ((t & 1) == 0 && t < 2 * kNeurons && nn < gate.rows) {
+        float v = gelu_tanh(total) * u;
+        if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)nn, step->position, v);
+        act[nn] = v;
+      }
     }
   }
 }
@@ -1136,6 +1154,8 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
 // Gated workgroups of kGatedWaves waves: the fewer workgroups, the less
 // redundant input-row work and L2 traffic for it.
 constexpr int kGatedWaves = 4;
+// Tiles of 7 neurons a K = 1,152 gated workgroup: its input row is made once for them.
+constexpr int kGatedTiles = 2;
 
 template <int MAXI, int MODE, int kWaves = kGatedWaves>
 hipError_t launch_gated(hipStream_t s, const DevStep* step, const QMatrix& gate,
@@ -1180,16 +1200,16 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix&
   }
 }
 
-template <int MODE, int WAVES>
+template <int MODE, int WAVES, int TPW>
 hipError_t launch_gated_pair(hipStream_t s, const DevStep* step, const QMatrix& gate,
                              const QMatrix& up, const GemvInput& in, float* act,
                              const uint32_t* edits, int layer) {
   constexpr int T = 64 * WAVES, kNeurons = T / (2 * pair::kLanes);
-  const size_t lds = (size_t)(2 * kNeurons * pair::kStride + kRedFloats +
+  const size_t lds = (size_t)(2 * 2 * kNeurons * pair::kStride + kRedFloats +
                               pair::kGroups * kXStride) * 4;
-  hipLaunchKernelGGL((gemv_gated_pair_kernel<MODE, WAVES>),
-                     dim3((gate.rows + kNeurons - 1) / kNeurons), dim3(T), lds, s, step, gate, up,
-                     in, act, edits, layer);
+  const int tiles = (gate.rows + kNeurons - 1) / kNeurons;
+  hipLaunchKernelGGL((gemv_gated_pair_kernel<MODE, WAVES, TPW>), dim3((tiles + TPW - 1) / TPW),
+                     dim3(T), lds, s, step, gate, up, in, act, edits, layer);
   return hipGetLastError();
 }
 
@@ -1204,8 +1224,8 @@ hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix
   }
   // K = 1,152: two groups every lane, 7 neurons a 4-wave workgroup.
   if (gate.cols == pair::kCols) {
-    return mode == 0 ? launch_gated_pair<0, 4>(s, step, gate, up, in, act, edits, layer)
-                     : launch_gated_pair<1, 4>(s, step, gate, up, in, act, edits, layer);
+    return mode == 0 ? launch_gated_pair<0, 4, kGatedTiles>(s, step, gate, up, in, act, edits, layer)
+                     : launch_gated_pair<1, 4, kGatedTiles>(s, step, gate, up, in, act, edits, layer);
   }
   const int items = max_items(gate.cols, 2);
   if (items <= 3) {
