@@ -131,6 +131,28 @@ def test_gated_every_scale_bit_exact(device):
     assert_same_bits(da.numpy()[0], orc.gated(g, u, rows, cols, x), "gated")
 
 
+# Neuron counts whose tiles of 7 do not fill the last workgroup's two: its
+# second tile is the last one again, recomputed to the same bits.
+@pytest.mark.parametrize("rows", [100, 21, 7])
+def test_gated_ragged_tiles_bit_exact(device, rows):
+    rng = np.random.default_rng(300 + rows)
+    cols, layers, layer, position = 1152, 2, 1, 9
+    g = q4_blocks(rng, rows, cols)
+    u = q4_blocks(rng, rows, cols)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    edits = [fz.Edit(layer, n, fz.EditKind.SET, 0.25 * n) for n in range(0, rows, 5)]
+    table = fz.edit_table(edits, layers, origin=position)
+    gc, gs = _q4_dev(device, g)
+    uc, us = _q4_dev(device, u)
+    dx, dt = device.array(x), device.array(table)
+    da = device.empty((1, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gated(device.handle, gc.ptr, gs.ptr, uc.ptr, us.ptr, rows,
+                                         cols, dx.ptr, da.ptr, 1, position, dt.ptr, layer))
+    want = orc.gated(g, u, rows, cols, x[0])
+    orc.lib().orc_edit_row(table.ctypes.data, layer, position, rows, want.ctypes.data)
+    assert_same_bits(da.numpy()[0], want, f"gated {rows} neurons")
+
+
 @pytest.mark.parametrize("rows,cols,tokens", [(1536, 1152, 5), (1152, 6912, 37),
                                                (1152, 1024, 64), (200, 96, 3)])
 def test_gemv_tiled_is_decode_bits(device, rows, cols, tokens):
