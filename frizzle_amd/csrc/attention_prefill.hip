@@ -40,7 +40,9 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
 }
 
 // ---- fold ------------------------------------------------------------------
-// A workgroup folds one row's chunks for 64 dimensions of one head. The
+// A workgroup folds one row's chunks for kFoldDims dimensions of one head
+// (16 for steps of up to 16 rows, whose few workgroups gain from more; 64
+// for longer steps, whose many rows would each repeat the scan 16 times). The
 // chunk states are staged into LDS; the running maximum and liveness before
 // each chunk come from a wave-wide prefix scan (a maximum and an or, exact
 // in any order while no chunk maximum is NaN; with one, lane 0 replays the
@@ -50,7 +52,6 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
 // a time; the chunk count is padded to 8 with records (1, 0, 0, 0) and zero
 // outputs, which leave o, l and liveness as they are (o and l are never -0,
 // so adding 0 * 0 changes no bits).
-constexpr int kFoldDims = 64;
 constexpr int kFoldBatch = 8;  // staging loads a thread keeps in flight; chunks a chain step reads
 
 __host__ __device__ constexpr int fold_padded(int chunks) {
@@ -85,8 +86,10 @@ __device__ __forceinline__ int wave_prefix_or(int v) {
   return v;
 }
 
+template <int kFoldDims>
 __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep* __restrict__ step,
                                                                   FoldArgs f) {
+  constexpr int kFoldVec4s = kFoldDims / 4;  // vec4s of a chunk's output a workgroup stages
   extern __shared__ __align__(16) float fold_smem[];
   const int row = blockIdx.y;
   if (row >= (int)step->tokens) return;
@@ -103,8 +106,9 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   int* lb = reinterpret_cast<int*>(mb + cap);                  // live before chunk c
   const float* part = f.partials + (size_t)row * f.max_chunks * QH * D;
   const float* stats = f.stats + (size_t)row * f.max_chunks * QH * 4;
-  // Stage: the chunk states (one a thread: count <= 224), then uint4 i of the
-  // head's block, chunk i / 16, dims 4 (i % 16); the padding's outputs zero.
+  // Stage: the chunk states (one a thread: count <= 224), then vec4 i of the
+  // head's block, chunk i / kFoldVec4s, dims 4 (i % kFoldVec4s); the
+  // padding's outputs zero.
   float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
   if (t < count) sv = ld4f(stats + ((size_t)t * QH + h) * 4);
   const int vec4s = count * (kFoldDims / 4);
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
 #pragma unroll
     for (int n = 0; n < kFoldBatch; ++n) {
       const int i = base + t + n * kThreads;
-      if (i < vec4s) v[n] = ld4f(part + ((size_t)(i >> 4) * QH + h) * D + dim0 + 4 * (i & 15));
+      if (i < vec4s) v[n] = ld4f(part + ((size_t)(i / kFoldVec4s) * QH + h) * D + dim0 + 4 * (i % kFoldVec4s));
     }
 #pragma unroll
     for (int n = 0; n < kFoldBatch; ++n) {
@@ -203,14 +207,20 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
 
 }  // namespace
 
-hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
-                                 int max_tokens) {
+template <int kFoldDims>
+hipError_t launch_fold(hipStream_t s, const DevStep* step, const FoldArgs& f, int max_tokens) {
   // po, st, rec, mb, lb for the chunk count padded to a batch.
   const size_t lds = (size_t)fold_padded(f.max_chunks) * (kFoldDims * 4 + 16 + 16 + 4 + 4);
-  if (f.max_chunks <= 0 || f.max_chunks > kMaxFoldChunks) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_fold_kernel, dim3(QH * (D / kFoldDims), max_tokens), dim3(kThreads),
-                     lds, s, step, f);
+  hipLaunchKernelGGL(attention_fold_kernel<kFoldDims>, dim3(QH * (D / kFoldDims), max_tokens),
+                     dim3(kThreads), lds, s, step, f);
   return hipGetLastError();
+}
+
+hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
+                                 int max_tokens) {
+  if (f.max_chunks <= 0 || f.max_chunks > kMaxFoldChunks) return hipErrorInvalidValue;
+  return max_tokens <= 16 ? launch_fold<16>(s, step, f, max_tokens)
+                          : launch_fold<64>(s, step, f, max_tokens);
 }
 
 hipError_t launch_attention(hipStream_t s, const DevStep* step, const AttentionArgs& a,
