@@ -30,9 +30,32 @@ __device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Lane l ^ mask's word: masks 1 and 2 by DPP quad permutes, 4 and 8 by DPP
+// row shifts (up or down by the lane's bit), 16 by a swizzle within the
+// 32-lane group, 32 through LDS. `mask` is a constant after unrolling.
+__device__ __forceinline__ int xor_lane(int v, int mask) {
+  const int lane = threadIdx.x & 63;
+  switch (mask) {
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // [1, 0, 3, 2]
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // [2, 3, 0, 1]
+    case 4: {
+      const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);
+      const int down = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+      return (lane & 4) ? down : up;
+    }
+    case 8: {
+      const int up = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xF, 0xF, false);
+      const int down = __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+      return (lane & 8) ? down : up;
+    }
+    case 16: return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 31);
+    default: return __shfl_xor(v, mask, 64);
+  }
+}
+
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, mask, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), mask, 64);
+  const uint32_t lo = (uint32_t)xor_lane((int)(uint32_t)v, mask);
+  const uint32_t hi = (uint32_t)xor_lane((int)(uint32_t)(v >> 32), mask);
   return ((uint64_t)hi << 32) | lo;
 }
 
