@@ -1146,7 +1146,9 @@ hipError_t dispatch_write(hipStream_t s, const DevStep* step, const QMatrix& w,
   if (items1 <= 2) return launch_write<1, 2, MODE, 1, 2, F>(s, step, w, in, y);
   if (items1 <= 4) return launch_write<1, 4, MODE, 1, 2, F>(s, step, w, in, y);
   // Up to 8 items (K to 8,192): four waves, so half as many workgroups stage
-  // the long input row.
+  // the long input row. K = 6,912 (7 items) has its own form, which issues
+  // no load for an eighth item.
+  if (items1 <= 7) return launch_write<1, 7, MODE, 1, 4, F>(s, step, w, in, y);
   if (items1 <= 8) return launch_write<1, 8, MODE, 1, 4, F>(s, step, w, in, y);
   return hipErrorInvalidValue;
 }
