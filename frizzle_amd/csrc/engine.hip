@@ -469,6 +469,23 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
     e = enqueue_decode_layer(m, l, pending);
     pending = m->layers[l].gains[5];
   }
+  if (e == hipSuccess && logits && m->embedding.format == kQ4_0) {
+    // A Q4_0 head takes the final norm in its prologue (every workgroup
+    // makes the normed row; the first also writes it to `normed`).
+    GemvInput h{};
+    h.hidden = m->hidden_b;
+    h.output = m->output;
+    h.post_gain = pending;
+    h.gain = m->output_norm;
+    h.normed_out = m->normed;
+    h.epsilon = c.epsilon;
+    e = launch_gemv_decode(s, m->step, m->embedding, h, 1, m->logits);
+    if (e == hipSuccess) {
+      e = launch_select(s, m->step, m->logits, c.vocab, m->topk_scratch, m->candidates,
+                        m->sampled, m->token_log, advance);
+    }
+    return check_hip(e, "enqueue_decode");
+  }
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden_b, m->normed,
                         c.epsilon, c.hidden, true};

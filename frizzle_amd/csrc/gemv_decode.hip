@@ -3,6 +3,8 @@
 //   the attention norm (and layer 0's embedding gather) before Q/K/V,
 //   the attention fold (local layers) before O,
 //   the feed-forward norm before gate/up (GELU and the pins after it).
+//   the final norm before a Q4_0 head (the first workgroup also writes the
+//     normed row).
 // Every workgroup computes its input row itself, redundantly, with the
 // reference's 256-invocation reduction tree (norm.wgsl:75-198), so every
 // workgroup holds the same bits; the first also writes the new hidden row.
@@ -508,8 +510,10 @@ __device__ __forceinline__ void prologue_finish(float* xs, float* red, Prologue<
     const int q = norm_vec4<T>(s >> 1, s & 1);
     if (q < vec4s && norm_thread<T>()) {
       const float4 x = P.v[s], g = P.g[s];
-      stage4(xs, q, make_float4((x.x * r) * g.x, (x.y * r) * g.y, (x.z * r) * g.z,
-                                (x.w * r) * g.w));
+      const float4 o = make_float4((x.x * r) * g.x, (x.y * r) * g.y, (x.z * r) * g.z,
+                                   (x.w * r) * g.w);
+      stage4(xs, q, o);
+      if (blockIdx.x == 0 && in.normed_out) *reinterpret_cast<float4*>(in.normed_out + 4 * q) = o;
     }
   }
 }

@@ -99,6 +99,7 @@ struct GemvInput {
   const float* partials;
   const float* stats;
   int window;
+  float* normed_out;  // modes 1 and 2: workgroup 0 also writes the normed row here
 };
 constexpr int kFoldPrologueChunks = 10;
 hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix& w,
