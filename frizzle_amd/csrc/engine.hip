@@ -516,11 +516,19 @@ int build_decode_graph(frz_model* m) {
   int rc = enqueue_step(m, 1, true, true);
   hipGraph_t graph = nullptr;
   const int end_rc = check_hip(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
-  if (rc != FRZ_OK) return rc;
-  if (end_rc != FRZ_OK) return end_rc;
+  if (rc == FRZ_OK) rc = end_rc;
+  hipGraphExec_t exec = nullptr;
+  if (rc == FRZ_OK) {
+    rc = check_hip(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+  }
+  if (rc != FRZ_OK) {
+    // Nothing is kept from a failed capture, so the next call captures anew.
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
   m->decode_graph = graph;
-  return check_hip(hipGraphInstantiate(&m->decode_exec, graph, nullptr, nullptr, 0),
-                   "hipGraphInstantiate");
+  m->decode_exec = exec;
+  return FRZ_OK;
 }
 
 // One fed decode step: the captured graph, or its launches one by one.
@@ -990,6 +998,8 @@ int frz_model_time_decode(frz_model* m, uint32_t position, uint32_t steps,
   if (steps > m->token_log_capacity || (uint64_t)position + steps > (uint64_t)m->c.context) {
     return fail(FRZ_ERR_ARGUMENT, "frz_model_time_decode: too many steps for the context");
   }
+  // The timed steps rewrite the caches from `position` on.
+  forget_prefix(m);
   if (m->use_graphs) {
     if (int rc = build_decode_graph(m)) return rc;
   }
@@ -1135,6 +1145,15 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
   // A sliding layer's ring must still hold the window before the resume.
   if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
   m->reused = common;
+  // From here the caches are rewritten: the record is forgotten until the
+  // run succeeds (a failed step leaves them partly rewritten, and the next
+  // run starts over, as the reference empties the cache on a step failure,
+  // runtime.h:51-54). The high-water mark is the most any run wrote since
+  // the caches were last refilled from position 0 (cache/kv.h:30-35), here
+  // counted before the steps so that a failure cannot understate it.
+  forget_prefix(m);
+  const uint64_t run_end = (uint64_t)prompt_len + (max_tokens > 1 ? max_tokens - 1 : 0);
+  m->written_end = common == 0 ? run_end : std::max(m->written_end, run_end);
   uint32_t pos = common;
   while (pos < prompt_len) {
     const uint32_t n = std::min<uint32_t>(kPrefillBlock, prompt_len - pos);
@@ -1142,20 +1161,25 @@ int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
     if (int rc = model_step(m, pos, n, prompt + pos, last ? 1 : 0, sampling)) return rc;
     pos += n;
   }
-  m->cached.assign(prompt, prompt + prompt_len);
-  m->cached_edits = placed;
-  m->written_end = prompt_len;
-  if (max_tokens == 0) return check_hip(hipStreamSynchronize(m->dev->stream), "generate sync");
+  if (max_tokens == 0) {
+    if (int rc = check_hip(hipStreamSynchronize(m->dev->stream), "generate sync")) return rc;
+    m->cached.assign(prompt, prompt + prompt_len);
+    m->cached_edits = placed;
+    return FRZ_OK;
+  }
   uint32_t record[4];
   if (int rc = frz_model_read_record(m, record)) return rc;
+  m->cached.assign(prompt, prompt + prompt_len);
+  m->cached_edits = placed;
   std::vector<uint32_t> out{record[0]};
   bool stopped = record[1] != 0 || std::find(stop_ids, stop_ids + stops, record[0]) != stop_ids + stops;
   if (!stopped && max_tokens > 1) {
     std::vector<uint32_t> more(max_tokens - 1), failed(max_tokens - 1);
     if (int rc = model_decode(m, prompt_len, max_tokens - 1, sampling, more.data(),
-                                  failed.data()))
+                              failed.data())) {
+      forget_prefix(m);
       return rc;
-    m->written_end = (uint64_t)prompt_len + max_tokens - 1;
+    }
     for (uint32_t i = 0; i + 1 < max_tokens; ++i) {
       out.push_back(more[i]);
       if (failed[i] || std::find(stop_ids, stop_ids + stops, more[i]) != stop_ids + stops) break;
@@ -1270,6 +1294,11 @@ int frz_generate_variants(frz_model* m, const uint32_t* prompt, uint32_t prompt_
   common = std::min(common, first_edit_difference(c, m->cached_edits, none));
   if (m->written_end > (uint64_t)common + c.local_slots - c.window) common = 0;
   m->reused = common;
+  // As in frz_generate: the record forgotten while the caches are rewritten,
+  // the high-water mark kept. The variants decode in caches of their own, so
+  // the model's own caches receive positions up to the prompt's last but one.
+  forget_prefix(m);
+  m->written_end = common == 0 ? origin : std::max<uint64_t>(m->written_end, origin);
   for (uint32_t pos = common; pos < origin;) {
     const uint32_t n = std::min<uint32_t>(kPrefillBlock, origin - pos);
     if (int rc = model_step(m, pos, n, prompt + pos, 0, sampling)) return rc;
@@ -1277,7 +1306,6 @@ int frz_generate_variants(frz_model* m, const uint32_t* prompt, uint32_t prompt_
   }
   m->cached.assign(prompt, prompt + origin);
   m->cached_edits = none;
-  m->written_end = origin;
   if (int rc = ensure_variants(m, (int)variants, max_tokens, stride, residuals_out != nullptr))
     return rc;
   frz_model::Variants& V = m->variants;

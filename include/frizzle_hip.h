@@ -456,7 +456,9 @@ int frz_model_read_hidden(frz_model* model, float* out, uint32_t rows);
 int frz_model_read_cache(frz_model* model, int layer, int values,
                          uint16_t* out, uint64_t count);
 /* Mean microseconds of each decode step over `steps` graph replays timed
- * with HIP events on the model's stream (the timed region of bench.py). */
+ * with HIP events on the model's stream (the timed region of bench.py).
+ * The steps rewrite the caches from `position` on, so the next
+ * frz_generate computes its prompt afresh rather than reusing it. */
 int frz_model_time_decode(frz_model* model, uint32_t position, uint32_t steps,
                           const frz_sampling* sampling, double* us_per_step);
 
