@@ -885,6 +885,107 @@ void orc_model_token(orc_model* m, uint32_t token, int position,
   }
 }
 
+namespace {
+// n rows of a product at once: y[t][o] = format_row_total(W_o, x_t) for each
+// row t, bit for bit (the same fma chain a range, k in order, and the same
+// ordered totals), with each weight row decoded once for all n rows. The
+// chains of the n rows are independent, so they step together over k.
+void gemm_rows(int format, const uint8_t* w, int rows, int cols, const float* x, int n,
+               float* y) {
+  const int groups = cols / 32;
+  const int bb = orc_block_bytes(format);
+  const size_t row_bytes = static_cast<size_t>(groups) * bb;
+  std::vector<float> xt(static_cast<size_t>(cols) * n);  // [k][t]
+  for (int t = 0; t < n; ++t)
+    for (int k = 0; k < cols; ++k) xt[static_cast<size_t>(k) * n + t] = x[static_cast<size_t>(t) * cols + k];
+#pragma omp parallel
+  {
+    std::vector<float> wrow(cols), s(n), total(n);
+#pragma omp for schedule(static)
+    for (int o = 0; o < rows; ++o) {
+      for (int g = 0; g < groups; ++g)
+        unpack_format(format, w + o * row_bytes + static_cast<size_t>(g) * bb, &wrow[g * 32]);
+      std::fill(total.begin(), total.end(), 0.0f);
+      for (int r = 0; r < kRanges; ++r) {
+        std::fill(s.begin(), s.end(), 0.0f);
+        for (int k = range_lo(r, groups) * 32; k < range_lo(r + 1, groups) * 32; ++k) {
+          const float wk = wrow[k];
+          const float* xk = &xt[static_cast<size_t>(k) * n];
+#pragma omp simd
+          for (int t = 0; t < n; ++t) s[t] = std::fma(wk, xk[t], s[t]);
+        }
+        for (int t = 0; t < n; ++t) total[t] = total[t] + s[t];
+      }
+      for (int t = 0; t < n; ++t) y[static_cast<size_t>(t) * rows + o] = total[t];
+    }
+  }
+}
+}  // namespace
+
+void orc_model_block(orc_model* m, const uint32_t* tokens, int n, int position,
+                     float* logits) {
+  const orc_config& c = m->c;
+  const int H = c.hidden;
+  const int qw = c.query_heads * c.head_dim;
+  const int kvw = c.kv_heads * c.head_dim;
+  const size_t N = static_cast<size_t>(n);
+  std::vector<float> hidden(N * H), normed(N * H), output(N * H, 0.0f), q(N * qw),
+      k(N * kvw), v(N * kvw), attn(N * qw), gate(N * c.ffn), up(N * c.ffn), act(N * c.ffn);
+  for (int t = 0; t < n; ++t) {
+    orc_gather_row_format(c.embedding_format, m->embedding, H, tokens[t],
+                          std::sqrt(static_cast<float>(H)), &hidden[static_cast<size_t>(t) * H]);
+  }
+  const float* pending = nullptr;
+  const float scale_log2e = static_cast<float>(
+      static_cast<double>(1.0f / std::sqrt(static_cast<float>(c.head_dim))) *
+      1.4426950408889634);
+  for (int l = 0; l < c.layers; ++l) {
+    const orc_layer_weights& w = m->w[l];
+    for (int t = 0; t < n; ++t) {
+      orc_norm_row(w.attn_norm, pending, pending != nullptr, pending != nullptr, 1.0f, c.epsilon,
+                   H, &hidden[t * static_cast<size_t>(H)], &output[t * static_cast<size_t>(H)],
+                   &normed[t * static_cast<size_t>(H)]);
+    }
+    std::copy(hidden.end() - H, hidden.end(), m->residuals.begin() + static_cast<size_t>(l) * H);
+    gemm_rows(2, w.q, qw, H, normed.data(), n, q.data());
+    gemm_rows(2, w.k, kvw, H, normed.data(), n, k.data());
+    gemm_rows(2, w.v, kvw, H, normed.data(), n, v.data());
+    for (int t = 0; t < n; ++t) {
+      orc_rope_row(position + t, m->slots[l], c.head_dim, c.query_heads, c.kv_heads, c.epsilon,
+                   m->turns[l].data(), w.q_norm, w.k_norm, &q[t * static_cast<size_t>(qw)],
+                   &k[t * static_cast<size_t>(kvw)], &v[t * static_cast<size_t>(kvw)],
+                   m->kcache[l].data(), m->vcache[l].data());
+    }
+#pragma omp parallel for schedule(dynamic)
+    for (int t = 0; t < n; ++t) {
+      orc_attention_row(position + t, m->windows[l], m->slots[l], c.head_dim, c.query_heads,
+                        c.kv_heads, scale_log2e, &q[t * static_cast<size_t>(qw)],
+                        m->kcache[l].data(), m->vcache[l].data(),
+                        &attn[t * static_cast<size_t>(qw)]);
+    }
+    gemm_rows(2, w.o, H, qw, attn.data(), n, output.data());
+    for (int t = 0; t < n; ++t) {
+      orc_norm_row(w.ffn_norm, w.post_attn_norm, 1, 1, 1.0f, c.epsilon, H,
+                   &hidden[t * static_cast<size_t>(H)], &output[t * static_cast<size_t>(H)],
+                   &normed[t * static_cast<size_t>(H)]);
+    }
+    gemm_rows(2, w.gate, c.ffn, H, normed.data(), n, gate.data());
+    gemm_rows(2, w.up, c.ffn, H, normed.data(), n, up.data());
+    for (size_t i = 0; i < N * c.ffn; ++i) act[i] = orc_gelu_tanh(gate[i]) * up[i];
+    for (int t = 0; t < n; ++t) {
+      orc_edit_row(m->edits.data(), l, static_cast<uint32_t>(position + t), c.ffn,
+                   &act[t * static_cast<size_t>(c.ffn)]);
+    }
+    gemm_rows(w.down_format, w.down, H, c.ffn, act.data(), n, output.data());
+    pending = w.post_ffn_norm;
+  }
+  // The final norm and the head on the last row (Rows::LastToken).
+  const size_t last = static_cast<size_t>(n - 1) * H;
+  orc_norm_row(m->output_norm, pending, 1, 1, 1.0f, c.epsilon, H, &hidden[last], &output[last],
+               m->normed.data());
+  if (logits) orc_gemv_format(c.embedding_format, m->embedding, c.vocab, H, m->normed.data(), logits);
+}
+
 void orc_model_set_capture(orc_model* m, int on) {
   m->capture = on != 0;
   m->cap.assign(static_cast<size_t>(m->c.layers) * 8, {});

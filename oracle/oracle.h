@@ -195,6 +195,16 @@ void orc_model_set_edits(orc_model* m, const uint32_t* table, int words);
  * (vocab floats) when `logits` is not null. */
 void orc_model_token(orc_model* m, uint32_t token, int position,
                      float* logits);
+/* A prefill block: n (1 .. 512) tokens from `position`, layer by layer, as
+ * one step of the reference's prefill runs them. Each row's arithmetic is
+ * orc_model_token's; each layer appends the block's keys and values before
+ * any row attends (a sliding layer's ring holds at least window + 512
+ * slots, so no row's window is overwritten). Writes the last row's logits
+ * when `logits` is not null; the residuals are the last row's. The capture
+ * store is not written (orc_model_token writes it). Pinned by equality with
+ * orc_model_token, token by token, in tests/test_oracle_pins.py. */
+void orc_model_block(orc_model* m, const uint32_t* tokens, int n, int position,
+                     float* logits);
 /* The last layer's output row after the final norm (hidden floats). */
 const float* orc_model_normed(const orc_model* m);
 /* [layers][hidden]: for the last token, the residual entering each layer

@@ -72,6 +72,7 @@ _SIGS = {
     "orc_model_destroy": (None, [_P]),
     "orc_model_set_edits": (None, [_P, _P, c_int]),
     "orc_model_token": (None, [_P, c_uint32, c_int, _P]),
+    "orc_model_block": (None, [_P, _P, c_int, c_int, _P]),
     "orc_model_normed": (c_void_p, [_P]),
     "orc_model_residuals": (c_void_p, [_P]),
     "orc_model_set_capture": (None, [_P, c_int]),
@@ -240,6 +241,25 @@ class OracleModel:
         lib().orc_model_token(self.handle, int(token), int(position),
                               _p(logits) if want_logits else None)
         return logits
+
+    def block(self, tokens, position, want_logits=True):
+        """A prefill block of up to 512 tokens from `position`; the last
+        row's logits."""
+        ids = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.empty(self.cfg.vocab, dtype=np.float32) if want_logits else None
+        lib().orc_model_block(self.handle, _p(ids), ids.size, int(position),
+                              _p(logits) if want_logits else None)
+        return logits
+
+    def prompt(self, tokens, position=0, block=512):
+        """A prompt in prefill blocks of `block` tokens; the last row's
+        logits."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        lg = None
+        for at in range(0, tokens.size, block):
+            part = tokens[at:at + block]
+            lg = self.block(part, position + at, want_logits=at + block >= tokens.size)
+        return lg
 
     def key_cache(self, layer):
         slots = lib().orc_model_slots(self.handle, layer)

@@ -22,10 +22,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _oracle_prompt(oracle, prompt):
-    lg = None
-    for p, tok in enumerate(prompt):
-        lg = oracle.token(int(tok), p, want_logits=(p == len(prompt) - 1))
-    return lg
+    """The prompt in the oracle's prefill blocks of 512 (each row's
+    arithmetic is its token-by-token path's)."""
+    return oracle.prompt(prompt)
 
 
 def _oracle_greedy(oracle, logits, position, steps):

@@ -474,3 +474,39 @@ def test_model_pin_reaches_the_residual_through_down(layer):
                                                  t[(1, "post_ffn_norm")])))
     m.close()
     m2.close()
+
+
+# ---- the prefill block ----------------------------------------------------------------
+
+@pytest.mark.parametrize("window,slots,pattern,blocks", [
+    (64, 640, 3, [37, 63, 100]),     # a ring of 640 wrapped by the third block
+    (512, 1024, 2, [300, 212, 40]),  # the real window, a global layer each second
+])
+def test_model_block_is_token_by_token(window, slots, pattern, blocks):
+    # A prefill block runs each row through the same arithmetic as a token
+    # alone: the last row's logits, every layer's caches and the residuals
+    # equal orc_model_token's run over the same positions, bit for bit,
+    # with a pin acting on some rows.
+    cfg = fz.gemma3_1b_config(layers=3, vocab=512, window=window, pattern=pattern,
+                              context=1024, local_slots=slots)
+    t = _tensors(cfg, 61, live={(l, r) for l in range(3) for r in MATRICES})
+    table = fz.edit_table([fz.Edit(1, 17, fz.EditKind.SET, 3.5, 0, 0xFFFFFFFF),
+                           fz.Edit(2, 900, fz.EditKind.SCALE, -2.0, 50, 120)], cfg.layers, 0)
+    a = orc.OracleModel(cfg.as_dict(), t)
+    b = orc.OracleModel(cfg.as_dict(), t)
+    a.set_edits(table)
+    b.set_edits(table)
+    ids = np.random.default_rng(62).integers(0, cfg.vocab, sum(blocks)).astype(np.uint32)
+    at = 0
+    for n in blocks:
+        got = a.block(ids[at:at + n], at)
+        for p in range(at, at + n):
+            want = b.token(int(ids[p]), p, want_logits=(p == at + n - 1))
+        assert np.array_equal(bits(got), bits(want)), (at, n)
+        assert np.array_equal(bits(a.residuals()), bits(b.residuals()))
+        for l in range(cfg.layers):
+            assert np.array_equal(a.key_cache(l), b.key_cache(l)), l
+            assert np.array_equal(a.value_cache(l), b.value_cache(l)), l
+        at += n
+    a.close()
+    b.close()
