@@ -104,6 +104,8 @@ _SIGS = {
                                  c_uint32]),
     "frz_op_rope_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int,
                                       c_int, c_float, c_float, c_uint32]),
+    "frz_op_rope_attention_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int,
+                                              c_int, c_float, c_float, c_uint32]),
     "frz_op_gather": (c_int, [_P, _P, _P, c_int, c_int, _P, c_uint32, c_float,
                               _P]),
     "frz_op_edit": (c_int, [_P, _P, c_int, _P, c_int, c_uint32, c_uint32]),

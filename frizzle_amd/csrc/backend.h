@@ -13,6 +13,9 @@ struct frz_device {
   hipDeviceProp_t props{};
   hipStream_t stream = nullptr;
   frz::DevStep* step = nullptr;  // the one-kernel ops' step record
+  // This device's copy of the static decode-attention workspace (the
+  // address hipGetSymbolAddress gave at frz_open, with this device current).
+  float* static_workspace = nullptr;
 };
 
 namespace frz {

@@ -60,6 +60,15 @@ DevStep host_step(uint32_t position, uint32_t tokens) {
   return s;
 }
 
+// The workspace of frz_op_rope_attention_noalloc: one row's chunk states
+// (kStaticChunks x 4 heads x 256 outputs, then 4 statistics a chunk and
+// head), 931,840 bytes. Every device the library opens holds its own copy
+// until the process ends; host code reaches it only through the address
+// frz_open takes for each device (frz_device::static_workspace).
+constexpr int kStaticChunks = kMaxFoldChunks;
+constexpr size_t kStaticPartialFloats = (size_t)kStaticChunks * 4 * 256;
+static __device__ __align__(256) float scratch[kStaticPartialFloats + kStaticPartialFloats / 64];
+
 }  // namespace
 
 int device_put_step(frz_device* dev, const DevStep& s) {
@@ -127,6 +136,17 @@ int frz_open(int ordinal, frz_device** out, frz_limits* limits) {
     delete dev;
     return rc;
   }
+  // This device's address of the static workspace (each device holds its own
+  // copy of the array; the name itself is no device address on the host).
+  void* workspace = nullptr;
+  if (int rc = check_hip(hipGetSymbolAddress(&workspace, HIP_SYMBOL(scratch)),
+                         "hipGetSymbolAddress(scratch)")) {
+    (void)hipFree(dev->step);
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+    return rc;
+  }
+  dev->static_workspace = static_cast<float*>(workspace);
   if (limits) {
     std::memset(limits, 0, sizeof *limits);
     std::strncpy(limits->name, prop.gcnArchName, sizeof(limits->name) - 1);
@@ -340,6 +360,44 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
   }
   (void)hipFree(partials);
   return rc;
+}
+
+int frz_op_rope_attention_noalloc(frz_device* dev, const float* qkv, const float* turns,
+                                  const float* query_gain, const float* key_gain,
+                                  uint16_t* key_cache, uint16_t* value_cache, float* out,
+                                  int slots, int window, float epsilon, float scale,
+                                  uint32_t position) {
+  if (!dev || !dev->static_workspace) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: no device");
+  }
+  if (window <= 0 || slots <= 0 || (int)position >= 0x7fffffff) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: bad window or slots");
+  }
+  const int max_chunks = attention_max_chunks(window, slots);
+  if (max_chunks > kStaticChunks) {
+    return fail(FRZ_ERR_ARGUMENT,
+                "frz_op_rope_attention_noalloc: window and slots reach " +
+                    std::to_string(max_chunks) + " chunks; the static workspace holds " +
+                    std::to_string(kStaticChunks) + " (at most 14,272 keys)");
+  }
+  // Chunk states at the same offsets the allocating entry point gives them:
+  // every state the fold reads is written first by this call's attention
+  // launch, so nothing needs clearing between calls.
+  float* partials = dev->static_workspace;
+  const size_t part_floats = (size_t)max_chunks * 4 * 256;
+  if (int rc = device_put_step(dev, host_step(position, 1))) return rc;
+  const float scale_log2e = (float)((double)scale * 1.4426950408889634);
+  DecodeAttentionArgs a{qkv,        turns,    query_gain,            key_gain, key_cache,
+                        value_cache, partials, partials + part_floats, slots,   window,
+                        256,        4,        1,                     max_chunks, epsilon,
+                        scale_log2e};
+  hipError_t e = launch_attention_decode(dev->stream, dev->step, a);
+  if (e == hipSuccess) {
+    e = launch_attention_fold(dev->stream, dev->step,
+                              FoldArgs{partials, partials + part_floats, out, window, max_chunks},
+                              1);
+  }
+  return device_finish(dev, e, "frz_op_rope_attention_noalloc");
 }
 
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales, int rows, int cols,

@@ -144,6 +144,19 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
                           uint16_t* key_cache, uint16_t* value_cache, float* out,
                           int slots, int window, float epsilon, float scale,
                           uint32_t position);
+/* The same as frz_op_rope_attention, allocating nothing: no counterpart in
+ * the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The chunk states live in a static workspace of 931,840 bytes that each
+ * device holds until the process ends, so window and slots may reach at
+ * most 224 chunks (14,272 keys; FRZ_ERR_ARGUMENT beyond). Every call on one
+ * device shares that workspace, which keeps the last call's contents (each
+ * call writes every state it reads): calls that overlap on one device race. */
+int frz_op_rope_attention_noalloc(frz_device* dev, const float* qkv, const float* turns,
+                                  const float* query_gain, const float* key_gain,
+                                  uint16_t* key_cache, uint16_t* value_cache, float* out,
+                                  int slots, int window, float epsilon, float scale,
+                                  uint32_t position);
 /* Embedding rows times scale (kernels/gather/gather.wgsl:25-48). */
 int frz_op_gather(frz_device* dev, const void* codes, const void* scales,
                   int rows, int cols, const uint32_t* ids, uint32_t tokens,
