@@ -54,6 +54,30 @@ class Edit(ctypes.Structure):
                 ("value", c_float), ("from_", c_uint32), ("until", c_uint32)]
 
 
+class PlanLimits(ctypes.Structure):
+    _fields_ = [("max_buffer_size", c_uint64), ("max_storage_binding_size", c_uint64),
+                ("storage_offset_alignment", c_uint32)]
+
+
+class LoadPolicy(ctypes.Structure):
+    _fields_ = [("memory_budget", c_uint64), ("rollback_reserve", c_uint32)]
+
+
+class Range(ctypes.Structure):
+    _fields_ = [("buffer", c_uint32), ("offset", c_uint64), ("length", c_uint64)]
+
+
+class Piece(ctypes.Structure):
+    _fields_ = [("range", Range), ("first_row", c_uint64), ("rows", c_uint64)]
+
+
+class PlanSummary(ctypes.Structure):
+    _fields_ = [(n, c_uint32) for n in ("buffers", "tensors", "pieces", "groups", "layers",
+                                        "scratch", "partial_rows", "context_offered",
+                                        "trained_context")] + [
+        (n, c_uint64) for n in ("weight_bytes", "cache_bytes", "scratch_bytes", "total_bytes")]
+
+
 class GgufTensor(ctypes.Structure):
     _fields_ = [("name", c_char * 65), ("type", c_uint32), ("dimensions", c_uint32),
                 ("shape", c_uint64 * 4), ("elements", c_uint64), ("offset", c_uint64),
@@ -183,6 +207,19 @@ _SIGS = {
     "frz_gguf_get_array": (c_int, [_P, _S, POINTER(c_uint32), POINTER(c_uint64)]),
     "frz_gemma3_config_from_gguf": (c_int, [_P, c_int, POINTER(ModelConfig)]),
     "frz_model_load_gguf": (c_int, [_P, _S]),
+    "frz_load_policy_default": (None, [POINTER(LoadPolicy)]),
+    "frz_plan_gemma3": (c_int, [_P, POINTER(PlanLimits), POINTER(LoadPolicy), POINTER(c_void_p),
+                                POINTER(PlanSummary), _P, ctypes.c_size_t]),
+    "frz_plan_free": (None, [_P]),
+    "frz_plan_error_text": (_S, [c_int]),
+    "frz_plan_config": (c_int, [_P, POINTER(ModelConfig)]),
+    "frz_plan_buffer": (c_int, [_P, c_uint32, POINTER(c_int), POINTER(c_uint64)]),
+    "frz_plan_tensor": (c_int, [_P, c_uint64, c_uint32, POINTER(Piece), POINTER(c_uint32)]),
+    "frz_plan_group": (c_int, [_P, c_uint32, POINTER(c_uint64), POINTER(c_uint32),
+                               POINTER(Range)]),
+    "frz_plan_cache": (c_int, [_P, c_uint32, POINTER(Range), POINTER(Range), POINTER(c_uint32)]),
+    "frz_plan_scratch": (c_int, [_P, _S, POINTER(Range)]),
+    "frz_plan_role": (c_int, [_P, c_int, c_int, POINTER(c_uint64)]),
 }
 
 _lib = None

@@ -135,3 +135,8 @@ struct File {
 int read_file(File& file, Index& out);
 
 }  // namespace frz::gguf
+
+// The C ABI's index handle (frizzle_hip.h, frz_gguf).
+struct frz_gguf {
+  frz::gguf::Index index;
+};

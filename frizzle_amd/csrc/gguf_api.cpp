@@ -12,9 +12,6 @@
 #include "../../include/frizzle_hip.h"
 #include "gguf.h"
 
-struct frz_gguf {
-  frz::gguf::Index index;
-};
 
 namespace frz {
 // Sets the calling thread's message and returns `status` (backend.hip).

@@ -26,7 +26,7 @@ ERRORS = [
 
 # GGUF's metadata value types and the tensor formats used here.
 U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
-T_F32, T_F16, T_Q4_0, T_Q8_0 = 0, 1, 2, 8
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0 = 0, 1, 2, 3, 8
 
 
 class GgufError(ValueError):
@@ -163,29 +163,46 @@ def _value(vtype, value):
     return struct.pack(_SCALAR[vtype], value)
 
 
-def write(path, tensors, metadata=(), alignment=32):
-    """A GGUF v3 file: tensors as (name, extents ne0 first, format, bytes),
-    metadata as (key, value type, value); data aligned to `alignment`."""
+def _encode(tensors, metadata, alignment):
+    """The header and index of a GGUF v3 file (tensors as (name, extents,
+    format, bytes)), padded to the data's alignment, and each tensor's data
+    offset and padded length."""
     md = [(k, t, v) for k, t, v in metadata]
     if alignment != 32 and not any(k == "general.alignment" for k, _, _ in md):
         md.append(("general.alignment", U32, alignment))
     out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(md)))
     for key, vtype, value in md:
         out += _gstr(key.encode()) + struct.pack("<I", vtype) + _value(vtype, value)
-    offset, blobs = 0, []
-    for name, dims, ttype, data in tensors:
+    offset, spans = 0, []
+    for name, dims, ttype, nbytes in tensors:
         out += _gstr(name.encode()) + struct.pack("<I", len(dims))
         out += b"".join(struct.pack("<q", d) for d in dims)
         out += struct.pack("<IQ", ttype, offset)
-        pad = (-len(data)) % alignment
-        blobs.append(bytes(data) + b"\0" * pad)
-        offset += len(data) + pad
+        pad = (-nbytes) % alignment
+        spans.append(nbytes + pad)
+        offset += nbytes + pad
     out += b"\0" * ((-len(out)) % alignment)
+    return bytes(out), spans
+
+
+def write(path, tensors, metadata=(), alignment=32):
+    """A GGUF v3 file: tensors as (name, extents ne0 first, format, bytes),
+    metadata as (key, value type, value); data aligned to `alignment`."""
+    head, spans = _encode([(n, d, t, len(b)) for n, d, t, b in tensors], metadata, alignment)
     with open(path, "wb") as f:
-        f.write(out)
-        for b in blobs:
-            f.write(b)
+        f.write(head)
+        for (_, _, _, data), span in zip(tensors, spans):
+            f.write(bytes(data) + b"\0" * (span - len(data)))
     return Path(path)
+
+
+def index_only(tensors, metadata=(), alignment=32):
+    """The front of a GGUF v3 file holding only its header and index
+    (tensors as (name, extents, format, data bytes)), and the size the whole
+    file would have: read with Index.read(front, size), whose index reads no
+    tensor data."""
+    head, spans = _encode(tensors, metadata, alignment)
+    return head, len(head) + sum(spans)
 
 
 LAYER_NAMES = {

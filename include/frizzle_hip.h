@@ -616,6 +616,91 @@ int frz_gemma3_config_from_gguf(const frz_gguf* index, int context,
  * output.weight. */
 int frz_model_load_gguf(frz_model* model, const char* path);
 
+/* ---- the residency plan (replaces residency::plan_residency,
+ *      src/core/residency/plan.h:14-326, under policy::LoadPolicy,
+ *      src/core/policy/policy.h:23-76) -----------------------------------
+ * Where every weight, each layer's KV cache and every working buffer lies
+ * on the device, and the context offered: a pure function of a Gemma 3
+ * file's index, the device's limits and the load policy (no device, no
+ * I/O). Three pools never share a buffer; every range starts at a multiple
+ * of the alignment and is its bytes rounded up to 4, at most min(binding,
+ * buffer) long. A weight is cut into pieces of whole rows in file order; a
+ * layer's Q, K, V and its gate, up form a group when they share a format and
+ * an input width and their span fits one range in one buffer. Each working
+ * buffer (the decoder's 18, graph.cpp:132-198) is a buffer of its own. A
+ * sliding layer's cache is a ring of window + 512 + rollback_reserve slots,
+ * a full-attention layer's the context offered: the largest from
+ * min(512, trained) to the trained context (gemma3.context_length) whose
+ * cache fits beside the weights and working buffers within the budget. */
+typedef struct frz_plan_limits {
+  uint64_t max_buffer_size;
+  uint64_t max_storage_binding_size;
+  uint32_t storage_offset_alignment; /* a power of two */
+} frz_plan_limits;
+/* LoadPolicy with its F16 cache: the bytes the plan may place, and the
+ * tokens a sliding layer's ring keeps beyond one step for rollback. */
+typedef struct frz_load_policy {
+  uint64_t memory_budget;
+  uint32_t rollback_reserve;
+} frz_load_policy;
+/* policy.h's defaults: 2 GiB, 4,096. */
+void frz_load_policy_default(frz_load_policy* out);
+/* PlanError (plan.h:305-319), plus a file that describes no Gemma 3 model. */
+enum frz_plan_error {
+  FRZ_PLAN_OK = 0,
+  FRZ_PLAN_EXCEEDS_BUDGET = 1,       /* summary->total_bytes: what 512 needs */
+  FRZ_PLAN_ROW_EXCEEDS_BINDING = 2,  /* subject: the tensor */
+  FRZ_PLAN_SCRATCH_EXCEEDS_BINDING = 3, /* subject: the working buffer */
+  FRZ_PLAN_OVERFLOW = 4,
+  FRZ_PLAN_NOT_DESCRIBED = 5         /* subject: the metadata key or tensor */
+};
+enum frz_pool { FRZ_POOL_WEIGHTS = 0, FRZ_POOL_CACHE = 1, FRZ_POOL_SCRATCH = 2 };
+typedef struct frz_range {
+  uint32_t buffer;
+  uint64_t offset;
+  uint64_t length;
+} frz_range;
+/* A weight piece: its range and the rows of the tensor it holds. */
+typedef struct frz_piece {
+  frz_range range;
+  uint64_t first_row;
+  uint64_t rows;
+} frz_piece;
+typedef struct frz_plan_summary {
+  uint32_t buffers, tensors, pieces, groups, layers, scratch;
+  uint32_t partial_rows;
+  uint32_t context_offered;
+  uint32_t trained_context;
+  uint64_t weight_bytes, cache_bytes, scratch_bytes, total_bytes;
+} frz_plan_summary;
+typedef struct frz_plan frz_plan;
+/* Plans the Gemma 3 model of `index`. Returns a frz_plan_error; on
+ * FRZ_PLAN_OK *out is a new plan (frz_plan_free). `subject` (when not null)
+ * receives the refusal's subject, cut to subject_cap - 1 bytes. */
+int frz_plan_gemma3(const frz_gguf* index, const frz_plan_limits* limits,
+                    const frz_load_policy* policy, frz_plan** out,
+                    frz_plan_summary* summary, char* subject, size_t subject_cap);
+void frz_plan_free(frz_plan* plan);
+const char* frz_plan_error_text(int error);
+/* The model's shapes, its context the context offered and its sliding
+ * rings the plan's. */
+int frz_plan_config(const frz_plan* plan, frz_model_config* out);
+int frz_plan_buffer(const frz_plan* plan, uint32_t index, int* pool, uint64_t* size);
+/* Tensor `tensor` of the index (index order): *pieces its piece count, and
+ * piece `piece` into *out when out is not null. */
+int frz_plan_tensor(const frz_plan* plan, uint64_t tensor, uint32_t piece, frz_piece* out,
+                    uint32_t* pieces);
+/* Group i: its members (tensor indices, output order), count and span. */
+int frz_plan_group(const frz_plan* plan, uint32_t index, uint64_t members[3],
+                   uint32_t* count, frz_range* span);
+int frz_plan_cache(const frz_plan* plan, uint32_t layer, frz_range* keys,
+                   frz_range* values, uint32_t* slots);
+/* A working buffer by its purpose ("hidden", "normed", ..., "captures"). */
+int frz_plan_scratch(const frz_plan* plan, const char* purpose, frz_range* out);
+/* The tensor index of a layer's role (layer -1: the embedding or the
+ * output norm). */
+int frz_plan_role(const frz_plan* plan, int layer, int role, uint64_t* tensor);
+
 #ifdef __cplusplus
 }
 #endif
