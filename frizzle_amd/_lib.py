@@ -220,6 +220,11 @@ _SIGS = {
     "frz_plan_cache": (c_int, [_P, c_uint32, POINTER(Range), POINTER(Range), POINTER(c_uint32)]),
     "frz_plan_scratch": (c_int, [_P, _S, POINTER(Range)]),
     "frz_plan_role": (c_int, [_P, c_int, c_int, POINTER(c_uint64)]),
+    "frz_plan_summarize": (c_int, [_P, POINTER(PlanSummary)]),
+    "frz_plan_format": (c_int, [_P, c_uint64, POINTER(c_uint32)]),
+    "frz_device_plan_limits": (c_int, [_P, POINTER(PlanLimits)]),
+    "frz_model_create_planned": (c_int, [_P, _P, POINTER(c_void_p)]),
+    "frz_model_planned_buffer": (c_int, [_P, c_uint32, POINTER(c_void_p), POINTER(c_uint64)]),
 }
 
 _lib = None

@@ -53,6 +53,9 @@ __global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
 // outputs, which leave o, l and liveness as they are (o and l are never -0,
 // so adding 0 * 0 changes no bits).
 constexpr int kFoldBatch = 8;  // staging loads a thread keeps in flight; chunks a chain step reads
+// Chunk states staged in LDS at once: a row's chunks are folded in segments
+// of this many, the running state carried between them, so any context folds.
+constexpr int kFoldSegment = 224;
 
 __host__ __device__ constexpr int fold_padded(int chunks) {
   return (chunks + kFoldBatch - 1) / kFoldBatch * kFoldBatch;
@@ -95,8 +98,7 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   if (row >= (int)step->tokens) return;
   const int p = (int)step->position + (step->variants ? 0 : row);
   const int count = chunk_range(p, f.window, 0).count;
-  const int padded = fold_padded(count);
-  const int cap = fold_padded(f.max_chunks);
+  const int cap = fold_padded(min(f.max_chunks, kFoldSegment));
   const int h = blockIdx.x / (D / kFoldDims), dim0 = (blockIdx.x % (D / kFoldDims)) * kFoldDims;
   const int t = threadIdx.x;
   float* po = fold_smem;                                       // [cap][64]
@@ -106,99 +108,121 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   int* lb = reinterpret_cast<int*>(mb + cap);                  // live before chunk c
   const float* part = f.partials + (size_t)row * f.max_chunks * QH * D;
   const float* stats = f.stats + (size_t)row * f.max_chunks * QH * 4;
-  // Stage: the chunk states (one a thread: count <= 224), then vec4 i of the
-  // head's block, chunk i / kFoldVec4s, dims 4 (i % kFoldVec4s); the
-  // padding's outputs zero.
-  float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (t < count) sv = ld4f(stats + ((size_t)t * QH + h) * 4);
-  const int vec4s = count * (kFoldDims / 4);
-  for (int base = 0; base < vec4s; base += kFoldBatch * kThreads) {
-    float4 v[kFoldBatch];
+  // Carried from segment to segment: the scan's maximum and liveness before
+  // the segment (wave 0), the serial replay's once a NaN maximum is seen
+  // (lane 0), and each dimension's chains (threads below kFoldDims).
+  bool carry_live = false, nan_seen = false, replay_live = false;
+  float carry_m = 0.0f, replay_m = 0.0f;
+  bool live = false;
+  float l = 0.0f, o = 0.0f;
+  int seg0 = 0;
+  for (;;) {
+    const int n = min(count - seg0, kFoldSegment);
+    const int padded = fold_padded(n);
+    // Stage: the segment's chunk states (one a thread: n <= 224), then vec4
+    // i of the head's block, chunk seg0 + i / kFoldVec4s, dims
+    // 4 (i % kFoldVec4s); the padding's outputs zero.
+    float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < n) sv = ld4f(stats + ((size_t)(seg0 + t) * QH + h) * 4);
+    const int vec4s = n * (kFoldDims / 4);
+    const float* seg_part = part + (size_t)seg0 * QH * D;
+    for (int base = 0; base < vec4s; base += kFoldBatch * kThreads) {
+      float4 v[kFoldBatch];
 #pragma unroll
-    for (int n = 0; n < kFoldBatch; ++n) {
-      const int i = base + t + n * kThreads;
-      if (i < vec4s) v[n] = ld4f(part + ((size_t)(i / kFoldVec4s) * QH + h) * D + dim0 + 4 * (i % kFoldVec4s));
-    }
-#pragma unroll
-    for (int n = 0; n < kFoldBatch; ++n) {
-      const int i = base + t + n * kThreads;
-      if (i < vec4s) reinterpret_cast<float4*>(po)[i] = v[n];
-    }
-  }
-  for (int i = vec4s + t; i < padded * (kFoldDims / 4); i += kThreads)
-    reinterpret_cast<float4*>(po)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (t < count) st[t] = sv;
-  __syncthreads();
-  if (t < 64) {
-    bool carry_live = false, nan = false;
-    float carry_m = 0.0f;
-    for (int base = 0; base < count; base += 64) {
-      const int c = base + t;
-      const float4 s4 = c < count ? st[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const bool cl = c < count && s4.z != 0.0f;
-      nan = nan || (cl && s4.x != s4.x);
-      const float v = wave_prefix_max(cl ? s4.x : -__builtin_inff());
-      const int lv = wave_prefix_or(cl ? 1 : 0);
-      // Exclusive: lane c - 1's (lane 0: nothing before).
-      const float ev = __builtin_bit_cast(
-          float, dpp_or_old<0x138>(__builtin_bit_cast(int, -__builtin_inff()), __builtin_bit_cast(int, v)));
-      const int el = dpp_or_old<0x138>(0, lv);
-      if (c < count) {
-        lb[c] = carry_live || el;
-        mb[c] = carry_live ? (el ? __builtin_fmaxf(carry_m, ev) : carry_m) : ev;
+      for (int k = 0; k < kFoldBatch; ++k) {
+        const int i = base + t + k * kThreads;
+        if (i < vec4s)
+          v[k] = ld4f(seg_part + ((size_t)(i / kFoldVec4s) * QH + h) * D + dim0 + 4 * (i % kFoldVec4s));
       }
-      const float last_v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-      const int last_l = __builtin_amdgcn_readlane(lv, 63);
-      carry_m = carry_live ? (last_l ? __builtin_fmaxf(carry_m, last_v) : carry_m) : last_v;
-      carry_live = carry_live || last_l;
-    }
-    if (__any(nan) && t == 0) {
-      bool live = false;
-      float m = 0.0f;
-      for (int c = 0; c < count; ++c) {
-        lb[c] = live;
-        mb[c] = m;
-        const Fold g = fold_factors(live, m, st[c].z != 0.0f, st[c].x);
-        m = g.m;
-        live = live || st[c].z != 0.0f;
+#pragma unroll
+      for (int k = 0; k < kFoldBatch; ++k) {
+        const int i = base + t + k * kThreads;
+        if (i < vec4s) reinterpret_cast<float4*>(po)[i] = v[k];
       }
     }
-  }
-  __syncthreads();
-  for (int c = t; c < padded; c += kThreads) {
-    if (c < count) {
-      const float4 s4 = st[c];
-      const Fold g = fold_factors(lb[c] != 0, mb[c], s4.z != 0.0f, s4.x);
-      rec[c] = make_float4(g.a, g.b, s4.y, s4.z);
-    } else {
-      rec[c] = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+    for (int i = vec4s + t; i < padded * (kFoldDims / 4); i += kThreads)
+      reinterpret_cast<float4*>(po)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < n) st[t] = sv;
+    __syncthreads();
+    if (t < 64) {
+      bool nan = false;
+      for (int base = 0; base < n; base += 64) {
+        const int c = base + t;
+        const float4 s4 = c < n ? st[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool cl = c < n && s4.z != 0.0f;
+        nan = nan || (cl && s4.x != s4.x);
+        const float v = wave_prefix_max(cl ? s4.x : -__builtin_inff());
+        const int lv = wave_prefix_or(cl ? 1 : 0);
+        // Exclusive: lane c - 1's (lane 0: nothing before).
+        const float ev = __builtin_bit_cast(
+            float, dpp_or_old<0x138>(__builtin_bit_cast(int, -__builtin_inff()), __builtin_bit_cast(int, v)));
+        const int el = dpp_or_old<0x138>(0, lv);
+        if (c < n) {
+          lb[c] = carry_live || el;
+          mb[c] = carry_live ? (el ? __builtin_fmaxf(carry_m, ev) : carry_m) : ev;
+        }
+        const float last_v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+        const int last_l = __builtin_amdgcn_readlane(lv, 63);
+        carry_m = carry_live ? (last_l ? __builtin_fmaxf(carry_m, last_v) : carry_m) : last_v;
+        carry_live = carry_live || last_l;
+      }
+      // Until a chunk maximum is NaN the scan is exact and the serial
+      // recursion's state is the scan's; from then on lane 0 replays it.
+      const bool replay = nan_seen || __any(nan);
+      if (replay && t == 0) {
+        for (int c = 0; c < n; ++c) {
+          lb[c] = replay_live;
+          mb[c] = replay_m;
+          const Fold g = fold_factors(replay_live, replay_m, st[c].z != 0.0f, st[c].x);
+          replay_m = g.m;
+          replay_live = replay_live || st[c].z != 0.0f;
+        }
+      }
+      nan_seen = replay;
+      if (!replay) {
+        replay_m = carry_m;
+        replay_live = carry_live;
+      }
     }
+    __syncthreads();
+    for (int c = t; c < padded; c += kThreads) {
+      if (c < n) {
+        const float4 s4 = st[c];
+        const Fold g = fold_factors(lb[c] != 0, mb[c], s4.z != 0.0f, s4.x);
+        rec[c] = make_float4(g.a, g.b, s4.y, s4.z);
+      } else {
+        rec[c] = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+    __syncthreads();
+    if (t < kFoldDims) {
+      for (int base = 0; base < padded; base += kFoldBatch) {
+        float4 r[kFoldBatch];
+        float v[kFoldBatch];
+#pragma unroll
+        for (int k = 0; k < kFoldBatch; ++k) {
+          r[k] = rec[base + k];
+          v[k] = po[(base + k) * kFoldDims + t];
+        }
+#pragma unroll
+        for (int k = 0; k < kFoldBatch; ++k) {
+          l = l * r[k].x + r[k].z * r[k].y;
+          o = o * r[k].x + v[k] * r[k].y;
+          live = live || r[k].w != 0.0f;
+        }
+      }
+    }
+    if (seg0 + n >= count) break;
+    seg0 += n;
+    __syncthreads();  // every thread is done with this segment's staging
   }
-  __syncthreads();
   if (t < kFoldDims) {
-    bool live = false;
-    float l = 0.0f, o = 0.0f;
-    for (int base = 0; base < padded; base += kFoldBatch) {
-      float4 r[kFoldBatch];
-      float v[kFoldBatch];
-#pragma unroll
-      for (int k = 0; k < kFoldBatch; ++k) {
-        r[k] = rec[base + k];
-        v[k] = po[(base + k) * kFoldDims + t];
-      }
-#pragma unroll
-      for (int k = 0; k < kFoldBatch; ++k) {
-        l = l * r[k].x + r[k].z * r[k].y;
-        o = o * r[k].x + v[k] * r[k].y;
-        live = live || r[k].w != 0.0f;
-      }
-    }
     f.out[(size_t)row * QH * D + h * D + dim0 + t] = live ? o / l : 0.0f;
     // The last row's (m, l), for the capture store: m as the last chunk's
     // fold leaves it.
+    const int c = count - 1 - seg0;
     if (f.store_stats && t == 0 && dim0 == 0 && row == (int)step->tokens - 1) {
-      const Fold g = fold_factors(lb[count - 1] != 0, mb[count - 1], st[count - 1].z != 0.0f,
-                                  st[count - 1].x);
+      const Fold g = fold_factors(lb[c] != 0, mb[c], st[c].z != 0.0f, st[c].x);
       f.store_stats[2 * h] = g.m;
       f.store_stats[2 * h + 1] = l;
     }
@@ -210,7 +234,8 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
 template <int kFoldDims>
 hipError_t launch_fold(hipStream_t s, const DevStep* step, const FoldArgs& f, int max_tokens) {
   // po, st, rec, mb, lb for the chunk count padded to a batch.
-  const size_t lds = (size_t)fold_padded(f.max_chunks) * (kFoldDims * 4 + 16 + 16 + 4 + 4);
+  const size_t lds =
+      (size_t)fold_padded(min(f.max_chunks, kFoldSegment)) * (kFoldDims * 4 + 16 + 16 + 4 + 4);
   hipLaunchKernelGGL(attention_fold_kernel<kFoldDims>, dim3(QH * (D / kFoldDims), max_tokens),
                      dim3(kThreads), lds, s, step, f);
   return hipGetLastError();
@@ -218,7 +243,7 @@ hipError_t launch_fold(hipStream_t s, const DevStep* step, const FoldArgs& f, in
 
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens) {
-  if (f.max_chunks <= 0 || f.max_chunks > kMaxFoldChunks) return hipErrorInvalidValue;
+  if (f.max_chunks <= 0 || f.max_chunks > kMaxContextChunks) return hipErrorInvalidValue;
   return max_tokens <= 16 ? launch_fold<16>(s, step, f, max_tokens)
                           : launch_fold<64>(s, step, f, max_tokens);
 }

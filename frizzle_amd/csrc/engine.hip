@@ -139,6 +139,12 @@ struct frz_model {
   std::vector<frz_capture_slots> slots;
   float *ro_normed = nullptr, *ro_logits = nullptr;
   uint32_t* ro_scratch = nullptr;
+  // A model created from a plan: its planned buffers (each one allocation,
+  // also listed in `owned`), whether the capture store is the plan's.
+  bool is_planned = false;
+  bool planned_store = false;
+  std::vector<void*> planned;
+  std::vector<uint64_t> planned_bytes;
 };
 
 namespace {
@@ -183,6 +189,11 @@ void forget_prefix(frz_model* m) {
 // and captured again at the next decode).
 int reformat(frz_model* m, QMatrix* w, int format) {
   if (w->format == format) return FRZ_OK;
+  if (m->is_planned) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: the plan placed this tensor in format " +
+                                      std::to_string(w->format) + ", not " +
+                                      std::to_string(format));
+  }
   if (int rc = check_hip(hipDeviceSynchronize(), "reformat sync")) return rc;
   QMatrix fresh;
   if (int rc = alloc_q4(m, &fresh, w->rows, w->cols, format)) return rc;
@@ -600,6 +611,240 @@ uint32_t first_edit_difference(const frz_model_config& c, const std::vector<uint
   return least;
 }
 
+// A planned range's device address.
+template <typename T>
+T* planned_at(frz_model* m, const frz_range& r) {
+  return reinterpret_cast<T*>(static_cast<uint8_t*>(m->planned[r.buffer]) + r.offset);
+}
+
+// A weight tensor of the plan as one piece: its address and GGUF format.
+int planned_tensor(frz_model* m, const frz_plan* plan, int layer, int role, uint8_t** at,
+                   uint32_t* format, uint64_t want_bytes) {
+  uint64_t tensor = 0;
+  uint32_t pieces = 0;
+  if (frz_plan_role(plan, layer, role, &tensor) != FRZ_OK ||
+      frz_plan_tensor(plan, tensor, 0, nullptr, &pieces) != FRZ_OK) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: the plan has no tensor for layer " +
+                                      std::to_string(layer) + " role " + std::to_string(role));
+  }
+  frz_piece piece;
+  if (pieces != 1 || frz_plan_tensor(plan, tensor, 0, &piece, nullptr) != FRZ_OK) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: tensor " + std::to_string(tensor) +
+                                      " is in " + std::to_string(pieces) +
+                                      " pieces; this backend runs each weight as one");
+  }
+  (void)frz_plan_format(plan, tensor, format);
+  if (piece.range.length < want_bytes) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: tensor " + std::to_string(tensor) +
+                                      "'s range is shorter than its role needs");
+  }
+  *at = planned_at<uint8_t>(m, piece.range);
+  return FRZ_OK;
+}
+
+// A working buffer: the plan's of that purpose when it is at least as large,
+// else the backend's own.
+template <typename T>
+int working_buffer(frz_model* m, const frz_plan* plan, T** p, const char* purpose, size_t bytes) {
+  frz_range r;
+  if (plan && frz_plan_scratch(plan, purpose, &r) == FRZ_OK && r.length >= bytes) {
+    *p = planned_at<T>(m, r);
+    return FRZ_OK;
+  }
+  return alloc(m, p, bytes);
+}
+
+// A matrix in the device layout at `at`: its codes, then its scales.
+QMatrix matrix_at(uint8_t* at, int rows, int cols, int format) {
+  const size_t blocks = (size_t)rows * cols / 32;
+  return QMatrix{at, reinterpret_cast<const uint16_t*>(at + blocks * code_bytes(format)), rows,
+                 cols, format};
+}
+
+// Builds a model: from a plan (its buffers, weights, caches and the working
+// buffers it names), or with every buffer its own allocation.
+int create_model(frz_device* dev, const frz_model_config& c, const frz_plan* plan,
+                 frz_model** out) {
+  // The kernels are built for Gemma-3's attention shape (d = 256, four query
+  // heads on one key-value head), rows the norm prologues take (hidden at most
+  // 2,048) and contexts up to the trained 32,768 tokens. A sliding ring holds
+  // a window and a prefill block, or every position the context has.
+  const int least_ring = std::min(c.window + kPrefillBlock, c.context);
+  if (c.head_dim != 256 || c.query_heads != 4 || c.kv_heads != 1 || c.hidden % 32 != 0 ||
+      c.ffn % 32 != 0 || c.vocab < kCandidates || c.layers <= 0 || c.pattern <= 0 ||
+      c.window <= 0 || c.context < kPrefillBlock || c.local_slots < least_ring ||
+      c.hidden > 2048 || attention_max_chunks(c.context, c.context) > kMaxContextChunks) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_create: unsupported shape");
+  }
+  if (plan && c.hidden != 1152) {
+    return fail(FRZ_ERR_ARGUMENT,
+                "frz_model_create_planned: the grouped Q/K/V product runs at K = 1,152 only");
+  }
+  (void)hipSetDevice(dev->ordinal);
+  frz_model* m = new frz_model();
+  m->dev = dev;
+  m->c = c;
+  auto bail = [m](int rc) {
+    frz_model_destroy(m);
+    return rc;
+  };
+  if (plan) {
+    frz_plan_summary sum;
+    if (int rc = frz_plan_summarize(plan, &sum)) return bail(rc);
+    m->planned.assign(sum.buffers, nullptr);
+    m->planned_bytes.assign(sum.buffers, 0);
+    for (uint32_t i = 0; i < sum.buffers; ++i) {
+      int pool = 0;
+      if (int rc = frz_plan_buffer(plan, i, &pool, &m->planned_bytes[i])) return bail(rc);
+      if (int rc = alloc(m, &m->planned[i], m->planned_bytes[i])) return bail(rc);
+    }
+  }
+  const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
+  size_t max_partials = 0;
+  m->layers.resize(c.layers);
+  for (int l = 0; l < c.layers; ++l) {
+    Layer& L = m->layers[l];
+    if (plan) {
+      uint8_t *q, *k, *v, *o, *gate, *up, *down;
+      uint32_t fq, fk, fv, fo, fg, fu, fd;
+      const uint64_t qb = (uint64_t)qw * c.hidden / 32 * 18, kb = (uint64_t)kvw * c.hidden / 32 * 18;
+      const uint64_t ob = (uint64_t)c.hidden * qw / 32 * 18, fb = (uint64_t)c.ffn * c.hidden / 32 * 18;
+      int rc = planned_tensor(m, plan, l, FRZ_ROLE_Q, &q, &fq, qb);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_K, &k, &fk, kb);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_V, &v, &fv, kb);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_O, &o, &fo, ob);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_GATE, &gate, &fg, fb);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_UP, &up, &fu, fb);
+      if (!rc) rc = planned_tensor(m, plan, l, FRZ_ROLE_DOWN, &down, &fd, fb);
+      if (rc) return bail(rc);
+      if (fq != kQ4_0 || fk != kQ4_0 || fv != kQ4_0 || fo != kQ4_0 || fg != kQ4_0 ||
+          fu != kQ4_0 || (fd != kQ4_0 && fd != kQ4_1 && fd != kQ8_0)) {
+        return bail(fail(FRZ_ERR_ARGUMENT,
+                         "frz_model_create_planned: layer " + std::to_string(l) +
+                             ": matrices Q4_0 (downs also Q4_1 or Q8_0)"));
+      }
+      // Q, K and V: one product over the members the plan placed apart.
+      L.qkv = matrix_at(q, qw, c.hidden, kQ4_0);
+      L.qkv.rows = qw + 2 * kvw;
+      const QMatrix km = matrix_at(k, kvw, c.hidden, kQ4_0), vm = matrix_at(v, kvw, c.hidden, kQ4_0);
+      L.qkv.split[0] = qw;
+      L.qkv.split[1] = qw + kvw;
+      L.qkv.member_codes[0] = km.codes;
+      L.qkv.member_scales[0] = km.scales;
+      L.qkv.member_codes[1] = vm.codes;
+      L.qkv.member_scales[1] = vm.scales;
+      L.o = matrix_at(o, c.hidden, qw, kQ4_0);
+      L.gate = matrix_at(gate, c.ffn, c.hidden, kQ4_0);
+      L.up = matrix_at(up, c.ffn, c.hidden, kQ4_0);
+      L.down = matrix_at(down, c.hidden, c.ffn, (int)fd);
+      for (int g = 0; g < 6; ++g) {
+        uint8_t* at;
+        uint32_t f;
+        const int role = FRZ_ROLE_ATTN_NORM + g;
+        if (int rc2 = planned_tensor(m, plan, l, role, &at, &f, (uint64_t)gain_width(c, role) * 4))
+          return bail(rc2);
+        L.gains[g] = reinterpret_cast<float*>(at);
+      }
+    } else {
+      if (int rc = alloc_q4(m, &L.qkv, qw + 2 * kvw, c.hidden)) return bail(rc);
+      if (int rc = alloc_q4(m, &L.o, c.hidden, qw)) return bail(rc);
+      if (int rc = alloc_q4(m, &L.gate, c.ffn, c.hidden)) return bail(rc);
+      if (int rc = alloc_q4(m, &L.up, c.ffn, c.hidden)) return bail(rc);
+      if (int rc = alloc_q4(m, &L.down, c.hidden, c.ffn)) return bail(rc);
+      for (int g = 0; g < 6; ++g) {
+        const int role = FRZ_ROLE_ATTN_NORM + g;
+        if (int rc = alloc(m, &L.gains[g], (size_t)gain_width(c, role) * 4)) return bail(rc);
+      }
+    }
+    const bool global = is_global(c, l);
+    L.window = global ? c.context : c.window;
+    size_t cache = 0;
+    if (plan) {
+      frz_range keys, values;
+      uint32_t slots = 0;
+      if (int rc = frz_plan_cache(plan, (uint32_t)l, &keys, &values, &slots)) return bail(rc);
+      L.slots = (int)slots;
+      cache = (size_t)L.slots * kvw * 2;
+      if (keys.length < cache || values.length < cache || L.slots < std::min(L.window + kPrefillBlock, c.context))
+        return bail(fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: layer " +
+                                               std::to_string(l) + "'s cache is too small"));
+      L.kcache = planned_at<uint16_t>(m, keys);
+      L.vcache = planned_at<uint16_t>(m, values);
+    } else {
+      L.slots = global ? c.context : c.local_slots;
+      cache = (size_t)L.slots * kvw * 2;
+      if (int rc = alloc(m, &L.kcache, cache)) return bail(rc);
+      if (int rc = alloc(m, &L.vcache, cache)) return bail(rc);
+    }
+    L.max_chunks = attention_max_chunks(L.window, L.slots);
+    max_partials = std::max(max_partials, (size_t)kPrefillBlock * L.max_chunks * qw);
+    (void)hipMemsetAsync(L.kcache, 0, cache, dev->stream);
+    (void)hipMemsetAsync(L.vcache, 0, cache, dev->stream);
+    std::vector<float> turns(c.head_dim / 2);
+    frz_rope_turns(global ? c.rope_global : c.rope_local, c.head_dim, turns.data());
+    if (int rc = alloc(m, &L.turns, turns.size() * 4)) return bail(rc);
+    (void)hipMemcpy(L.turns, turns.data(), turns.size() * 4, hipMemcpyHostToDevice);
+  }
+  if (plan) {
+    uint8_t *emb, *norm;
+    uint32_t fe, fn;
+    if (int rc = planned_tensor(m, plan, -1, FRZ_ROLE_EMBEDDING, &emb, &fe,
+                                (uint64_t)c.vocab * c.hidden / 32 * 18))
+      return bail(rc);
+    if (int rc = planned_tensor(m, plan, -1, FRZ_ROLE_OUTPUT_NORM, &norm, &fn, (uint64_t)c.hidden * 4))
+      return bail(rc);
+    if (fe != kQ4_0 && fe != kQ8_0)
+      return bail(fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: the embedding is Q4_0 or Q8_0"));
+    m->embedding = matrix_at(emb, c.vocab, c.hidden, (int)fe);
+    m->output_norm = reinterpret_cast<float*>(norm);
+  } else {
+    if (int rc = alloc_q4(m, &m->embedding, c.vocab, c.hidden)) return bail(rc);
+    if (int rc = alloc(m, &m->output_norm, (size_t)c.hidden * 4)) return bail(rc);
+  }
+  const size_t B = kPrefillBlock;
+  m->partial_floats = max_partials;
+  auto working = [&](auto** p, const char* purpose, size_t bytes) {
+    return working_buffer(m, plan, p, purpose, bytes);
+  };
+  if (int rc = working(&m->hidden, "hidden", B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->hidden_b, (size_t)c.hidden * 4)) return bail(rc);
+  if (int rc = working(&m->normed, "normed", B * c.hidden * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->qkv, B * (qw + 2 * kvw) * 4)) return bail(rc);
+  if (int rc = working(&m->attn, "attention", B * qw * 4)) return bail(rc);
+  if (int rc = working(&m->output, "output", B * c.hidden * 4)) return bail(rc);
+  if (int rc = working(&m->act, "activation", B * c.ffn * 4)) return bail(rc);
+  if (int rc = working(&m->logits, "logits", (size_t)c.vocab * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->topk_scratch, topk_scratch_words(c.vocab) * 4)) return bail(rc);
+  if (int rc = working(&m->candidates, "candidates", 2 * kCandidates * 4)) return bail(rc);
+  if (int rc = working(&m->sampled, "sampled", 4 * 4)) return bail(rc);
+  m->token_log_capacity = 1u << 16;
+  if (int rc = alloc(m, &m->token_log, (size_t)2 * m->token_log_capacity * 4)) return bail(rc);
+  const size_t edit_words = 2 * (size_t)c.layers + 5 * (size_t)kMaxEdits;
+  if (int rc = working(&m->edits, "edit_table", edit_words * 4)) return bail(rc);
+  (void)hipMemsetAsync(m->edits, 0, edit_words * 4, dev->stream);
+  (void)hipMemsetAsync(m->sampled, 0, 16, dev->stream);
+  (void)hipMemsetAsync(m->output, 0, B * c.hidden * 4, dev->stream);
+  if (plan) {
+    // The capture store is the plan's "captures" buffer when it holds it.
+    frz_range r;
+    const uint64_t words = frz_capture_words(&c, nullptr);
+    if (frz_plan_scratch(plan, "captures", &r) == FRZ_OK && words != 0 && r.length >= words * 4) {
+      m->store = planned_at<float>(m, r);
+      m->planned_store = true;
+    }
+  }
+  if (int rc = alloc(m, &m->step, sizeof(DevStep))) return bail(rc);
+  if (int rc = check_hip(hipHostMalloc((void**)&m->step_host, sizeof(DevStep)), "hipHostMalloc"))
+    return bail(rc);
+  std::memset(m->step_host, 0, sizeof(DevStep));
+  m->edit_words.assign(2 * c.layers, 0);
+  m->is_planned = plan != nullptr;
+  if (int rc = check_hip(hipStreamSynchronize(dev->stream), "create sync")) return bail(rc);
+  *out = m;
+  return FRZ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -664,83 +909,29 @@ int frz_synth_tensor(const frz_model_config* config, uint64_t seed, int layer, i
 
 int frz_model_create(frz_device* dev, const frz_model_config* config, frz_model** out) {
   if (!dev || !config || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_create: null argument");
-  const frz_model_config& c = *config;
-  // The kernels are built for Gemma-3's attention shape (d = 256, four query
-  // heads on one key-value head), rows the norm prologues take (hidden at most
-  // 2,048) and contexts whose chunk states the fold stages at once.
-  if (c.head_dim != 256 || c.query_heads != 4 || c.kv_heads != 1 || c.hidden % 32 != 0 ||
-      c.ffn % 32 != 0 || c.vocab < kCandidates || c.layers <= 0 || c.pattern <= 0 ||
-      c.window <= 0 || c.context < kPrefillBlock || c.local_slots < c.window + kPrefillBlock ||
-      c.hidden > 2048 || attention_max_chunks(c.context, c.context) > kMaxFoldChunks) {
-    return fail(FRZ_ERR_ARGUMENT, "frz_model_create: unsupported shape");
-  }
-  (void)hipSetDevice(dev->ordinal);
-  frz_model* m = new frz_model();
-  m->dev = dev;
-  m->c = c;
-  auto bail = [m](int rc) {
-    frz_model_destroy(m);
-    return rc;
-  };
-  const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
-  size_t max_partials = 0;
-  m->layers.resize(c.layers);
-  for (int l = 0; l < c.layers; ++l) {
-    Layer& L = m->layers[l];
-    if (int rc = alloc_q4(m, &L.qkv, qw + 2 * kvw, c.hidden)) return bail(rc);
-    if (int rc = alloc_q4(m, &L.o, c.hidden, qw)) return bail(rc);
-    if (int rc = alloc_q4(m, &L.gate, c.ffn, c.hidden)) return bail(rc);
-    if (int rc = alloc_q4(m, &L.up, c.ffn, c.hidden)) return bail(rc);
-    if (int rc = alloc_q4(m, &L.down, c.hidden, c.ffn)) return bail(rc);
-    for (int g = 0; g < 6; ++g) {
-      const int role = FRZ_ROLE_ATTN_NORM + g;
-      if (int rc = alloc(m, &L.gains[g], (size_t)gain_width(c, role) * 4)) return bail(rc);
-    }
-    const bool global = is_global(c, l);
-    L.slots = global ? c.context : c.local_slots;
-    L.window = global ? c.context : c.window;
-    L.max_chunks = attention_max_chunks(L.window, L.slots);
-    max_partials = std::max(max_partials, (size_t)kPrefillBlock * L.max_chunks * qw);
-    const size_t cache = (size_t)L.slots * kvw * 2;
-    if (int rc = alloc(m, &L.kcache, cache)) return bail(rc);
-    if (int rc = alloc(m, &L.vcache, cache)) return bail(rc);
-    (void)hipMemsetAsync(L.kcache, 0, cache, dev->stream);
-    (void)hipMemsetAsync(L.vcache, 0, cache, dev->stream);
-    std::vector<float> turns(c.head_dim / 2);
-    frz_rope_turns(global ? c.rope_global : c.rope_local, c.head_dim, turns.data());
-    if (int rc = alloc(m, &L.turns, turns.size() * 4)) return bail(rc);
-    (void)hipMemcpy(L.turns, turns.data(), turns.size() * 4, hipMemcpyHostToDevice);
-  }
-  if (int rc = alloc_q4(m, &m->embedding, c.vocab, c.hidden)) return bail(rc);
-  if (int rc = alloc(m, &m->output_norm, (size_t)c.hidden * 4)) return bail(rc);
-  const size_t B = kPrefillBlock;
-  m->partial_floats = max_partials;
-  if (int rc = alloc(m, &m->hidden, B * c.hidden * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->hidden_b, (size_t)c.hidden * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->normed, B * c.hidden * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->qkv, B * (qw + 2 * kvw) * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->attn, B * qw * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->output, B * c.hidden * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->act, B * c.ffn * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->logits, (size_t)c.vocab * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->topk_scratch, topk_scratch_words(c.vocab) * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->candidates, 2 * kCandidates * 4)) return bail(rc);
-  if (int rc = alloc(m, &m->sampled, 4 * 4)) return bail(rc);
-  m->token_log_capacity = 1u << 16;
-  if (int rc = alloc(m, &m->token_log, (size_t)2 * m->token_log_capacity * 4)) return bail(rc);
-  const size_t edit_words = 2 * (size_t)c.layers + 5 * (size_t)kMaxEdits;
-  if (int rc = alloc(m, &m->edits, edit_words * 4)) return bail(rc);
-  (void)hipMemsetAsync(m->edits, 0, edit_words * 4, dev->stream);
-  (void)hipMemsetAsync(m->sampled, 0, 16, dev->stream);
-  (void)hipMemsetAsync(m->output, 0, B * c.hidden * 4, dev->stream);
-  if (int rc = alloc(m, &m->step, sizeof(DevStep))) return bail(rc);
-  if (int rc = check_hip(hipHostMalloc((void**)&m->step_host, sizeof(DevStep)), "hipHostMalloc"))
-    return bail(rc);
-  std::memset(m->step_host, 0, sizeof(DevStep));
-  m->edit_words.assign(2 * c.layers, 0);
-  if (int rc = check_hip(hipStreamSynchronize(dev->stream), "create sync")) return bail(rc);
-  *out = m;
+  return create_model(dev, *config, nullptr, out);
+}
+
+int frz_model_create_planned(frz_device* dev, const frz_plan* plan, frz_model** out) {
+  if (!dev || !plan || !out) return fail(FRZ_ERR_ARGUMENT, "frz_model_create_planned: null argument");
+  frz_model_config c;
+  if (int rc = frz_plan_config(plan, &c)) return rc;
+  return create_model(dev, c, plan, out);
+}
+
+int frz_model_planned_buffer(const frz_model* m, uint32_t index, void** dev_ptr, uint64_t* size) {
+  if (!m || index >= m->planned.size())
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_planned_buffer: no such planned buffer");
+  if (dev_ptr) *dev_ptr = m->planned[index];
+  if (size) *size = m->planned_bytes[index];
+  return FRZ_OK;
+}
+
+int frz_device_plan_limits(frz_device* dev, frz_plan_limits* out) {
+  if (!dev || !out) return fail(FRZ_ERR_ARGUMENT, "frz_device_plan_limits: null argument");
+  out->max_buffer_size = dev->props.totalGlobalMem;
+  out->max_storage_binding_size = dev->props.totalGlobalMem;
+  out->storage_offset_alignment = 256;
   return FRZ_OK;
 }
 
@@ -793,6 +984,14 @@ int frz_model_set_tensor_format(frz_model* m, int layer, int role, int format, c
     if (int rc = reformat(m, &L.down, format)) return rc;
   }
   const int qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
+  if (has_members(L.qkv) && (role == FRZ_ROLE_Q || role == FRZ_ROLE_K || role == FRZ_ROLE_V)) {
+    // Each member in its own planned range.
+    const int member = role - FRZ_ROLE_Q;
+    QMatrix w{member == 0 ? L.qkv.codes : L.qkv.member_codes[member - 1],
+              member == 0 ? L.qkv.scales : L.qkv.member_scales[member - 1],
+              member == 0 ? qw : kvw, c.hidden, kQ4_0};
+    return upload_q4(m, w, 0, w.rows, data);
+  }
   switch (role) {
     case FRZ_ROLE_Q: return upload_q4(m, L.qkv, 0, qw, data);
     case FRZ_ROLE_K: return upload_q4(m, L.qkv, qw, kvw, data);
@@ -835,14 +1034,17 @@ int frz_model_synthesize(frz_model* m, uint64_t seed) {
 int frz_model_set_capture(frz_model* m, int enabled) {
   if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_capture: null model");
   const frz_model_config& c = m->c;
-  if (enabled && !m->store) {
+  if (enabled && m->slots.empty()) {
     const uint64_t words = frz_capture_words(&c, nullptr);
     if (words == 0) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_capture: store too large");
     std::vector<frz_capture_slots> slots(c.layers);
     for (int l = 0; l < c.layers; ++l) {
       if (int rc = frz_capture_layer(&c, l, &slots[l])) return rc;
     }
-    if (int rc = alloc(m, &m->store, words * 4)) return rc;
+    // A planned model's store is the plan's "captures" buffer.
+    if (!m->store) {
+      if (int rc = alloc(m, &m->store, words * 4)) return rc;
+    }
     if (int rc = alloc(m, &m->ro_normed, (size_t)c.hidden * 4)) return rc;
     if (int rc = alloc(m, &m->ro_logits, (size_t)c.vocab * 4)) return rc;
     if (int rc = alloc(m, &m->ro_scratch, topk_scratch_words(c.vocab) * 4)) return rc;

@@ -486,10 +486,18 @@ __global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_
   Tile<NB, GATED> T;
   T.block = lane / D;
   const int row = min((int)blockIdx.x * D + lane % D, w.rows - 1);
-  const uint32_t blocks = (uint32_t)w.rows * (uint32_t)groups;
-  T.row_group0 = (uint32_t)row * (uint32_t)groups;
-  T.codes[0] = buffer_of(w.codes, (uint32_t)code_bytes(F) * blocks);
-  T.scales[0] = buffer_of(w.scales, 2u * (uint32_t)scale_halves(F) * blocks);
+  // The tile's member (a fused product over members placed apart): members
+  // split at multiples of 32 rows, so a tile lies in one.
+  const MemberRow mr = member_row(w, (int)blockIdx.x * D);
+  const int member_rows = w.split[1] != 0 && (int)blockIdx.x * D >= w.split[1] ? w.rows - w.split[1]
+                          : w.split[0] != 0 && (int)blockIdx.x * D >= w.split[0]
+                              ? (w.split[1] != 0 ? w.split[1] : w.rows) - w.split[0]
+                          : w.split[0] != 0 ? w.split[0]
+                                            : w.rows;
+  const uint32_t blocks = (uint32_t)member_rows * (uint32_t)groups;
+  T.row_group0 = (uint32_t)(row - ((int)blockIdx.x * D - mr.row)) * (uint32_t)groups;
+  T.codes[0] = buffer_of(mr.codes, (uint32_t)code_bytes(F) * blocks);
+  T.scales[0] = buffer_of(mr.scales, 2u * (uint32_t)scale_halves(F) * blocks);
   if (GATED) {
     T.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
     T.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
@@ -658,6 +666,8 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token) {
   if (w.cols % 32 != 0 || w.rows <= 0) return hipErrorInvalidValue;
+  if (has_members(w) && (w.split[0] % 32 != 0 || w.split[1] % 32 != 0 || w.format != kQ4_0))
+    return hipErrorInvalidValue;
   if (max_tokens <= 1 || last_token) {
     GemvInput in{};
     in.x = x + (size_t)(last_token ? max_tokens - 1 : 0) * x_stride;

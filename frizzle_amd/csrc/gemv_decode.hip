@@ -883,12 +883,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_pair_kernel(const DevStep* __
   const pair::Plan P = pair::plan(p);
   Prologue<T, X4> pro;
   prologue_load<MODE, T, X4>(pro, in, step, w.cols);
-  // Lanes past the rows load row 0's blocks, unused.
-  const int base = live ? row * pair::kGroups : 0;
-  const uint4 c0 = reinterpret_cast<const uint4*>(w.codes)[base + P.g0];
-  const uint16_t d0 = w.scales[base + P.g0];
-  const uint4 c1 = reinterpret_cast<const uint4*>(w.codes)[base + P.g1];
-  const uint16_t d1 = w.scales[base + P.g1];
+  // Lanes past the rows load row 0's blocks, unused. A fused product over
+  // members reads each row from its member's streams.
+  const MemberRow mr = member_row(w, live ? row : 0);
+  const int base = mr.row * pair::kGroups;
+  const uint4 c0 = reinterpret_cast<const uint4*>(mr.codes)[base + P.g0];
+  const uint16_t d0 = mr.scales[base + P.g0];
+  const uint4 c1 = reinterpret_cast<const uint4*>(mr.codes)[base + P.g1];
+  const uint16_t d1 = mr.scales[base + P.g1];
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, w.cols);
   __syncthreads();
   float s0, s1;
@@ -1185,6 +1187,10 @@ hipError_t launch_gemv_decode(hipStream_t s, const DevStep* step, const QMatrix&
     return hipErrorInvalidValue;
   }
   if (mode != 0 && w.cols > kNormMaxCols) return hipErrorInvalidValue;
+  // Members are read by the K = 1,152 pair form of fewer than 16,384 rows.
+  if (has_members(w) &&
+      (w.format != kQ4_0 || w.cols != pair::kCols || w.rows >= 16384 || mode == 3))
+    return hipErrorInvalidValue;
   if (mode == 2 && in.table.format != kQ4_0 && in.table.format != kQ8_0)
     return hipErrorInvalidValue;
   // Q4_1 and Q8_0 weights (a file's downs and tied head) take a plain row.

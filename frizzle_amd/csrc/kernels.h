@@ -55,13 +55,38 @@ constexpr int gguf_block_bytes(int format) {
 // streams, every block's code bytes in row-major block order, then every
 // block's scale halves (the reference's device layout,
 // device_layout.h:114-115).
+//
+// A fused product over members placed apart (a plan's Q, K, V group, each
+// member in its own device layout at its own offset, residency/plan.h): rows
+// from split[0] on are member 1's, rows from split[1] on member 2's, each
+// counted from its member's first row; 0 ends the list. Splits are
+// multiples of 32 rows (a prefill tile never straddles two members), and
+// only Q4_0 products over K = 1,152 take members.
 struct QMatrix {
   const uint8_t* codes;    // rows * cols / 32 blocks of code_bytes(format)
   const uint16_t* scales;  // rows * cols / 32 blocks of scale_halves(format)
   int rows;
   int cols;
   int format = kQ4_0;
+  int split[2] = {0, 0};
+  const uint8_t* member_codes[2] = {nullptr, nullptr};
+  const uint16_t* member_scales[2] = {nullptr, nullptr};
 };
+
+// Row `row`'s member: its streams and the row within them.
+struct MemberRow {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  int row;
+};
+__host__ __device__ inline MemberRow member_row(const QMatrix& w, int row) {
+  if (w.split[1] != 0 && row >= w.split[1])
+    return {w.member_codes[1], w.member_scales[1], row - w.split[1]};
+  if (w.split[0] != 0 && row >= w.split[0])
+    return {w.member_codes[0], w.member_scales[0], row - w.split[0]};
+  return {w.codes, w.scales, row};
+}
+inline bool has_members(const QMatrix& w) { return w.split[0] != 0; }
 
 // ---- products ----------------------------------------------------------
 // y[t][o] = sum_k W[o][k] x[t][k] for t < step.tokens (or only the last
@@ -218,7 +243,10 @@ struct FoldArgs {
 };
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens);
-constexpr int kMaxFoldChunks = 224;  // chunk states a fold stages in LDS: 14,272 keys
+constexpr int kMaxFoldChunks = 224;  // chunk states of the static decode workspace: 14,272 keys
+// Chunks a context may reach: Gemma 3 1B's trained 32,768 tokens, plus the
+// partial chunk a window straddles (the fold stages them in segments).
+constexpr int kMaxContextChunks = 32768 / kChunkKeys + 1;
 
 // The capture store's copies at the step that ends the prompt: the last row
 // of src (rows row_stride words apart) into dst, word for word

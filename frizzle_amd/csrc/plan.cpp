@@ -155,6 +155,7 @@ struct frz_plan {
   uint32_t context_offered = 0;
   uint64_t weight_bytes = 0, cache_bytes = 0, scratch_bytes = 0, total_bytes = 0;
   ModelDesc model;
+  std::vector<uint32_t> formats;  // each tensor's GGUF format, index order
 };
 
 namespace {
@@ -506,6 +507,7 @@ int frz_plan_gemma3(const frz_gguf* index, const frz_plan_limits* limits,
   std::string subj;
   int rc = describe(index, p->model, subj) == FRZ_OK ? FRZ_PLAN_OK : FRZ_PLAN_NOT_DESCRIBED;
   if (rc == FRZ_PLAN_OK) rc = place_weights(index->index, p->model, *limits, *p, subj);
+  for (const Tensor& t : index->index.tensors) p->formats.push_back(t.type);
   if (rc == FRZ_PLAN_OK) {
     p->weight_bytes = pool_bytes(p->buffers, FRZ_POOL_WEIGHTS);
     rc = place_scratch(p->model, *limits, *p, subj);
@@ -518,7 +520,10 @@ int frz_plan_gemma3(const frz_gguf* index, const frz_plan_limits* limits,
     p->cache_bytes = pool_bytes(p->buffers, FRZ_POOL_CACHE);
     p->total_bytes = p->weight_bytes + p->scratch_bytes + p->cache_bytes;
     p->model.config.context = (int)p->context_offered;
-    p->model.config.local_slots = (int)p->model.config.window + 512 + (int)policy->rollback_reserve;
+    // A sliding layer's ring as placed: window + 512 + reserve, or the whole
+    // context when that is shorter.
+    p->model.config.local_slots = (int)std::min<uint64_t>(
+        (uint64_t)p->model.config.window + 512 + policy->rollback_reserve, p->context_offered);
   }
   summarize(*p, summary);
   copy_subject(subj, subject, subject_cap);
@@ -531,6 +536,19 @@ int frz_plan_gemma3(const frz_gguf* index, const frz_plan_limits* limits,
 }
 
 void frz_plan_free(frz_plan* plan) { delete plan; }
+
+int frz_plan_summarize(const frz_plan* p, frz_plan_summary* out) {
+  if (!p || !out) return frz::fail(FRZ_ERR_ARGUMENT, "frz_plan_summarize: null argument");
+  summarize(*p, out);
+  return FRZ_OK;
+}
+
+int frz_plan_format(const frz_plan* p, uint64_t tensor, uint32_t* format) {
+  if (!p || !format || tensor >= p->formats.size())
+    return frz::fail(FRZ_ERR_ARGUMENT, "frz_plan_format: index");
+  *format = p->formats[tensor];
+  return FRZ_OK;
+}
 
 const char* frz_plan_error_text(int error) {
   switch (error) {

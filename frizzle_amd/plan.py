@@ -50,6 +50,13 @@ def limits(max_buffer_size, max_storage_binding_size, storage_offset_alignment=2
     return PlanLimits(max_buffer_size, max_storage_binding_size, storage_offset_alignment)
 
 
+def device_limits(device):
+    """The limits this device grants a plan (frz_device_plan_limits)."""
+    lim = PlanLimits()
+    check(load().frz_device_plan_limits(device.handle, ctypes.byref(lim)))
+    return lim
+
+
 def _summary(s):
     return {n: getattr(s, n) for n, _ in s._fields_}
 

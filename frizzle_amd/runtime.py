@@ -246,6 +246,19 @@ class Model:
         check(self.lib.frz_model_create(device.handle, byref(cfg), byref(h)))
         self.handle = h.value
 
+    @classmethod
+    def planned(cls, device, plan):
+        """A model created from a residency plan (frz_model_create_planned):
+        its buffers the plan's, its context the one the plan offered."""
+        self = cls.__new__(cls)
+        self.device = device
+        self.lib = device.lib
+        self.cfg = plan.config()
+        h = c_void_p()
+        check(self.lib.frz_model_create_planned(device.handle, plan._h, byref(h)))
+        self.handle = h.value
+        return self
+
     def set_tensor(self, layer, role, data, fmt=None):
         """A role's tensor as GGUF bytes; fmt a GGUF format number (Q4_1 or
         Q8_0 where the role takes one), else the role's Q4_0 or F32."""

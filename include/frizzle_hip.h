@@ -682,6 +682,9 @@ int frz_plan_gemma3(const frz_gguf* index, const frz_plan_limits* limits,
                     frz_plan_summary* summary, char* subject, size_t subject_cap);
 void frz_plan_free(frz_plan* plan);
 const char* frz_plan_error_text(int error);
+int frz_plan_summarize(const frz_plan* plan, frz_plan_summary* out);
+/* A tensor's GGUF format as the plan placed it. */
+int frz_plan_format(const frz_plan* plan, uint64_t tensor, uint32_t* format);
 /* The model's shapes, its context the context offered and its sliding
  * rings the plan's. */
 int frz_plan_config(const frz_plan* plan, frz_model_config* out);
@@ -700,6 +703,28 @@ int frz_plan_scratch(const frz_plan* plan, const char* purpose, frz_range* out);
 /* The tensor index of a layer's role (layer -1: the embedding or the
  * output norm). */
 int frz_plan_role(const frz_plan* plan, int layer, int role, uint64_t* tensor);
+/* Limits this device grants a plan: buffers and bindings as large as its
+ * memory, ranges aligned to 256 bytes (every tensor stays in one piece). */
+int frz_device_plan_limits(frz_device* dev, frz_plan_limits* out);
+/* A model created from a plan (replaces Engine::begin_load's Upload::begin
+ * over the plan, src/core/runtime/engine.cpp:575, upload.h:276): one
+ * allocation for each planned buffer; every weight, norm gain and layer
+ * cache at its planned range, in the device layout (a layer's Q, K and V
+ * read as one product over the three members the plan grouped); the
+ * context the plan offered and its rings. The working buffers the plan
+ * names that this backend reads as they are (hidden, normed, attention,
+ * output, activation, logits, candidates, sampled, edit_table, captures)
+ * are the planned ones; the backend's own (the fused Q/K/V rows, a second
+ * hidden row, the attention partials of every chunk, the selection's
+ * scratch, the token log) are allocated beside them. Every weight must be
+ * one piece (frz_device_plan_limits keeps them so), Q, K and V Q4_0 with
+ * K = 1,152. Tensors are then set as for any model (frz_model_set_tensor*,
+ * frz_model_load_gguf), each in the format the plan placed it in. */
+int frz_model_create_planned(frz_device* dev, const frz_plan* plan, frz_model** out);
+/* The planned buffer `index` of a model created from a plan: its device
+ * address and size (for a caller that writes a tensor's bytes itself). */
+int frz_model_planned_buffer(const frz_model* model, uint32_t index, void** dev_ptr,
+                             uint64_t* size);
 
 #ifdef __cplusplus
 }

@@ -384,7 +384,9 @@ def test_rope_bit_exact(device, base, position):
 
 @pytest.mark.parametrize("position,tokens,window,slots", [
     (0, 1, 512, 5120), (700, 1, 512, 640), (5000, 1, 512, 5120), (100, 4, 512, 5120),
-    (1000, 1, 4096, 4096), (4095, 1, 32768, 8192), (63, 2, 512, 5120)])
+    (1000, 1, 4096, 4096), (4095, 1, 32768, 8192), (63, 2, 512, 5120),
+    # past the 224 chunk states one fold stage holds: folded in segments
+    (20000, 3, 32768, 32768), (32767, 1, 32768, 32768), (14400, 1, 14400, 16384)])
 def test_attention_bit_exact(device, position, tokens, window, slots):
     rng = np.random.default_rng(position + tokens)
     qh, kvh, d = 4, 1, 256
@@ -504,7 +506,8 @@ def test_draw_matches_oracle(device, temperature, top_k, top_p, min_p):
 
 @pytest.mark.parametrize("position,window,slots,base", [
     (0, 512, 5120, 1e4), (63, 512, 5120, 1e4), (64, 512, 5120, 1e4), (700, 512, 640, 1e4),
-    (5000, 512, 5120, 1e4), (4100, 8192, 8192, 1e6), (1000, 64, 640, 1e4)])
+    (5000, 512, 5120, 1e4), (4100, 8192, 8192, 1e6), (1000, 64, 640, 1e4),
+    (30000, 32768, 32768, 1e6), (14336, 32768, 32768, 1e6)])
 def test_rope_attention_decode_bit_exact(device, position, window, slots, base):
     # The decode kernel fuses QK-norm, rope, the KV append and attention; its
     # query, cache slot and output are the separate kernels' bits.

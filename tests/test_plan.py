@@ -243,6 +243,11 @@ def test_rollback_reserve_sizes_the_sliding_rings(index):
     assert cfg.local_slots == 1024 and cfg.context == 32768 and cfg.window == 512
 
 
+def test_rings_are_cut_to_a_shorter_context():
+    p = fp.Plan(pinned_index(trained=2048), webgpu())
+    assert p.config().local_slots == 2048 == p.cache(0)[2]
+
+
 def test_row_wider_than_a_binding_is_refused_by_name(index):
     # The embedding's Q8_0 row is 1,224 bytes: a 1,024-byte binding cannot
     # hold it, and it comes first in file order.
