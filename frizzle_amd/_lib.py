@@ -225,6 +225,15 @@ _SIGS = {
     "frz_device_plan_limits": (c_int, [_P, POINTER(PlanLimits)]),
     "frz_model_create_planned": (c_int, [_P, _P, POINTER(c_void_p)]),
     "frz_model_planned_buffer": (c_int, [_P, c_uint32, POINTER(c_void_p), POINTER(c_uint64)]),
+    "frz_program_check": (c_int, [_P, _P, c_uint32, _P, _P, ctypes.c_size_t]),
+    "frz_program_build": (c_int, [_P, _P, _P, c_uint32, _P, POINTER(c_void_p), _P,
+                                  ctypes.c_size_t]),
+    "frz_program_run": (c_int, [_P, _P, _P, c_uint32, _P, _P]),
+    "frz_poll": (c_int, [_P, c_int]),
+    "frz_program_outstanding": (c_uint32, [_P]),
+    "frz_program_cancel": (c_int, [_P]),
+    "frz_program_destroy": (None, [_P]),
+    "frz_program_mark_lost": (c_int, [_P]),
 }
 
 _lib = None

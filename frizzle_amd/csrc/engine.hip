@@ -1311,6 +1311,46 @@ int frz_model_read_cache(frz_model* m, int layer, int values, uint16_t* out, uin
   return read_back(m, out, values ? L.vcache : L.kcache, count * 2);
 }
 
+}  // extern "C"
+
+namespace frz {
+
+// One step of a program's run (program.hip): the step record, already in
+// pinned memory, is copied to the device in stream order; a fed decode step
+// of one token with logits replays the decode graph (its launches one by
+// one when graphs are off), any other step runs the rows path; a step with
+// logits then copies the draw's 16-byte record to `readback` (pinned). The
+// caches are rewritten, so generation's prompt-reuse record is forgotten.
+int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback) {
+  hipStream_t s = m->dev->stream;
+  forget_prefix(m);
+  const DevStep& st = *pinned_step;
+  const bool decode = st.tokens == 1 && st.fed != 0 && st.logits != 0 && !st.variants;
+  if (decode && m->use_graphs) {
+    if (int rc = build_decode_graph(m)) return rc;
+  }
+  if (int rc = check_hip(hipMemcpyAsync(m->step, pinned_step, sizeof(DevStep),
+                                        hipMemcpyHostToDevice, s),
+                         "program step record"))
+    return rc;
+  if (decode) {
+    if (int rc = launch_decode_step(m)) return rc;
+  } else {
+    if (int rc = enqueue_step(m, (int)st.tokens, st.logits != 0, false)) return rc;
+  }
+  if (st.logits != 0 && readback) {
+    return check_hip(hipMemcpyAsync(readback, m->sampled, 16, hipMemcpyDeviceToHost, s),
+                     "program readback");
+  }
+  return FRZ_OK;
+}
+
+hipStream_t model_stream(const frz_model* m) { return m->dev->stream; }
+
+}  // namespace frz
+
+extern "C" {
+
 int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
                  const uint32_t* edit_table, uint32_t edit_words, const frz_sampling* sampling,
                  uint32_t max_tokens, const uint32_t* stop_ids, uint32_t stops,

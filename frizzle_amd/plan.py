@@ -144,6 +144,11 @@ class Plan:
         check(self._lib.frz_plan_scratch(self._h, purpose.encode(), ctypes.byref(r)))
         return (r.buffer, r.offset, r.length)
 
+    def format(self, tensor):
+        f = ctypes.c_uint32()
+        check(self._lib.frz_plan_format(self._h, tensor, ctypes.byref(f)))
+        return f.value
+
     def role(self, layer, role):
         from ._lib import ROLE
         t = ctypes.c_uint64()

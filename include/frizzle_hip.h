@@ -726,6 +726,131 @@ int frz_model_create_planned(frz_device* dev, const frz_plan* plan, frz_model** 
 int frz_model_planned_buffer(const frz_model* model, uint32_t index, void** dev_ptr,
                              uint64_t* size);
 
+/* ---- the program (replaces kernels::Program, src/core/kernels/program.h:
+ *      264-402, over kernels::Launch, interface.h:320-363, reported in order
+ *      as kernels::Order does, order.h:68-104) ------------------------------
+ * A graph's launches, as graph::Builder emits them for Gemma 3
+ * (src/core/graph/graph.cpp:290-470), each described as the reference's
+ * Launch with its WGSL named by a kernel number instead of its text. The
+ * program recognises the Gemma 3 graph in them (every stage in the graph's
+ * order, named by its role and layer as graph.h names them, and bound to
+ * the plan's tensors, caches and working buffers) and runs each step
+ * through this backend's fused kernels; anything else is refused, Build,
+ * naming the launch. */
+enum frz_kernel {
+  FRZ_KERNEL_GATHER = 0,            /* kernels/gather/gather.wgsl */
+  FRZ_KERNEL_NORM = 1,              /* kernels/norm/norm.wgsl */
+  FRZ_KERNEL_MATMUL = 2,            /* kernels/matmul/matmul.wgsl, any entry point */
+  FRZ_KERNEL_ROPE = 3,              /* kernels/rope/rope.wgsl with rope_cache.wgsl */
+  FRZ_KERNEL_ATTENTION = 4,         /* kernels/attention/attention.wgsl main */
+  FRZ_KERNEL_ATTENTION_COMBINE = 5, /* attention.wgsl combine */
+  FRZ_KERNEL_EDIT = 6,              /* edit/edit.wgsl */
+  FRZ_KERNEL_TOPK = 7,              /* kernels/topk/topk.wgsl, either pass */
+  FRZ_KERNEL_DRAW = 8,              /* sampler/draw.wgsl */
+  FRZ_KERNEL_CAPTURE = 9,           /* capture/capture.wgsl: a copy or a readout */
+  FRZ_KERNEL_CAPTURE_WEIGHTS = 10   /* capture/weights.wgsl */
+};
+enum frz_rows { FRZ_ROWS_EVERY_TOKEN = 0, FRZ_ROWS_LAST_TOKEN = 1, FRZ_ROWS_PROMPT_END = 2 };
+enum frz_key_split {
+  FRZ_KEY_SPLIT_NONE = 0,
+  FRZ_KEY_SPLIT_PER_CHUNK = 1,
+  FRZ_KEY_SPLIT_WHEN_SPLIT = 2
+};
+#define FRZ_NO_LAYER 0xFFFFFFFFu
+/* A bound range of one of the plan's buffers (kernels::Binding). */
+typedef struct frz_binding {
+  uint32_t buffer;
+  uint64_t offset;
+  uint64_t size;
+} frz_binding;
+/* kernels::Launch. `role` and `layer` are the graph's names (graph.h). */
+typedef struct frz_launch {
+  int kernel;              /* frz_kernel */
+  const char* entry_point; /* the WGSL entry point, or null for "main" */
+  int format;              /* GGUF format of the weights it unpacks, or -1 */
+  int pack_format;         /* the format it packs (the cache's), or -1 */
+  const void* constants;
+  uint32_t constants_bytes; /* at most 768 */
+  const frz_binding* bindings;
+  uint32_t binding_count;
+  uint32_t invocations_per_row;
+  uint32_t workgroup_size;
+  int rows;                /* frz_rows */
+  uint32_t rows_per_tile;  /* 0: a launch over rows */
+  int key_split;           /* frz_key_split */
+  uint32_t window;
+  uint32_t partial_rows;
+  uint32_t tokens_least, tokens_most; /* the steps it runs in, by token count */
+  const char* role;
+  uint32_t layer;          /* FRZ_NO_LAYER for the embedding and the output */
+} frz_launch;
+/* kernels::Step: the 64-byte head (sampler::apply's settings and seed) and
+ * the step's token ids. */
+typedef struct frz_step_record {
+  uint32_t position;
+  uint32_t tokens;     /* 1 .. 512 */
+  uint32_t logits;     /* 1: the last token's logits are drawn from */
+  uint32_t fed;        /* 1: one token, the last step's draw */
+  uint32_t seed[2];
+  uint32_t top_k;
+  float temperature;
+  float top_p;
+  float min_p;
+  float log_min_p;
+  uint32_t padding[5];
+  uint32_t ids[512];
+} frz_step_record;
+/* kernels::RunInput: bytes written into a range of one of the plan's
+ * buffers before the step (to.size bytes from `bytes`). */
+typedef struct frz_run_input {
+  frz_binding to;
+  const void* bytes;
+} frz_run_input;
+/* kernels::StepCallback: `readback` (the draw's 16-byte record for a step
+ * that asked for logits) and `message` are valid only during the call. */
+typedef void (*frz_step_callback)(int status, const char* message, const void* readback,
+                                  uint32_t readback_bytes, void* userdata);
+typedef struct frz_program frz_program;
+
+/* The build's checks without a device (Program::build's refusals,
+ * program.h:29-41, then the Gemma 3 graph's recognition): FRZ_OK, or
+ * FRZ_ERR_BUILD with the message naming the launch. Pure. */
+int frz_program_check(const frz_plan* plan, const frz_launch* launches, uint32_t count,
+                      const frz_binding* readback, char* message, size_t message_cap);
+/* Program::build over a model created from `plan` (the upload whose buffers
+ * the bindings index; it must outlive the program). The program turns the
+ * model's capture store on, as the graph's capture launches write it. */
+int frz_program_build(frz_model* upload, const frz_plan* plan, const frz_launch* launches,
+                      uint32_t count, const frz_binding* readback, frz_program** out,
+                      char* message, size_t message_cap);
+/* Program::run: at most two steps outstanding. Refused at once, FRZ_ERR_STEP
+ * through `done` before this returns (and not numbered): a third step while
+ * two are outstanding, a step of 0 or more than 512 tokens, and any step
+ * once the device is lost (FRZ_ERR_DEVICE_LOST). Failed, FRZ_ERR_STEP, with
+ * nothing run, reported in order: a step past the context, or an input
+ * outside its buffer or not of whole words. Otherwise `done` is called by
+ * frz_poll once the step has finished. */
+int frz_program_run(frz_program* program, const frz_step_record* step,
+                    const frz_run_input* inputs, uint32_t input_count,
+                    frz_step_callback done, void* userdata);
+/* Calls the callbacks of the steps that have settled, in the order they
+ * were run (a later one waits for an earlier), on the calling thread. With
+ * `wait`, first waits for the oldest outstanding step. The number of
+ * callbacks made. */
+int frz_poll(frz_program* program, int wait);
+uint32_t frz_program_outstanding(const frz_program* program);
+/* Reports every outstanding step FRZ_ERR_CANCELLED, in run order, once the
+ * device has finished it (its results are not reported); the program stays
+ * usable (the runtime's cancel, runtime.h:49-56). */
+int frz_program_cancel(frz_program* program);
+/* Destroys the program; outstanding steps are reported FRZ_ERR_CANCELLED. */
+void frz_program_destroy(frz_program* program);
+/* A host-side stand-in for the device reporting itself lost (no device
+ * fault is made): steps settling from now on are reported
+ * FRZ_ERR_DEVICE_LOST and new ones refused so. For tests of the failure
+ * path; a real loss (a HIP error on the stream) takes the same path. */
+int frz_program_mark_lost(frz_program* program);
+
 #ifdef __cplusplus
 }
 #endif
