@@ -47,6 +47,37 @@ __device__ __forceinline__ float h2f(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// -0 in a register the compiler does not see into. fma(x, h, -0) is the
+// product x h rounded once, the sign of a zero product kept (x h + -0 is
+// x h for every x h, zeros included), and with h a half it stays one mixed
+// fma instead of a conversion and a multiply.
+__device__ __forceinline__ float negative_zero() {
+  float z;
+  asm("v_mov_b32 %0, 0x80000000" : "=v"(z));
+  return z;
+}
+
+// dot4 of q with the four halves of words w0 (low, high) and w1: each
+// product rounded, added ((p0 + p1) + p2) + p3.
+__device__ __forceinline__ float dot4_halves(float4 q, uint32_t w0, uint32_t w1, float nz) {
+  const half2v a = __builtin_bit_cast(half2v, w0), b = __builtin_bit_cast(half2v, w1);
+  const float p0 = __builtin_fmaf(q.x, (float)a.x, nz);
+  const float p1 = __builtin_fmaf(q.y, (float)a.y, nz);
+  const float p2 = __builtin_fmaf(q.z, (float)b.x, nz);
+  const float p3 = __builtin_fmaf(q.w, (float)b.y, nz);
+  return ((p0 + p1) + p2) + p3;
+}
+
+// Orders a wave's LDS accesses around it: a wave's LDS instructions execute
+// in program order; this keeps the compiler from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 struct Fold {
   float a, b, m;
 };

@@ -3,6 +3,7 @@
 // device's stream and launches one kernel family there; ops wait for their
 // work so their host arguments need not outlive the call.
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -334,8 +335,16 @@ int frz_op_rope_attention(frz_device* dev, const float* qkv, const float* turns,
                           const float* query_gain, const float* key_gain, uint16_t* key_cache,
                           uint16_t* value_cache, float* out, int slots, int window,
                           float epsilon, float scale, uint32_t position) {
-  if (window <= 0 || slots <= 0 || (int)position >= 0x7fffffff) {
-    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention: bad window or slots");
+  if (window <= 0 || slots <= 0 || slots > (1 << 21) || position >= (1u << 24)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention: bad window or slots (at most 2,097,152 slots,"
+                                  " positions under 2^24)");
+  }
+  if ((uint64_t)slots < std::min<uint64_t>((uint64_t)window, (uint64_t)position + 1) ||
+      (slots < kChunkKeys && position >= (uint32_t)slots)) {
+    // The window's keys need slots of their own (the step's key is appended
+    // while the others are read), and a chunk's rows may wrap the ring once.
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention: the ring holds fewer slots than the window's keys"
+                                  " (or, under 64 slots, than the positions)");
   }
   const int max_chunks = attention_max_chunks(window, slots);
   const size_t part_floats = (size_t)max_chunks * 4 * 256;
@@ -370,8 +379,16 @@ int frz_op_rope_attention_noalloc(frz_device* dev, const float* qkv, const float
   if (!dev || !dev->static_workspace) {
     return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: no device");
   }
-  if (window <= 0 || slots <= 0 || (int)position >= 0x7fffffff) {
-    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: bad window or slots");
+  if (window <= 0 || slots <= 0 || slots > (1 << 21) || position >= (1u << 24)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: bad window or slots (at most 2,097,152 slots,"
+                                  " positions under 2^24)");
+  }
+  if ((uint64_t)slots < std::min<uint64_t>((uint64_t)window, (uint64_t)position + 1) ||
+      (slots < kChunkKeys && position >= (uint32_t)slots)) {
+    // The window's keys need slots of their own (the step's key is appended
+    // while the others are read), and a chunk's rows may wrap the ring once.
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_rope_attention_noalloc: the ring holds fewer slots than the window's keys"
+                                  " (or, under 64 slots, than the positions)");
   }
   const int max_chunks = attention_max_chunks(window, slots);
   if (max_chunks > kStaticChunks) {

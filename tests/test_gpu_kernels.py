@@ -504,20 +504,14 @@ def test_draw_matches_oracle(device, temperature, top_k, top_p, min_p):
         assert np.array_equal(dr.numpy(), want), (trial, dr.numpy(), want)
 
 
-@pytest.mark.parametrize("position,window,slots,base", [
-    (0, 512, 5120, 1e4), (63, 512, 5120, 1e4), (64, 512, 5120, 1e4), (700, 512, 640, 1e4),
-    (5000, 512, 5120, 1e4), (4100, 8192, 8192, 1e6), (1000, 64, 640, 1e4),
-    (30000, 32768, 32768, 1e6), (14336, 32768, 32768, 1e6)])
-def test_rope_attention_decode_bit_exact(device, position, window, slots, base):
-    # The decode kernel fuses QK-norm, rope, the KV append and attention; its
-    # query, cache slot and output are the separate kernels' bits.
-    rng = np.random.default_rng(position + window)
+def _rope_attention_case(device, position, window, slots, base, kc, vc, rng):
+    """The fused decode kernel at one position over caches kc, vc (f16
+    bits): its cache slot and its output against the oracle's, the output
+    as (got, want)."""
     qh, d = 4, 256
     qkv = rng.normal(0, 2, 6 * d).astype(np.float32)
     qg = (1 + 0.1 * rng.normal(0, 1, d)).astype(np.float32)
     kg = (1 + 0.1 * rng.normal(0, 1, d)).astype(np.float32)
-    kc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16).view(np.uint16)
-    vc = (rng.integers(-96, 97, slots * d) / 32.0).astype(np.float16).view(np.uint16)
     turns = fz.rope_turns(base, d)
     dqkv, dk, dv = device.array(qkv), device.array(kc), device.array(vc)
     dt, dqg, dkg = device.array(turns), device.array(qg), device.array(kg)
@@ -538,4 +532,61 @@ def test_rope_attention_decode_bit_exact(device, position, window, slots, base):
     scale_log2e = np.float32(np.float64(np.float32(0.0625)) * 1.4426950408889634)
     orc.lib().orc_attention_row(position, window, slots, d, qh, 1, scale_log2e, q.ctypes.data,
                                 want_k.ctypes.data, want_v.ctypes.data, want.ctypes.data)
-    assert_same_bits(do.numpy(), want, "decode attention")
+    return do.numpy(), want
+
+
+@pytest.mark.parametrize("position,window,slots,base", [
+    (0, 512, 5120, 1e4), (63, 512, 5120, 1e4), (64, 512, 5120, 1e4), (700, 512, 640, 1e4),
+    (5000, 512, 5120, 1e4), (4100, 8192, 8192, 1e6), (1000, 64, 640, 1e4),
+    (30000, 32768, 32768, 1e6), (14336, 32768, 32768, 1e6), (4360, 512, 4672, 1e4),
+    (4391, 512, 4672, 1e4), (100, 64, 96, 1e4), (40, 512, 48, 1e4)])
+def test_rope_attention_decode_bit_exact(device, position, window, slots, base):
+    # The decode kernel fuses QK-norm, rope, the KV append and attention; its
+    # query, cache slot and output are the separate kernels' bits. Cases with
+    # a partial first chunk, the step's key first or last in its chunk, a
+    # ring that wraps inside a chunk, and rings under a chunk long.
+    rng = np.random.default_rng(position + window)
+    kc = (rng.integers(-96, 97, slots * 256) / 32.0).astype(np.float16).view(np.uint16)
+    vc = (rng.integers(-96, 97, slots * 256) / 32.0).astype(np.float16).view(np.uint16)
+    got, want = _rope_attention_case(device, position, window, slots, base, kc, vc, rng)
+    assert_same_bits(got, want, "decode attention")
+
+
+def test_rope_attention_decode_subnormal_and_nonfinite_rows(device):
+    # f16 subnormals in the cache enter the products exactly; a value row the
+    # token does not see but whose tile it scores (the first tile's keys
+    # before the window) still multiplies its weight 0: an infinity there
+    # makes its dimension NaN, as in the reference.
+    position, window, slots = 5000, 512, 5120
+    rng = np.random.default_rng(7)
+    kc = (rng.integers(-96, 97, slots * 256) / 32.0).astype(np.float16)
+    vc = (rng.integers(-96, 97, slots * 256) / 32.0).astype(np.float16)
+    sub = rng.integers(1, 1024, slots * 256).astype(np.uint16)  # subnormal bit patterns
+    pick = rng.random(slots * 256) < 0.3
+    kc = kc.view(np.uint16).copy()
+    vc = vc.view(np.uint16).copy()
+    kc[pick] = sub[pick] | (rng.integers(0, 2, pick.sum()).astype(np.uint16) << 15)
+    vc[pick] = sub[pick]
+    got, want = _rope_attention_case(device, position, window, slots, 1e4, kc, vc, rng)
+    assert_same_bits(got, want, "decode attention, subnormal cache")
+    earliest = position + 1 - window
+    first = earliest // 8 * 8
+    assert first < earliest  # a key the token does not see, in a scored tile
+    vc[first * 256 + 17] = 0x7C00  # +inf
+    got, want = _rope_attention_case(device, position, window, slots, 1e4, kc, vc,
+                                     np.random.default_rng(8))
+    assert np.isnan(want[17::256]).all() and np.isnan(got[17::256]).all()
+    keep = ~np.isnan(want)
+    assert np.array_equal(np.isnan(got), ~keep)
+    assert_same_bits(got[keep], want[keep], "decode attention, other dimensions")
+
+
+@pytest.mark.parametrize("position,window,slots", [(100, 512, 96), (100, 16, 32)])
+def test_rope_attention_decode_refuses_short_rings(device, position, window, slots):
+    # A ring with fewer slots than the window's keys would have the step's
+    # key appended over a key the step reads; under 64 slots, a chunk's rows
+    # could wrap it twice. Both are refused before any launch.
+    rng = np.random.default_rng(3)
+    kc = np.zeros(slots * 256, np.uint16)
+    with pytest.raises(fz.FrzError, match="fewer slots than the window"):
+        _rope_attention_case(device, position, window, slots, 1e4, kc, kc.copy(), rng)
