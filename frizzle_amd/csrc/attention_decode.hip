@@ -151,8 +151,8 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   const int l = lane & 31;
   float2 turn;
   float4 va, vb, xa, xb, ga, gb;
+  if (w == 1) turn = ld2f(a.turns + 2 * lane);
   if (w == 0) {
-    turn = ld2f(a.turns + 2 * lane);
     const float* src = a.qkv + (key_lane ? QH : h) * D;
     va = ld4f(src + 4 * l);
     vb = ld4f(src + D / 2 + 4 * l);
@@ -177,46 +177,50 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   // Lane t's part of key row jj: the 8 halves 8 (4m + u) .. +7 for m = 0..7,
   // so that a key's 4 lanes read 64 contiguous bytes a load (a wave's load
   // touches 16 cache lines, where quarter rows a lane would touch 64).
-  uint4 kr[kKeyLoads];
-  {
+  // Thread t's share of the value rows' dimensions: uint4 i = t + 256 n is
+  // row i / kRowParts, halves q kDims + 8 (i % kRowParts) .. +7. (Registers
+  // named by constant indices: an array indexed in a loop is placed in LDS
+  // before the loop is unrolled, and its stores then wait for each load.)
+  const int vrow = t / kRowParts, part = t % kRowParts;
+  uint4 kr[kKeyLoads], vr[kValueParts];
+  auto request_rows = [&]() {
     const __amdgpu_buffer_rsrc_t kres = cache_resource(a.key_cache, a.slots);
     int slot = base + jj;
     slot = slot >= a.slots ? slot - a.slots : slot;
     const int at = jj < cached ? slot * (D * 2) + 16 * u : kPastEnd;
 #pragma unroll
     for (int m = 0; m < kKeyLoads; ++m) kr[m] = load_row_part(kres, at + 64 * m);
-  }
-  // Thread t's share of the value rows' dimensions: uint4 i = t + 256 n is
-  // row i / kRowParts, halves q kDims + 8 (i % kRowParts) .. +7. (Registers
-  // named by constant indices: an array indexed in a loop is placed in LDS
-  // before the loop is unrolled, and its stores then wait for each load.)
-  const int vrow = t / kRowParts, part = t % kRowParts;
-  const __amdgpu_buffer_rsrc_t vres = cache_resource(a.value_cache, a.slots);
-  auto value_part = [&](int n) {
-    const int rr = vrow + kRowStep * n;
-    int slot = base + rr;
-    slot = slot >= a.slots ? slot - a.slots : slot;
-    return load_row_part(vres, rr < cached ? slot * (D * 2) + 2 * (q * kDims + 8 * part) : kPastEnd);
+    const __amdgpu_buffer_rsrc_t vres = cache_resource(a.value_cache, a.slots);
+    auto value_part = [&](int n) {
+      const int rr = vrow + kRowStep * n;
+      int vslot = base + rr;
+      vslot = vslot >= a.slots ? vslot - a.slots : vslot;
+      return load_row_part(vres,
+                           rr < cached ? vslot * (D * 2) + 2 * (q * kDims + 8 * part) : kPastEnd);
+    };
+    vr[0] = value_part(0);
+    vr[1] = value_part(1);
+    if constexpr (kValueParts == 8) {
+      vr[2] = value_part(2); vr[3] = value_part(3); vr[4] = value_part(4);
+      vr[5] = value_part(5); vr[6] = value_part(6); vr[7] = value_part(7);
+    } else {
+      static_assert(kValueParts == 2, "8 or 2 value parts a thread");
+    }
   };
-  uint4 vr[kValueParts];
-  vr[0] = value_part(0);
-  vr[1] = value_part(1);
-  if constexpr (kValueParts == 8) {
-    vr[2] = value_part(2); vr[3] = value_part(3); vr[4] = value_part(4);
-    vr[5] = value_part(5); vr[6] = value_part(6); vr[7] = value_part(7);
-  } else {
-    static_assert(kValueParts == 2, "8 or 2 value parts a thread");
-  }
+  request_rows();
   // Nothing below moves above the loads: the rope's arithmetic waits for its
   // inputs, which would hold back loads issued after it.
   __builtin_amdgcn_sched_barrier(0);
-  if (w == 0) {
-    // The rope angles: lane L turns pairs 2L and 2L + 1.
+  // Wave 1 turns the rope angles (lane L pairs 2L and 2L + 1) while wave 0
+  // normalizes; a barrier hands the angles over.
+  if (w == 1) {
     float s0, c0, s1, c1;
     rope_angle(turn.x, (uint32_t)p, &s0, &c0);
     rope_angle(turn.y, (uint32_t)p, &s1, &c1);
     *reinterpret_cast<float2*>(&S.sine[2 * lane]) = make_float2(s0, s1);
     *reinterpret_cast<float2*>(&S.cosine[2 * lane]) = make_float2(c0, c1);
+  }
+  if (w == 0) {
     // The head's sum of squares: the halving tree over its 32 lanes. Each
     // 32-lane group's lane 0 ends with the total (level 16 by a swizzle
     // within the group, lane l ^ 16; levels 8 to 1 within a row by DPP),
@@ -232,8 +236,11 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
       const int lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
       sum = __builtin_bit_cast(float, key_lane ? hi : lo);
     }
-    wave_lds_sync();
-    rope_norm_rotate(va, vb, sum, D, a.epsilon, ga, gb, l, S.cosine, S.sine);
+    rope_normalize(va, vb, sum, D, a.epsilon, ga, gb);
+  }
+  __syncthreads();  // the angles
+  if (w == 0) {
+    rope_rotate(va, vb, l, S.cosine, S.sine);
     if (!key_lane) {
       const float sc = a.scale_log2e;
       *reinterpret_cast<float4*>(&S.q[4 * l]) =
@@ -310,15 +317,11 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
     stage(5, vr[5]); stage(6, vr[6]); stage(7, vr[7]);
   }
   __syncthreads();
-  if (w >= kOutWaves) return;
-  // The summing waves: lane L is key L. Its score, then dimension t of
-  // every value row the chunk uses, read now to land under the weights'
-  // arithmetic.
+  // The waves that sum the output dimensions, and one that sums l (the last
+  // of them, or wave 1 when one wave sums the outputs): lane L is key L.
+  constexpr int kLWave = kOutWaves > 1 ? kOutWaves - 1 : 1;
+  if (w > kLWave) return;
   const float sl = S.s[4 * lane];
-  const _Float16* vh = reinterpret_cast<const _Float16*>(S.v);
-  _Float16 vt[kChunkKeys];
-#pragma unroll
-  for (int key = 0; key < kChunkKeys; ++key) vt[key] = vh[key * kDims + t];
   // (attention.wgsl:304-340) A key is live when the token sees it; a tile is
   // seen when any of its keys is. A tile's maximum is over its live scores,
   // and tile T's running maximum over the seen tiles' maxima up to T: max is
@@ -330,13 +333,28 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   const bool live = lane < valid && r.k_begin + lane + a.window > p;
   const uint64_t live_bits = __ballot(live);
   const int tile = lane >> 3;
-  uint32_t seen_tiles = 0;  // bit T: tile T seen
-#pragma unroll
-  for (int tt = 0; tt < kTiles; ++tt) seen_tiles |= ((live_bits >> (8 * tt)) & 0xFFu) ? 1u << tt : 0u;
+  // Bit T: tile T seen (each byte of the ballot or-ed into its low bit,
+  // the 8 low bits gathered by one multiply).
+  uint64_t any = live_bits | (live_bits >> 4);
+  any |= any >> 2;
+  any |= any >> 1;
+  const uint32_t seen_tiles =
+      (uint32_t)(((any & 0x0101010101010101ull) * 0x0102040810204080ull) >> 56);
   const bool tile_seen = (seen_tiles >> tile) & 1u;
   const bool seen_before = (seen_tiles & ((1u << tile) - 1u)) != 0;
   const float none = __builtin_bit_cast(float, 0x7FC00000u);
   const float top = max8(live ? sl : none);
+  // Dimension t of every value row the chunk uses, read now to land under
+  // the weights' arithmetic: after the score has landed (an LDS counter
+  // holds 15 reads, so a wait for a read issued before 64 others would
+  // wait for 49 of them too).
+  __builtin_amdgcn_sched_barrier(0);
+  const _Float16* vh = reinterpret_cast<const _Float16*>(S.v);
+  _Float16 vt[kChunkKeys];
+  if (w < kOutWaves) {
+#pragma unroll
+    for (int key = 0; key < kChunkKeys; ++key) vt[key] = vh[key * kDims + t];
+  }
   float run = tile_seen ? top : none;
   run = __builtin_fmaxf(run, dpp_or<0x118, 0xF>(run, none));  // row_shr:8: the row's first tile
   run = __builtin_fmaxf(run, dpp_or<0x142, 0xA>(run, none));  // row_bcast:15: rows 1, 3
@@ -371,7 +389,7 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   tsum = tsum + row_shl<7>(e);
   wave_lds_sync();
   const size_t slot_at = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
-  if (w == kOutWaves - 1) {
+  if (w == kLWave) {
     float cl = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < kTiles; ++tt) {
@@ -383,6 +401,7 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
           make_float4(cm, cl, chunk_live ? 1.0f : 0.0f, 0.0f);
     }
   }
+  if (w >= kOutWaves) return;
   // O = O a + sum_b e_b v_b per tile, over all 8 tiles: a tile past the
   // chunk's has a = 1 and zero weights and rows, and leaves o as it is (o is
   // never -0, and 0 * 0 adds +0); so does every key past the chunk's end.

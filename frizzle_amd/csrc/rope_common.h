@@ -34,17 +34,21 @@ __device__ __forceinline__ float rope_lane_squares(float4 a, float4 b) {
   return dot4f(a, a) + dot4f(b, b);
 }
 
-// Normalize by r = 1/sqrt(sum / d + eps), times the gain, then turn each pair
-// (k, k + d/2) by its angle: x' = x c - y s, y' = x s + y c.
-// The gain's values for the lane: ga at 4 lane, gb at d/2 + 4 lane.
-__device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum, int head_dim,
-                                                 float epsilon, float4 ga, float4 gb, int lane,
-                                                 const float* cosines, const float* sines) {
+// The normalization: x r g for r = 1/sqrt(sum / d + eps), the gain's values
+// for the lane ga at 4 lane, gb at d/2 + 4 lane.
+__device__ __forceinline__ void rope_normalize(float4& a, float4& b, float sum, int head_dim,
+                                               float epsilon, float4 ga, float4 gb) {
   const float r = inverse_sqrt(sum / (float)head_dim + epsilon);
   a.x = (a.x * r) * ga.x; a.y = (a.y * r) * ga.y;
   a.z = (a.z * r) * ga.z; a.w = (a.w * r) * ga.w;
   b.x = (b.x * r) * gb.x; b.y = (b.y * r) * gb.y;
   b.z = (b.z * r) * gb.z; b.w = (b.w * r) * gb.w;
+}
+
+// The turn of pairs (k, k + d/2), k = 4 lane .. 4 lane + 3, by their angles:
+// x' = x c - y s, y' = x s + y c.
+__device__ __forceinline__ void rope_rotate(float4& a, float4& b, int lane, const float* cosines,
+                                            const float* sines) {
   const int k = 4 * lane;
   const float c0 = cosines[k], c1 = cosines[k + 1], c2 = cosines[k + 2], c3 = cosines[k + 3];
   const float s0 = sines[k], s1 = sines[k + 1], s2 = sines[k + 2], s3 = sines[k + 3];
@@ -54,6 +58,14 @@ __device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum
                                 a.z * s2 + b.z * c2, a.w * s3 + b.w * c3);
   a = ra;
   b = rb;
+}
+
+// Normalize, then turn.
+__device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum, int head_dim,
+                                                 float epsilon, float4 ga, float4 gb, int lane,
+                                                 const float* cosines, const float* sines) {
+  rope_normalize(a, b, sum, head_dim, epsilon, ga, gb);
+  rope_rotate(a, b, lane, cosines, sines);
 }
 
 __device__ __forceinline__ void rope_norm_rotate(float4& a, float4& b, float sum, int head_dim,
