@@ -47,6 +47,11 @@ GEMV_BYTES = GEMV_ROWS * GEMV_COLS // 32 * 18 + GEMV_COLS * 4 + GEMV_ROWS * 4
 ROLES = ["q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm", "k_norm",
          "post_attn_norm", "ffn_norm", "post_ffn_norm"]
 
+LAYER_WEIGHT_BYTES = 15_095_808
+LAYER_GAIN_BYTES = 4 * (4 * 1152 + 2 * 256)
+LAYER_KV_BYTES = 512 * 2 * 256 * 2
+LAYER_ACT_BYTES = 4 * (3 * 1152 + 1536 + 1024 + 3 * 1152 + 2 * 6912 + 1152)
+
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -79,6 +84,10 @@ def parse():
                         "with frz_model_load_gguf, check its tokens, print one JSON line")
     p.add_argument("--prefill-only", action="store_true",
                    help="only the 2,048-token prefill, printed as one JSON line (for profiles)")
+    p.add_argument("--probes", action="store_true",
+                   help="only the floors: an empty kernel's launch (on the stream and "
+                        "graph-replayed) and streaming reads of each decode product's "
+                        "weight bytes (one JSON line)")
     p.add_argument("--gemv-stream", action="store_true",
                    help="time the GEMV launches on the stream, not replayed from a graph")
     return p.parse_args()
@@ -138,6 +147,64 @@ def gemv_roofline(fz, dev, copies, iters, seed, graph=True):
     for a in codes + scales + [x, y]:
         a.free()
     return us.value
+
+
+# Weight bytes of each decode product of one layer (Q4_0: 18 bytes a block
+# of 32), and the layer's.
+PRODUCT_BYTES = {
+    "qkv 1536x1152": 1536 * 1152 // 32 * 18,
+    "o 1152x1024": 1152 * 1024 // 32 * 18,
+    "gate+up 2x6912x1152": 2 * 6912 * 1152 // 32 * 18,
+    "down 1152x6912": 1152 * 6912 // 32 * 18,
+    "layer": LAYER_WEIGHT_BYTES,
+}
+STREAM_SPAN = 768 << 20  # bytes walked per size: past the 256 MB last-level cache
+
+
+def floors(fz, dev, iters=6400, graph=True):
+    """The launch floor (an empty kernel, on the stream and graph-replayed)
+    and the streaming floor of each product's weight bytes (reads of
+    distinct copies, so they come from HBM; graph-replayed unless `graph` is
+    false, for the profiler)."""
+    import ctypes
+    lib = fz.load()
+    us = ctypes.c_double()
+    launch = {}
+    for graph, name in ((0, "stream"), (1, "graph")):
+        fz._lib.check(lib.frz_bench_launch_floor(dev.handle, iters, graph, ctypes.byref(us)))
+        launch[name] = us.value
+    sink = dev.empty((1024,), np.uint32)
+    big = dev.empty((STREAM_SPAN,), np.uint8)
+    streams = []
+    for what, nbytes in PRODUCT_BYTES.items():
+        nbytes = (nbytes + 255) // 256 * 256
+        copies = max(1, STREAM_SPAN // nbytes)
+        ptrs = (ctypes.c_void_p * copies)(*[big.ptr + c * nbytes for c in range(copies)])
+        fz._lib.check(lib.frz_bench_stream(dev.handle, ptrs, copies, ctypes.c_uint64(nbytes),
+                                           sink.ptr, max(iters // 10, copies),
+                                           1 if graph else 0, ctypes.byref(us)))
+        streams.append({"what": what, "bytes": nbytes, "copies": copies, "us": us.value,
+                        "gbs": nbytes / (us.value * 1e-6) / 1e9,
+                        "us_at_peak": nbytes / (HBM_PEAK_GBS * 1e9) * 1e6})
+    big.free()
+    sink.free()
+    return {"launch_floor_us": launch, "stream_floor": streams,
+            "how": "empty kernel (1 workgroup of 64 threads) launched back to back; "
+                   "streaming reads by 1,024 workgroups x 256 threads, 4 uint4 loads in "
+                   "flight a thread, over distinct copies spanning 768 MiB, "
+                   + ("graph-replayed" if graph else "launched on the stream")
+                   + "; HIP events on the launching stream"}
+
+
+def host_cpu():
+    """The host CPU's model name, from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def cpu_sample(orc, cfg, tensors, prompt, budget_s, max_tokens):
@@ -267,10 +334,6 @@ def steered_batch(fz, model, dev, cfg, seed, prompt_len=1024, variants=16, token
 # One local layer's single-token decode (its five launches): algorithmic bytes
 # = its Q4_0 weights, its gains, its 512 keys and values read (F16), and the
 # activation rows its launches read and write.
-LAYER_WEIGHT_BYTES = 15_095_808
-LAYER_GAIN_BYTES = 4 * (4 * 1152 + 2 * 256)
-LAYER_KV_BYTES = 512 * 2 * 256 * 2
-LAYER_ACT_BYTES = 4 * (3 * 1152 + 1536 + 1024 + 3 * 1152 + 2 * 6912 + 1152)
 
 
 def one_layer(fz, model, cfg, seed, position, iters=500):
@@ -334,6 +397,13 @@ def main():
         gguf_load(fz, args.seed)
         return
 
+    if args.probes:
+        dev = fz.Device(0)
+        out = floors(fz, dev, graph=not args.gemv_stream)
+        dev.close()
+        print(json.dumps({"probes": True, **out}))
+        return
+
     context = 8192
     assert args.prompt + args.warmup + args.steps + 1 <= context
     cfg = fz.gemma3_1b_config(context=context)
@@ -380,7 +450,12 @@ def main():
             "value": decoded / secs, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{decoded} greedy decode tokens of the full 26-layer model after a "
                       f"16-token prompt (positions 17..{16 + decoded}), CPU oracle, "
-                      f"OpenMP over output rows, {secs:.1f}s"}
+                      f"OpenMP over output rows, {secs:.1f}s",
+            "context": f"positions 17..{16 + decoded}: attention over at most "
+                       f"{16 + decoded} keys, where the GPU's value is timed at positions "
+                       f"{args.prompt + args.warmup + 1}..{args.prompt + args.warmup + args.steps} "
+                       "(a 512-key window and up to 4,360 keys); the products, which "
+                       "dominate a step, are the same"}
         log(f"parity {parity}; cpu {cpu_baseline['value']:.3f} tok/s")
 
     # A 2,048-token prefill (its positions are written again by the prompt
@@ -442,10 +517,17 @@ def main():
 
     us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
                        not args.gemv_stream)
+    # The same launches one by one on the stream, as the profiler sees them
+    # (its trace does not follow graph launches).
+    us_stream = gemv_roofline(fz, dev, args.gemv_copies, min(args.gemv_iters, 640), args.seed,
+                              False)
     achieved = GEMV_BYTES / (us * 1e-6) / 1e9
-    log(f"gemv 6912x1152: {us:.3f} us/launch, {achieved:.0f} GB/s")
+    log(f"gemv 6912x1152: {us:.3f} us/launch, {achieved:.0f} GB/s "
+        f"({us_stream:.3f} us a launch on the stream)")
     model.close()
     dev.close()
+    if cpu_baseline is not None:
+        cpu_baseline["host_cpu"] = host_cpu()
 
     out = {
         "metric": "decode tok/s + Q4_0 GEMV achieved HBM GB/s (% of 8 TB/s), Gemma-3-1B",
@@ -467,8 +549,17 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": committed_traffic(),
+                     "traffic_source": "committed counter summary "
+                                       "profiles/q4_0_gemv_6912x1152_traffic.md (FETCH_SIZE "
+                                       "+ WRITE_SIZE a dispatch, scaled by a 256 MiB copy's "
+                                       "counters), not measured in this run",
                      "kernel": "Q4_0 decode GEMV 6912x1152 (gemv_pair_kernel<0, 4>: 18 lanes a row, 14 rows a workgroup)",
-                     "us_per_launch": us, "algorithmic_bytes": GEMV_BYTES},
+                     "launch_mode": "graph replay of 64 launches over 64 weight copies"
+                                    if not args.gemv_stream else "launches on the stream",
+                     "us_per_launch": us, "us_per_launch_stream": us_stream,
+                     "profile": "profiles/q4_0_gemv_6912x1152_kernel_stats.md (rocprofv3, "
+                                "launches on the stream: compare us_per_launch_stream)",
+                     "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,
         "parity": parity,
         "one_layer": layer,

@@ -137,6 +137,9 @@ _SIGS = {
     "frz_op_draw": (c_int, [_P, _P, POINTER(Sampling), c_uint32, c_uint32,
                             _P]),
     "frz_op_numerics": (c_int, [_P, c_int, _P, _P, c_int]),
+    "frz_bench_launch_floor": (c_int, [_P, c_int, c_int, POINTER(c_double)]),
+    "frz_bench_stream": (c_int, [_P, POINTER(c_void_p), c_int, c_uint64, _P, c_int, c_int,
+                                 POINTER(c_double)]),
     "frz_bench_gemv": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p), c_int,
                                c_int, c_int, _P, _P, c_int, c_int, POINTER(c_double)]),
     "frz_bench_gated": (c_int, [_P, POINTER(c_void_p), POINTER(c_void_p),

@@ -61,6 +61,34 @@ DevStep host_step(uint32_t position, uint32_t tokens) {
   return s;
 }
 
+// The floor a launch costs: a kernel that does nothing.
+__global__ void empty_kernel() {}
+
+// The floor a product's bytes cost: every uint4 of a buffer read once, 4 in
+// flight a thread, xor-folded into one word a workgroup (written so the
+// reads stay). kStreamBlocks workgroups fill the chip.
+constexpr int kStreamBlocks = 1024;
+constexpr int kFloorCopies = 64;
+__global__ __launch_bounds__(256) void stream_kernel(const uint4* __restrict__ src, size_t n4,
+                                                     uint32_t* __restrict__ sink) {
+  __shared__ uint32_t fold[4];
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t x = 0;
+  for (; i + 3 * stride < n4; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    x ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n4; i += stride) {
+    const uint4 a = src[i];
+    x ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+  if ((threadIdx.x & 63) == 0) fold[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = fold[0] ^ fold[1] ^ fold[2] ^ fold[3];
+}
+
 // The workspace of frz_op_rope_attention_noalloc: one row's chunk states
 // (kStaticChunks x 4 heads x 256 outputs, then 4 statistics a chunk and
 // head), 931,840 bytes. Every device the library opens holds its own copy
@@ -573,6 +601,32 @@ int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
     return launch_gated(dev->stream, dev->step, q4(gate_codes[c], gate_scales[c], rows, cols),
                         q4(up_codes[c], up_scales[c], rows, cols), x, act, 1, nullptr, 0);
   }, "frz_bench_gated", us_per_launch);
+}
+
+int frz_bench_launch_floor(frz_device* dev, int iters, int graph, double* us_per_launch) {
+  if (!dev || iters <= 0 || !us_per_launch) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_bench_launch_floor: bad argument");
+  }
+  return bench_graph(dev, kFloorCopies, iters, graph, [&](int) {
+    hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, dev->stream);
+    return hipGetLastError();
+  }, "frz_bench_launch_floor", us_per_launch);
+}
+
+int frz_bench_stream(frz_device* dev, const void* const* buffers, int copies, uint64_t bytes,
+                     uint32_t* sink, int iters, int graph, double* us_per_launch) {
+  if (!dev || !buffers || copies <= 0 || bytes < 16 || bytes % 16 || !sink || iters <= 0 ||
+      !us_per_launch) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_bench_stream: bad argument");
+  }
+  for (int c = 0; c < copies; ++c) {
+    if (!buffers[c]) return fail(FRZ_ERR_ARGUMENT, "frz_bench_stream: null buffer");
+  }
+  return bench_graph(dev, copies, iters, graph, [&](int c) {
+    hipLaunchKernelGGL(stream_kernel, dim3(kStreamBlocks), dim3(256), 0, dev->stream,
+                       static_cast<const uint4*>(buffers[c]), (size_t)(bytes / 16), sink);
+    return hipGetLastError();
+  }, "frz_bench_stream", us_per_launch);
 }
 
 int frz_copy(frz_device* dev, void* dev_dst, const void* dev_src, uint64_t bytes) {

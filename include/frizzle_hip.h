@@ -215,6 +215,17 @@ int frz_bench_gated(frz_device* dev, const void* const* gate_codes,
                     int copies, int rows, int cols, const float* x, float* act,
                     int iters, int graph, double* us_per_launch);
 
+/* Floors, measured the same way: an empty kernel launched `iters` times
+ * (with `graph`, 64 launches captured and replayed), and a streaming read of
+ * `bytes` (a multiple of 16) from each of `copies` device buffers in turn, by
+ * 1,024 workgroups, xor-folded into sink[0..1023] (device memory of 1,024
+ * words). No counterpart in the reference (measurement only). */
+int frz_bench_launch_floor(frz_device* dev, int iters, int graph,
+                           double* us_per_launch);
+int frz_bench_stream(frz_device* dev, const void* const* buffers, int copies,
+                     uint64_t bytes, uint32_t* sink, int iters, int graph,
+                     double* us_per_launch);
+
 /* Each pair's turns a position for a rotary base (src/core/kernels/rope/
  * rope.cpp:95-106): theta_k / 2 pi in f64, rounded once to f32. */
 void frz_rope_turns(float base, int head_dim, float* turns);
