@@ -222,11 +222,11 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   }
   if (w == 0) {
     // The head's sum of squares: the halving tree over its 32 lanes. Each
-    // 32-lane group's lane 0 ends with the total (level 16 by a swizzle
-    // within the group, lane l ^ 16; levels 8 to 1 within a row by DPP),
-    // which goes to the group's lanes.
+    // 32-lane group's lane 0 ends with the total (level 16 by a lane swap,
+    // lane l + 16; levels 8 to 1 within a row by DPP), which goes to the
+    // group's lanes.
     float sum = rope_lane_squares(va, vb);
-    sum = sum + __builtin_bit_cast(float, other_row(__builtin_bit_cast(int, sum)));
+    sum = sum + lane_plus16(sum);
     sum = sum + row_shl<8>(sum);
     sum = sum + row_shl<4>(sum);
     sum = sum + row_shl<2>(sum);

@@ -236,10 +236,11 @@ __device__ __forceinline__ bool norm_thread() {
 // barrier. `red` is 256 floats the call owns: a second tree uses another.
 
 // The halving tree's last six levels over a wave's 64 sums: lane l adds
-// lane l + stride for strides 32 .. 1; lane 0's total, broadcast.
+// lane l + stride for strides 32 .. 1 (strides 32 and 16 by lane swaps,
+// 8 .. 1 by DPP); lane 0's total, broadcast.
 __device__ __forceinline__ float wave_tree(float s) {
-  s = s + __shfl_down(s, 32, 64);
-  s = s + __shfl_down(s, 16, 64);
+  s = s + lane_plus32(s);
+  s = s + lane_plus16(s);
   s = s + row_shl<8>(s);
   s = s + row_shl<4>(s);
   s = s + row_shl<2>(s);

@@ -165,6 +165,23 @@ __device__ __forceinline__ float row_shl(float v) {
                                                                0x100 + N, 0xF, 0xF, true));
 }
 
+// v_permlane32_swap a, b exchanges rows 2-3 of a with rows 0-1 of b, and
+// v_permlane16_swap a, b the odd rows of a with the even rows of b (a row is
+// 16 lanes), both VALU operations. Written as asm with their operands named,
+// so each result is the register the instruction defines; the wait states
+// before them cover a VALU write of their inputs just before.
+__device__ __forceinline__ float lane_plus32(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return b;  // lanes 0-31: lane l + 32; lanes 32-63: their own
+}
+
+__device__ __forceinline__ float lane_plus16(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return b;  // rows 0 and 2: lane l + 16; rows 1 and 3: their own
+}
+
 // F16 to f32, exact, subnormals kept.
 FRZ_HD float f16_unpack(uint32_t h) {
   const uint32_t sign = (h & 0x8000u) << 16;
