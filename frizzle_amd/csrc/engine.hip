@@ -802,6 +802,9 @@ int create_model(frz_device* dev, const frz_model_config& c, const frz_plan* pla
     if (int rc = alloc(m, &m->output_norm, (size_t)c.hidden * 4)) return bail(rc);
   }
   const size_t B = kPrefillBlock;
+  // The O product's fold prologue reads the states of kFoldPrologueChunks
+  // chunks whatever a step's count (a prefill block's states are larger).
+  max_partials = std::max(max_partials, (size_t)64 * kFoldPrologueChunks * qw);
   m->partial_floats = max_partials;
   auto working = [&](auto** p, const char* purpose, size_t bytes) {
     return working_buffer(m, plan, p, purpose, bytes);

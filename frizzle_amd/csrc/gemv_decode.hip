@@ -308,15 +308,14 @@ __device__ __forceinline__ void prologue_load(Prologue<T, X4>& P, const GemvInpu
     return;
   }
   if (MODE == 3) {
-    // Chunks past the window's count, and chunk states past the (chunk,
-    // head) pairs for a whole wave, are not loaded (the count is the same
-    // for every thread; the second test is uniform over the wave).
-    const int count = window_chunks(step, in.window);
-    if (((int)threadIdx.x & ~63) < count * attn::QH)
-      P.st = ld4(in.stats + 4 * min((int)threadIdx.x, count * attn::QH - 1));
+    // Every chunk state the prologue can fold is loaded, whatever the
+    // window's count (the buffers hold kFoldPrologueChunks chunks; states
+    // past the count are never used), so no load waits for the step's
+    // position. Wave 0 holds the (chunk, head) statistics.
+    if (threadIdx.x < 64)
+      P.st = ld4(in.stats + 4 * min((int)threadIdx.x, kFoldPrologueChunks * attn::QH - 1));
 #pragma unroll
     for (int c = 0; c < kFoldPrologueChunks; ++c) {
-      if (c >= count) continue;
 #pragma unroll
       for (int j = 0; j < Shape<T>::kFoldVec4s; ++j) {
         P.po[c][j] = ld4(in.partials + c * kFoldWidth + 4 * ((int)threadIdx.x + j * T));
@@ -664,6 +663,20 @@ __device__ __forceinline__ float row_total(const float* parts) {
   return total;
 }
 
+// The layer's pin words [first, count], loaded through a vector register:
+// a scalar load would be waited for before the kernel's other scalar loads,
+// its arguments, which everything after waits on; a vector load is waited
+// for where its words are used, at the end. Without a table the words are
+// read from `fallback` (any two readable words) and not used: no branch
+// around the load, whose join would wait for it.
+__device__ __forceinline__ uint2 request_pin_words(const uint32_t* __restrict__ edits, int layer,
+                                                   const void* fallback) {
+  int at = 2 * layer;
+  asm volatile("" : "+v"(at));
+  const uint32_t* src = edits ? edits + at : static_cast<const uint32_t*>(fallback);
+  return make_uint2(src[0], src[1]);
+}
+
 // A layer's pins on neuron n at `position` (edit.wgsl:55-76): the layer's
 // edits are sorted by neuron then first position (edit.cpp:20-31), so a
 // binary search finds the neuron's; its ranges never overlap.
@@ -983,18 +996,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   const int r = lane & 31;
   const int local = wave * 2 + (lane >> 5);
   const int n = blockIdx.x * kNeurons + local;
-  // The layer's pin words are read first, off the end's critical path.
-  uint32_t pin_first = 0, pin_count = 0;
-  if (edits) {
-    pin_first = edits[2 * layer];
-    pin_count = edits[2 * layer + 1];
-  }
   LanePlan<2, MAXI> plan;
   lane_plan<2, MAXI>(plan, gate.cols >> 5, 2 * local, r);
   Prologue<T, X4> pro;
   prologue_load<MODE, T, X4>(pro, in, step, gate.cols);
   LaneWeights<MAXI> W;
   load_neuron<MAXI>(W, plan, gate, up, n);
+  const uint2 pins = request_pin_words(edits, layer, step);
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, gate.cols);
   __syncthreads();
   lane_chains<2, MAXI>(W, plan, xs, parts);
@@ -1004,7 +1012,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_kernel(const DevStep* _
   const float u = row_shl<1>(total);  // lane t + 1: even t stays in its row
   if (r == 0 && n < gate.rows) {
     float v = gelu_tanh(total) * u;
-    if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)n, step->position, v);
+    if (edits && pins.y) v = apply_pins(edits, pins.x, pins.y, (uint32_t)n, step->position, v);
     act[n] = v;
   }
 }
@@ -1030,12 +1038,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
   const int which = q >= pair::kLanes ? 1 : 0;
   const int tiles = (gate.rows + kNeurons - 1) / kNeurons;
   auto tile_of = [&](int k) { return min((int)blockIdx.x * TPW + k, tiles - 1); };
-  uint32_t pin_first = 0, pin_count = 0;
-  if (edits) {
-    pin_first = edits[2 * layer];
-    pin_count = edits[2 * layer + 1];
-  }
   const pair::Plan P = pair::plan(q - which * pair::kLanes);
+  // Every argument the loads use, read at once (a single wait, rather than
+  // one for each block of code that first needs one).
+  asm volatile("" ::"s"(gate.codes), "s"(gate.scales), "s"(up.codes), "s"(up.scales),
+               "s"(in.x), "s"(in.hidden), "s"(in.output), "s"(in.post_gain), "s"(in.gain),
+               "s"(in.epsilon), "s"(edits), "s"(layer));
   Prologue<T, X4> pro;
   prologue_load<MODE, T, X4>(pro, in, step, gate.cols);
   const QMatrix& m = which ? up : gate;
@@ -1050,6 +1058,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
     d[b][1] = m.scales[base + P.g1];
   };
   load_tile(0, 0);
+  const uint2 pins = request_pin_words(edits, layer, step);
   prologue_finish<MODE, T, X4>(xs, red, pro, in, step, gate.cols);
   __syncthreads();
   float4 x0[8], x1[8];
@@ -1078,7 +1087,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_gated_pair_kernel(
       const int nn = tile_of(k) * kNeurons + (t >> 1);
       if ((t & 1) == 0 && t < 2 * kNeurons && nn < gate.rows) {
         float v = gelu_tanh(total) * u;
-        if (pin_count) v = apply_pins(edits, pin_first, pin_count, (uint32_t)nn, step->position, v);
+        if (edits && pins.y) v = apply_pins(edits, pins.x, pins.y, (uint32_t)nn, step->position, v);
         act[nn] = v;
       }
     }
