@@ -429,17 +429,19 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
 
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
                                    const DecodeAttentionArgs& a, int rows) {
-  if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1 || rows < 1)
+  if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1 || rows < 1 ||
+      a.grid_chunks < 0 || a.grid_chunks > a.max_chunks)
     return hipErrorInvalidValue;
+  const int chunks = a.grid_chunks > 0 ? a.grid_chunks : a.max_chunks;
   // A grid of a few dozen workgroups (a sliding window, one row) is split
   // four ways by output dimension, to spread the value rows over more CUs;
   // a longer one already fills the chip.
-  if (a.max_chunks * rows <= 16) {
-    hipLaunchKernelGGL(attention_decode_kernel<4>, dim3(a.max_chunks, QH * 4, rows),
-                       dim3(kThreads), 0, s, step, a);
+  if (chunks * rows <= 16) {
+    hipLaunchKernelGGL(attention_decode_kernel<4>, dim3(chunks, QH * 4, rows), dim3(kThreads), 0,
+                       s, step, a);
   } else {
-    hipLaunchKernelGGL(attention_decode_kernel<1>, dim3(a.max_chunks, QH, rows), dim3(kThreads),
-                       0, s, step, a);
+    hipLaunchKernelGGL(attention_decode_kernel<1>, dim3(chunks, QH, rows), dim3(kThreads), 0, s,
+                       step, a);
   }
   return hipGetLastError();
 }

@@ -25,22 +25,21 @@ __device__ __forceinline__ float dot4v(float4 a, float4 b) {
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxVec4 = 4;  // rows up to 4,096 wide
 
-// The workgroup's sum in the reference's tree (norm.wgsl:75-85): halving
-// the 256 partial sums at each level.
+// The workgroup's sum in the reference's tree (norm.wgsl:75-85), halving
+// the 256 partial sums at each level: levels 128 and 64 in registers from
+// LDS, the last six across the wave, so every wave has the total after one
+// barrier. `partial` is 256 floats the call owns.
 __device__ __forceinline__ float norm_reduce(float* partial, float v) {
-  const int i = threadIdx.x;
+  const int i = threadIdx.x, lane = i & 63;
   partial[i] = v;
   __syncthreads();
-  for (int stride = kNormThreads / 2; stride > 0; stride >>= 1) {
-    if (i < stride) partial[i] = partial[i] + partial[i + stride];
-    __syncthreads();
-  }
-  return partial[0];
+  return wave_tree((partial[lane] + partial[lane + 128]) +
+                   (partial[lane + 64] + partial[lane + 192]));
 }
 
 __global__ __launch_bounds__(kNormThreads) void norm_kernel(
     const DevStep* __restrict__ step, NormArgs a) {
-  __shared__ float partial[kNormThreads];
+  __shared__ float partial[2][kNormThreads];
   const int tokens = (int)step->tokens;
   const int row = a.last_token ? tokens - 1 : (int)blockIdx.x;
   if (row >= tokens) return;
@@ -59,15 +58,28 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
 #pragma unroll
     for (int k = 0; k < kNormMaxVec4; ++k) {
       const int q = i + k * kNormThreads;
-      if (k < per && q < vec4s) y[k] = ld4(a.output + base + 4 * q);
+      if (k < per && q < vec4s) {
+        y[k] = ld4(a.output + base + 4 * q);
+        // A split product's output: the prefix of its first ranges, then
+        // the later range sums added in range order.
+        if (a.parts) {
+#pragma unroll
+          for (int j = 0; j < kSplitParts; ++j) {
+            const float4 s = ld4(a.parts + j * a.parts_stride + base + 4 * q);
+            y[k].x = y[k].x + s.x;
+            y[k].y = y[k].y + s.y;
+            y[k].z = y[k].z + s.z;
+            y[k].w = y[k].w + s.w;
+          }
+        }
+      }
     }
     float squares = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNormMaxVec4; ++k) {
       if (k < per && i + k * kNormThreads < vec4s) squares = squares + dot4v(y[k], y[k]);
     }
-    const float r = inverse_sqrt(norm_reduce(partial, squares) / n + a.epsilon);
-    __syncthreads();
+    const float r = inverse_sqrt(norm_reduce(partial[0], squares) / n + a.epsilon);
 #pragma unroll
     for (int k = 0; k < kNormMaxVec4; ++k) {
       const int q = i + k * kNormThreads;
@@ -109,7 +121,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
   for (int k = 0; k < kNormMaxVec4; ++k) {
     if (k < per && i + k * kNormThreads < vec4s) squares = squares + dot4v(x[k], x[k]);
   }
-  const float r = inverse_sqrt(norm_reduce(partial, squares) / n + a.epsilon);
+  const float r = inverse_sqrt(norm_reduce(partial[1], squares) / n + a.epsilon);
 #pragma unroll
   for (int k = 0; k < kNormMaxVec4; ++k) {
     const int q = i + k * kNormThreads;

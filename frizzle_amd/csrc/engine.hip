@@ -101,6 +101,9 @@ struct frz_model {
   float *hidden = nullptr, *hidden_b = nullptr, *normed = nullptr, *qkv = nullptr, *attn = nullptr,
         *output = nullptr, *act = nullptr, *logits = nullptr, *partials = nullptr,
         *stats = nullptr;
+  // A split down product's later range sums (kSplitParts x 16 rows x hidden),
+  // added by the norm that reads its output.
+  float* split_parts = nullptr;
   uint32_t *topk_scratch = nullptr, *candidates = nullptr, *sampled = nullptr,
            *token_log = nullptr, *edits = nullptr;
   uint32_t token_log_capacity = 0;
@@ -125,6 +128,7 @@ struct frz_model {
     int rows = 0;
     uint32_t steps = 0, edit_stride = 0;
     bool capture = false;  // this run writes the residual capture
+    uint32_t position = 0;  // the step being enqueued: every row's position
     std::vector<uint16_t*> kcache, vcache;
     float* logits = nullptr;
     float* residuals = nullptr;
@@ -299,10 +303,15 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     return m->store + (m->slots[l].*field).first;
   };
   const float* pending = nullptr;
+  // Where the last down product left its later range sums, when it split.
+  const float* pending_parts = nullptr;
+  const size_t parts_stride = (size_t)kSplitRows * H;
   for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
     const Layer& L = m->layers[l];
     NormArgs attn_norm{L.gains[0], pending, m->output, m->hidden, m->normed,
                        c.epsilon, H, false};
+    attn_norm.parts = pending_parts;
+    attn_norm.parts_stride = parts_stride;
     if (cap) {
       attn_norm.store_x = slot(l, &frz_capture_slots::residual);
       if (l > 0) attn_norm.store_added = slot(l - 1, &frz_capture_slots::mlp_added);
@@ -326,6 +335,8 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                               vcache,      m->partials, m->partials + m->partial_floats,
                               L.slots,     L.window, c.head_dim, c.query_heads, c.kv_heads,
                               L.max_chunks, c.epsilon, scale_log2e, qkv_stride, cache_stride};
+        // The rows' position is known here: only its live chunks launch.
+        d.grid_chunks = std::min(L.max_chunks, live_chunks(v->position, L.window));
         e = launch_attention_decode(s, m->step, d, max_tokens);
       }
       if (e == hipSuccess) {
@@ -378,13 +389,22 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
       e = launch_capture_copy(s, m->step, m->act, c.ffn, c.ffn,
                               slot(l, &frz_capture_slots::neurons));
     }
-    if (e == hipSuccess)
-      e = launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
+    // Down over a step of few rows splits its tiles' ranges in halves; the
+    // next norm adds the later half's sums.
+    const bool split = max_tokens <= kSplitRows && gemv_splits(L.down, max_tokens);
+    if (e == hipSuccess) {
+      e = split ? launch_gemv_split(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens,
+                                    m->split_parts, parts_stride)
+                : launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
+    }
     pending = L.gains[5];
+    pending_parts = split ? m->split_parts : nullptr;
   }
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden, m->normed,
                         c.epsilon, H, v == nullptr};
+    final_norm.parts = pending_parts;
+    final_norm.parts_stride = parts_stride;
     if (cap) final_norm.store_added = slot(c.layers - 1, &frz_capture_slots::mlp_added);
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
@@ -818,6 +838,8 @@ int create_model(frz_device* dev, const frz_model_config& c, const frz_plan* pla
   if (int rc = working(&m->act, "activation", B * c.ffn * 4)) return bail(rc);
   if (int rc = working(&m->logits, "logits", (size_t)c.vocab * 4)) return bail(rc);
   if (int rc = alloc(m, &m->partials, (max_partials + max_partials / 64) * 4)) return bail(rc);
+  if (int rc = alloc(m, &m->split_parts, (size_t)kSplitParts * kSplitRows * c.hidden * 4))
+    return bail(rc);
   if (int rc = alloc(m, &m->topk_scratch, topk_scratch_words(c.vocab) * 4)) return bail(rc);
   if (int rc = working(&m->candidates, "candidates", 2 * kCandidates * 4)) return bail(rc);
   if (int rc = working(&m->sampled, "sampled", 4 * 4)) return bail(rc);
@@ -1592,6 +1614,7 @@ int frz_generate_variants(frz_model* m, const uint32_t* prompt, uint32_t prompt_
   for (uint32_t v = 0; v < variants; ++v) st.ids[v] = prompt[origin];
   if (int rc = put_step(m)) return rc;
   for (uint32_t t = 0; t < max_tokens; ++t) {
+    V.position = origin + t;
     if (int rc = enqueue_rows(m, (int)variants, true, &V)) return rc;
   }
   std::vector<uint32_t> log((size_t)max_tokens * variants * 2);

@@ -26,12 +26,11 @@ __device__ __forceinline__ float half_to_float(uint16_t h) {
 
 // A layer's pins on neuron n at `position` (edit.wgsl:55-76): the layer's
 // edits are sorted by neuron then first position (edit.cpp:20-31), so a
-// binary search finds the neuron's; its ranges never overlap.
-__device__ __forceinline__ float apply_edits(const uint32_t* __restrict__ t,
-                                             int layer, uint32_t n,
-                                             uint32_t position, float value) {
-  const uint32_t first = t[2 * layer];
-  const uint32_t count = t[2 * layer + 1];
+// binary search finds the neuron's; its ranges never overlap. `first` and
+// `count` are the table's words for the layer.
+__device__ __forceinline__ float apply_pin_words(const uint32_t* __restrict__ t, uint32_t first,
+                                                 uint32_t count, uint32_t n, uint32_t position,
+                                                 float value) {
   uint32_t lo = 0, hi = count;
   while (lo < hi) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -49,6 +48,11 @@ __device__ __forceinline__ float apply_edits(const uint32_t* __restrict__ t,
     }
   }
   return value;
+}
+
+__device__ __forceinline__ float apply_edits(const uint32_t* __restrict__ t, int layer, uint32_t n,
+                                             uint32_t position, float value) {
+  return apply_pin_words(t, t[2 * layer], t[2 * layer + 1], n, position, value);
 }
 
 // ---- prefill form: matrix cores ------------------------------------------
@@ -214,7 +218,6 @@ struct Schedule {
   int steps;
   uint32_t flags[kMaxSteps / 8];  // 4 bits per step
   uint32_t word[kMaxSteps * kWords];
-  int16_t pass_start[kRanges / NB + 1];  // first step of pass p; steps at the end
 };
 
 // One step's schedule words, read ahead into scalar registers.
@@ -391,24 +394,6 @@ __device__ __forceinline__ void chain_step(const Tile<NB, GATED>& T, const StepI
   wave_sync();
 }
 
-// A pass's range sums kept apart, when the passes of a tile are split over
-// the workgroup's waves: range NB p + b's sum for output (row, token) at
-// sums[(NB p + b) D^2 + row D + token].
-template <int NB>
-__device__ __forceinline__ void store_pass(typename Mfma<NB>::Acc& acc, float* sums, int pass) {
-  using M = Mfma<NB>;
-  constexpr int S = M::kSlots, D = M::kDim;
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-#pragma unroll
-    for (int o = 0; o < S; ++o)
-      sums[(NB * pass + b) * D * D + M::slot_row(lane, o) * D + lane % D] = acc[S * b + o];
-  }
-#pragma unroll
-  for (int i = 0; i < NB * S; ++i) acc[i] = 0.0f;
-}
-
 // A pass's range sums join the totals in range order.
 template <int NB>
 __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
@@ -425,44 +410,27 @@ __device__ __forceinline__ void close_pass(typename Mfma<NB>::Acc& acc,
 
 // Step t, with the schedule of steps t .. t + 2 in hand; starts reading
 // step t + 3's (first used a step later, so its wait costs nothing).
-template <int NB, bool GATED, int F, bool SPLIT>
+template <int NB, bool GATED, int F>
 __device__ __forceinline__ void run_step(const Tile<NB, GATED>& T, const Schedule<NB>& S, int t,
                                          StepInfo<NB> (&I)[4], float4 (&G)[8],
                                          const Weights<GATED, F>& W, Weights<GATED, F>& W_next,
                                          typename Mfma<NB>::Acc (&acc)[GATED ? 2 : 1],
-                                         float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots],
-                                         float* sums, int& pass) {
-  constexpr int D2 = Mfma<NB>::kDim * Mfma<NB>::kDim;
+                                         float (&total)[GATED ? 2 : 1][Mfma<NB>::kSlots]) {
   I[3] = step_info(S, t + 3);
   chain_step<NB, GATED, F>(T, I[1], I[2], G, W, W_next, acc);
   if (I[0].flags & kCloses) {
 #pragma unroll
-    for (int m = 0; m < (GATED ? 2 : 1); ++m) {
-      if constexpr (SPLIT) {
-        store_pass<NB>(acc[m], sums + m * kRanges * D2, pass);
-      } else {
-        close_pass<NB>(acc[m], total[m]);
-      }
-    }
-    ++pass;
+    for (int m = 0; m < (GATED ? 2 : 1); ++m) close_pass<NB>(acc[m], total[m]);
   }
   I[0] = I[1];
   I[1] = I[2];
   I[2] = I[3];
 }
 
-// Waves of a workgroup that split a tile's passes: one pass (four ranges)
-// a wave.
-constexpr int kSplitWaves = 8;
-
 // Grid: x = D-row tiles, y = groups of kTileWaves x D tokens, a wave's own
-// D tokens. SPLIT (one token tile, of a step of D tokens at most): y = the
-// token tile, and the workgroup's kSplitWaves waves share it, wave w taking
-// the passes from w (kRanges / NB) / kSplitWaves on; their range sums meet
-// in LDS and are added in range order, the same sums in the same order.
-// Rows and tokens past the ends are read clamped and not stored.
-template <int NB, bool GATED, int F = kQ4_0, bool SPLIT = false>
-__global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_ranges(
+// D tokens. Rows and tokens past the ends are read clamped and not stored.
+template <int NB, bool GATED, int F = kQ4_0>
+__global__ __launch_bounds__(kTileWaves * 64) void gemm_ranges(
     const DevStep* __restrict__ step, QMatrix w, QMatrix up,
     const float* __restrict__ x, int x_stride, uint32_t x_bytes, float* __restrict__ y,
     int y_stride, const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride,
@@ -471,15 +439,11 @@ __global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_
   constexpr int D = M::kDim;
   constexpr int SL = M::kSlots;
   constexpr int kMats = GATED ? 2 : 1;
-  constexpr int kWaves = SPLIT ? kSplitWaves : kTileWaves;
-  constexpr int kPassesPerWave = (kRanges / NB) / kSplitWaves;
-  static_assert(!SPLIT || (NB == 4 && kPassesPerWave >= 1), "split tiles are 16 x 16");
-  __shared__ float4 staged[kWaves][kXBuf];
-  __shared__ float sums[SPLIT ? kMats * kRanges * D * D : 1];
+  __shared__ float4 staged[kTileWaves][kXBuf];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int tokens = (int)step->tokens;
-  const int token0 = SPLIT ? (int)blockIdx.y * D : (int)(blockIdx.y * kTileWaves + wave) * D;
-  // Whole waves (whole workgroups when SPLIT) leave, before any barrier.
+  const int token0 = (int)(blockIdx.y * kTileWaves + wave) * D;
+  // Whole waves leave (there is no barrier).
   if (token0 >= tokens) return;
   const int groups = w.cols >> 5;
 
@@ -522,15 +486,11 @@ __global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_
     for (int o = 0; o < SL; ++o) total[m][o] = 0.0f;
   }
 
-  // This wave's steps: all of them, or its passes' when SPLIT.
-  int pass = SPLIT ? wave * kPassesPerWave : 0;
-  const int t0 = SPLIT ? S.pass_start[pass] : 0;
-  const int t1 = SPLIT ? S.pass_start[pass + kPassesPerWave] : S.steps;
-  // Step t0 staged; step t0 + 1's inputs and step t0's weights in registers.
+  // Step 0 staged; step 1's inputs and step 0's weights in registers.
   StepInfo<NB> I[4];
-  I[0] = step_info(S, t0);
-  I[1] = step_info(S, t0 + 1);
-  I[2] = step_info(S, t0 + 2);
+  I[0] = step_info(S, 0);
+  I[1] = step_info(S, 1);
+  I[2] = step_info(S, 2);
   float4 G[8];
   load_inputs(T, I[0], G);
   stage_inputs(T, I[0], G);
@@ -538,39 +498,10 @@ __global__ __launch_bounds__((SPLIT ? kSplitWaves : kTileWaves) * 64) void gemm_
   Weights<GATED, F> W0, W1;
   load_weights(T, I[0], W0);
   wave_sync();
-  for (int t = t0; t < t1; t += 2) {
-    run_step<NB, GATED, F, SPLIT>(T, S, t, I, G, W0, W1, acc, total, sums, pass);
-    if (t + 1 >= t1) break;
-    run_step<NB, GATED, F, SPLIT>(T, S, t + 1, I, G, W1, W0, acc, total, sums, pass);
-  }
-
-  if constexpr (SPLIT) {
-    // Output i of the tile (row i / D, token i % D): its 32 range sums in
-    // range order from +0, as the unsplit close adds them.
-    __syncthreads();
-    if (threadIdx.x >= D * D) return;
-    const int i = threadIdx.x;
-    const int tk = token0 + i % D, n = (int)blockIdx.x * D + i / D;
-    if (tk >= tokens || n >= w.rows) return;
-    float tot[kMats];
-#pragma unroll
-    for (int m = 0; m < kMats; ++m) {
-      tot[m] = 0.0f;
-#pragma unroll
-      for (int r = 0; r < kRanges; ++r) tot[m] = tot[m] + sums[(m * kRanges + r) * D * D + i];
-    }
-    float* yr = y + (size_t)tk * y_stride;
-    if (!GATED) {
-      yr[n] = tot[0];
-    } else {
-      const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tk);
-      const uint32_t* table =
-          edits && step->variants ? edits + (size_t)tk * edit_stride : edits;
-      float v = gelu_tanh(tot[0]) * tot[kMats - 1];
-      if (table) v = apply_edits(table, layer, (uint32_t)n, position, v);
-      yr[n] = v;
-    }
-    return;
+  for (int t = 0; t < S.steps; t += 2) {
+    run_step<NB, GATED, F>(T, S, t, I, G, W0, W1, acc, total);
+    if (t + 1 >= S.steps) break;
+    run_step<NB, GATED, F>(T, S, t + 1, I, G, W1, W0, acc, total);
   }
 
   const int tok = token0 + lane % D;
@@ -602,7 +533,6 @@ bool build_schedule(int groups, Schedule<NB>& S) {
   S = Schedule<NB>{};
   int t = 0;
   for (int p = 0; p < kRanges / NB; ++p) {
-    S.pass_start[p] = (int16_t)t;
     int lo[NB], len[NB], steps = 0;
     for (int b = 0; b < NB; ++b) {
       const int r = NB * p + b;
@@ -624,11 +554,350 @@ bool build_schedule(int groups, Schedule<NB>& S) {
     }
   }
   S.steps = t;
-  S.pass_start[kRanges / NB] = (int16_t)t;
   return t > 0;
 }
 
-template <int NB, bool GATED, int F = kQ4_0, bool SPLIT = false>
+// ---- steps of at most 16 rows: a pass a wave ------------------------------
+// A step of at most 16 rows (a batch of variants, a prompt's last rows) makes
+// one 16 x 16 tile per 16 output rows. A workgroup takes a tile and its eight
+// waves a pass each. A pass is any four of the 32 ranges, chained in the four
+// blocks of one v_mfma_f32_16x16x1_4b_f32 per k; the range sums meet in LDS
+// by range index and are added in range order, so which ranges share a pass
+// changes no bit, and the host puts ranges of one length together: a pass
+// runs past a range's end only where the lengths mix. Each lane loads its
+// own operands straight from memory - its row's block of its range's group
+// and its token's 32 inputs of that group, which the matrix instruction reads
+// from the lane that loaded them - and a wave keeps its loads DEPTH steps
+// ahead of its products. Loads past a range's end read zeros through the
+// buffer resources' bounds: a zero input times a zero weight adds a zero.
+constexpr int kPassWaves = kRanges / 4;
+constexpr uint32_t kPastEnd = 0x40000000u;  // an offset past every buffer here
+
+struct PassOrder {
+  uint32_t word[kPassWaves];  // byte b of word p: the range in block b of pass p
+};
+
+// Pass p's word, p wave-uniform (the selects stay scalar).
+__device__ __forceinline__ uint32_t pass_word(const PassOrder& o, int p) {
+  uint32_t v = o.word[0];
+#pragma unroll
+  for (int i = 1; i < kPassWaves; ++i) v = p == i ? o.word[i] : v;
+  return v;
+}
+
+__device__ __forceinline__ int range_lo(int r, int groups) { return (r * groups) >> 5; }
+
+template <bool GATED, int F>
+struct PassLane {
+  static constexpr int kMats = GATED ? 2 : 1;
+  __amdgpu_buffer_rsrc_t x, codes[kMats], scales[kMats];
+  uint32_t x_tok[2];  // offsets of float4 l % 8 of tokens l / 8 and 8 + l / 8
+  int lo[4], len[4];  // the pass's ranges, block by block (wave-uniform)
+  uint32_t blk0;      // the lane's row's block of its range's first group
+  int my_len;         // its range's groups
+  float4* x_put;      // where it stages its loads (+ 8 kXLine i)
+  const float4* x_get;  // its own line
+};
+
+// Step s's inputs, coalesced: instruction i reads lines 8 i .. 8 i + 7 of
+// the step (line L: block L / 16, token L % 16), 16 bytes a lane; a block
+// past its range's end reads zeros.
+template <bool GATED, int F>
+__device__ __forceinline__ void load_pass_inputs(const PassLane<GATED, F>& L, int s,
+                                                 float4 (&G)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int b = i >> 1;
+    const uint32_t at = s < L.len[b] ? 128u * (uint32_t)(L.lo[b] + s) : kPastEnd;
+    G[i] = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(L.x, L.x_tok[i & 1], (int)at, 0));
+  }
+}
+
+// Step s's weights of a lane: past its range's end, zeros.
+template <bool GATED, int F>
+__device__ __forceinline__ void load_pass_weights(const PassLane<GATED, F>& L, int s,
+                                                  Weights<GATED, F>& W) {
+  const bool live = s < L.my_len;
+  const uint32_t blk = L.blk0 + (uint32_t)s;
+#pragma unroll
+  for (int m = 0; m < PassLane<GATED, F>::kMats; ++m) {
+    if constexpr (F == kQ8_0) {
+      const uint32_t co = live ? 32u * blk : kPastEnd;
+      W.c[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(L.codes[m], co, 0, 0));
+      W.c[1] = __builtin_bit_cast(uint4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(L.codes[m], co + 16, 0, 0));
+      W.d[0] = __builtin_amdgcn_raw_buffer_load_b16(L.scales[m], live ? 2u * blk : kPastEnd, 0, 0);
+    } else if constexpr (F == kQ4_1) {
+      W.c[0] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(L.codes[m], live ? 16u * blk : kPastEnd, 0, 0));
+      W.d[0] = __builtin_amdgcn_raw_buffer_load_b32(L.scales[m], live ? 4u * blk : kPastEnd, 0, 0);
+    } else {
+      W.c[m] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(L.codes[m], live ? 16u * blk : kPastEnd, 0, 0));
+      W.d[m] = __builtin_amdgcn_raw_buffer_load_b16(L.scales[m], live ? 2u * blk : kPastEnd, 0, 0);
+    }
+  }
+}
+
+// One step: the inputs loaded for it pass through the wave's LDS lines to
+// the lanes that multiply them (a wave's LDS accesses run in order), then
+// the 32 products per block.
+template <bool GATED, int F>
+__device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const float4 (&G)[8],
+                                          const Weights<GATED, F>& W,
+                                          typename Mfma<4>::Acc (&acc)[GATED ? 2 : 1]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) L.x_put[8 * kXLine * i] = G[i];
+  wave_sync();
+  float4 xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xv[i] = L.x_get[i];
+  wave_sync();
+  chain_half<4, GATED, F, 0>(xv, W, acc);
+  chain_half<4, GATED, F, 1>(xv, W, acc);
+}
+
+// Grid: x = 16-row tiles; y = the halves of a split tile (HALVES = 2: the
+// workgroup of half h takes passes 4 h .. 4 h + 3, which hold ranges
+// 16 h .. 16 h + 15; half 0 writes their prefix to y, half 1 each range's
+// sum to parts). Rows past the end are read clamped and not stored; tokens
+// past the step's read clamped and not stored. STEPS: the longest range's
+// groups (every pass is that long or one shorter), or 0 for a loop over any
+// length.
+template <bool GATED, int F, int STEPS, int HALVES>
+__global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
+    const DevStep* __restrict__ step, QMatrix w, QMatrix up, const float* __restrict__ x,
+    int x_stride, uint32_t x_bytes, float* __restrict__ y, int y_stride,
+    const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride, PassOrder order,
+    float* __restrict__ parts, size_t parts_stride) {
+  using M = Mfma<4>;
+  constexpr int D = M::kDim, SL = M::kSlots;
+  constexpr int kMats = GATED ? 2 : 1;
+  constexpr int kWaves = kPassWaves / HALVES, kHalfRanges = kRanges / HALVES;
+  static_assert(!GATED || HALVES == 1, "a gated product combines in its workgroup");
+  // The waves' staging lines; once every chain is done, the range sums.
+  constexpr int kStageFloats = kWaves * kXBuf * 4;
+  constexpr int kSumFloats = kMats * kHalfRanges * D * D;
+  __shared__ __align__(16) float lds[kStageFloats > kSumFloats ? kStageFloats : kSumFloats];
+  float* sums = lds;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int tokens = (int)step->tokens;
+  const int groups = w.cols >> 5;
+  const int row0 = (int)blockIdx.x * D;
+
+  // The combining thread's output (row i / D, token i % D) and, gated, its
+  // table's pin words for the layer, read now and used at the end.
+  const int i_out = t & (D * D - 1);
+  const int tk_out = min(i_out % D, tokens - 1);
+  const uint32_t* table = edits && step->variants ? edits + (size_t)tk_out * edit_stride : edits;
+  uint2 pins = make_uint2(0u, 0u);
+  if (GATED) {
+    int at = 2 * layer;
+    asm volatile("" : "+v"(at));
+    const uint32_t* src = table ? table + at : reinterpret_cast<const uint32_t*>(step);
+    pins = make_uint2(src[0], src[1]);
+  }
+
+  // The pass: its four ranges and its steps, the longest of them.
+  const int half = HALVES == 1 ? 0 : (int)blockIdx.y;
+  const uint32_t word = pass_word(order, wave + kWaves * half);
+  PassLane<GATED, F> L;
+  int steps = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int r = (word >> (8 * b)) & 0xFF;
+    L.lo[b] = range_lo(r, groups);
+    L.len[b] = range_lo(r + 1, groups) - L.lo[b];
+    steps = max(steps, L.len[b]);
+  }
+  const int r = (word >> (8 * (lane >> 4))) & 0xFF;
+  const int lo = range_lo(r, groups);
+  L.my_len = range_lo(r + 1, groups) - lo;
+  const int row = min(row0 + (lane & (D - 1)), w.rows - 1);
+  // The tile's member (a product fused over members placed apart): members
+  // split at multiples of 32 rows, so a tile lies in one.
+  const MemberRow mr = member_row(w, row0);
+  const int member_rows = w.split[1] != 0 && row0 >= w.split[1] ? w.rows - w.split[1]
+                          : w.split[0] != 0 && row0 >= w.split[0]
+                              ? (w.split[1] != 0 ? w.split[1] : w.rows) - w.split[0]
+                          : w.split[0] != 0 ? w.split[0]
+                                            : w.rows;
+  const uint32_t blocks = (uint32_t)member_rows * (uint32_t)groups;
+  L.blk0 = (uint32_t)(row - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
+  L.codes[0] = buffer_of(mr.codes, (uint32_t)code_bytes(F) * blocks);
+  L.scales[0] = buffer_of(mr.scales, 2u * (uint32_t)scale_halves(F) * blocks);
+  if (GATED) {
+    L.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
+    L.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
+  }
+  L.x = buffer_of(x, x_bytes);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int tok = min(8 * h + (lane >> 3), tokens - 1);
+    L.x_tok[h] = 4u * ((uint32_t)tok * (uint32_t)x_stride + 4u * (uint32_t)(lane & 7));
+  }
+  float4* staged = reinterpret_cast<float4*>(lds) + wave * kXBuf;
+  L.x_put = staged + (lane >> 3) * kXLine + (lane & 7);
+  L.x_get = staged + lane * kXLine;
+
+  typename M::Acc acc[kMats];
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int i = 0; i < 4 * SL; ++i) acc[m][i] = 0.0f;
+  }
+  if constexpr (STEPS > 0) {
+    // Straight-line steps over a ring of kDepth operand sets: every load is
+    // issued unconditionally, so each wait is for the oldest loads only; a
+    // pass one step shorter skips its last step.
+    constexpr int kDepth = STEPS < 3 ? STEPS : 3;
+    float4 G[kDepth][8];
+    Weights<GATED, F> W[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      load_pass_inputs(L, d, G[d]);
+      load_pass_weights(L, d, W[d]);
+    }
+#pragma unroll
+    for (int k = 0; k < STEPS; ++k) {
+      if (k + 1 < STEPS || k < steps) pass_step(L, G[k % kDepth], W[k % kDepth], acc);
+      if (k + kDepth < STEPS) {
+        load_pass_inputs(L, k + kDepth, G[k % kDepth]);
+        load_pass_weights(L, k + kDepth, W[k % kDepth]);
+      }
+    }
+  } else {
+    // Any length: two operand sets, one step ahead.
+    float4 G[2][8];
+    Weights<GATED, F> W[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      load_pass_inputs(L, d, G[d]);
+      load_pass_weights(L, d, W[d]);
+    }
+    for (int k = 0; k < steps; k += 2) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        if (k + d >= steps) break;
+        pass_step(L, G[d], W[d], acc);
+        load_pass_inputs(L, k + d + 2, G[d]);
+        load_pass_weights(L, k + d + 2, W[d]);
+      }
+    }
+  }
+
+  // Range r's sum for output (row o, token j) at
+  // sums[(m kHalfRanges + r - half kHalfRanges) D^2 + o D + j].
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int rb = ((word >> (8 * b)) & 0xFF) - half * kHalfRanges;
+#pragma unroll
+      for (int o = 0; o < SL; ++o)
+        sums[(m * kHalfRanges + rb) * D * D + M::slot_row(lane, o) * D + (lane & (D - 1))] =
+            acc[m][SL * b + o];
+    }
+  }
+  __syncthreads();
+  if (t >= D * D) return;
+  const int tk = i_out % D, n = row0 + i_out / D;
+  if (tk >= tokens || n >= w.rows) return;
+  if (HALVES == 2 && half == 1) {
+#pragma unroll
+    for (int j = 0; j < kHalfRanges; ++j)
+      parts[j * parts_stride + (size_t)tk * y_stride + n] = sums[j * D * D + i_out];
+    return;
+  }
+  float tot[kMats];
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+    tot[m] = 0.0f;
+#pragma unroll
+    for (int r2 = 0; r2 < kHalfRanges; ++r2)
+      tot[m] = tot[m] + sums[(m * kHalfRanges + r2) * D * D + i_out];
+  }
+  float* yr = y + (size_t)tk * y_stride;
+  if (!GATED) {
+    yr[n] = tot[0];
+  } else {
+    const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tk);
+    float v = gelu_tanh(tot[0]) * tot[kMats - 1];
+    if (table && pins.y) v = apply_pin_words(table, pins.x, pins.y, (uint32_t)n, position, v);
+    yr[n] = v;
+  }
+}
+
+// The passes: ranges sorted by length, longest first, four a pass (each
+// half's own ranges when a tile is split in halves).
+PassOrder pass_order(int groups, int halves) {
+  int idx[kRanges];
+  for (int r = 0; r < kRanges; ++r) idx[r] = r;
+  auto len = [groups](int r) { return ((r + 1) * groups >> 5) - (r * groups >> 5); };
+  const int per = kRanges / halves;
+  for (int h = 0; h < halves; ++h)
+    std::stable_sort(idx + h * per, idx + (h + 1) * per,
+                     [&](int a, int b) { return len(a) > len(b); });
+  PassOrder o{};
+  for (int e = 0; e < kRanges; ++e) o.word[e / 4] |= (uint32_t)idx[e] << (8 * (e % 4));
+  return o;
+}
+
+template <bool GATED, int F>
+hipError_t launch_pass_tiles(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
+                             const float* x, int x_stride, float* y, int y_stride, int max_tokens,
+                             const uint32_t* edits, int layer, uint32_t edit_stride = 0,
+                             float* parts = nullptr, size_t parts_stride = 0) {
+  const int groups = w.cols >> 5;
+  const uint64_t x_bytes = 4ull * (uint64_t)x_stride * (uint64_t)max_tokens;
+  const uint64_t codes = (uint64_t)code_bytes(F) * (uint64_t)w.rows * (uint64_t)groups;
+  // Every range holds a group; offsets stay below the past-the-end one.
+  if (groups < kRanges || groups >= 0x8000 || max_tokens > Mfma<4>::kDim ||
+      x_bytes >= kPastEnd || codes >= kPastEnd) {
+    return hipErrorInvalidValue;
+  }
+  const int halves = parts ? 2 : 1;
+  const PassOrder order = pass_order(groups, halves);
+  const dim3 grid((w.rows + Mfma<4>::kDim - 1) / Mfma<4>::kDim, halves);
+  const int threads = kPassWaves / halves * 64;
+  // Straight-line forms for the lengths of the model's products (K = 1,024,
+  // 1,152 and 6,912); a loop for the others.
+  const int longest = (groups + kRanges - 1) / kRanges;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, step, w, up, x, x_stride,
+                       (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, order, parts,
+                       parts_stride);
+  };
+  if constexpr (!GATED) {
+    if (parts) {
+      if (F == kQ4_0 && longest == 7) {
+        launch(pass_tiles_kernel<GATED, F, 7, 2>);
+      } else {
+        launch(pass_tiles_kernel<GATED, F, 0, 2>);
+      }
+      return hipGetLastError();
+    }
+  }
+  if (longest == 1) {
+    launch(pass_tiles_kernel<GATED, F, 1, 1>);
+  } else if (longest == 2) {
+    launch(pass_tiles_kernel<GATED, F, 2, 1>);
+  } else {
+    if constexpr (!GATED && F == kQ4_0) {
+      if (longest == 7) {
+        launch(pass_tiles_kernel<GATED, F, 7, 1>);
+        return hipGetLastError();
+      }
+    }
+    launch(pass_tiles_kernel<GATED, F, 0, 1>);
+  }
+  return hipGetLastError();
+}
+
+template <int NB, bool GATED, int F = kQ4_0>
 hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
                          const float* x, int x_stride, float* y, int y_stride, int max_tokens,
                          const uint32_t* edits, int layer, uint32_t edit_stride = 0) {
@@ -641,23 +910,17 @@ hipError_t launch_ranges(hipStream_t s, const DevStep* step, QMatrix w, QMatrix 
       !build_schedule<NB>(groups, S)) {
     return hipErrorInvalidValue;
   }
-  // Split passes need every pass to hold work: a range of a group at least.
-  if (SPLIT && groups < kRanges) return hipErrorInvalidValue;
-  const int token_span = SPLIT ? D : kTileWaves * D;
+  const int token_span = kTileWaves * D;
   const dim3 grid((w.rows + D - 1) / D, (max_tokens + token_span - 1) / token_span);
-  hipLaunchKernelGGL((gemm_ranges<NB, GATED, F, SPLIT>), grid,
-                     dim3((SPLIT ? kSplitWaves : kTileWaves) * 64), 0, s, step, w, up, x,
-                     x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, S);
+  hipLaunchKernelGGL((gemm_ranges<NB, GATED, F>), grid, dim3(kTileWaves * 64), 0, s, step, w, up,
+                     x, x_stride, (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, S);
   return hipGetLastError();
 }
 
-// A step of at most 16 rows over K of 32 groups or more (a batch of variants)
-// fills few waves with one 16 x 16 tile each; such a step splits each tile's
-// passes over a workgroup's waves, unless the product has tiles enough to
-// fill the chip without (the 262,144-row head has 16,384).
-bool split_passes(const QMatrix& w, int max_tokens) {
-  return max_tokens <= Mfma<4>::kDim && (w.cols >> 5) >= kRanges &&
-         w.rows <= 2048 * Mfma<4>::kDim;
+// A step of at most 16 rows over K of 32 groups or more (a batch of
+// variants, a prompt's last rows) takes a pass a wave.
+bool pass_tiles(const QMatrix& w, int max_tokens) {
+  return max_tokens <= Mfma<4>::kDim && (w.cols >> 5) >= kRanges;
 }
 
 }  // namespace
@@ -679,17 +942,17 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
   // 32 x 32 tiles waste half their columns on 16 tokens or fewer.
   const bool wide = (size_t)w.rows * (size_t)max_tokens >= (size_t)768 * 1024 &&
                     max_tokens > Mfma<4>::kDim;
-  if (split_passes(w, max_tokens)) {
+  if (pass_tiles(w, max_tokens)) {
     switch (w.format) {
       case kQ4_0:
-        return launch_ranges<4, false, kQ4_0, true>(s, step, w, w, x, x_stride, y, y_stride,
-                                                    max_tokens, nullptr, 0);
+        return launch_pass_tiles<false, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                               max_tokens, nullptr, 0);
       case kQ4_1:
-        return launch_ranges<4, false, kQ4_1, true>(s, step, w, w, x, x_stride, y, y_stride,
-                                                    max_tokens, nullptr, 0);
+        return launch_pass_tiles<false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride,
+                                               max_tokens, nullptr, 0);
       case kQ8_0:
-        return launch_ranges<4, false, kQ8_0, true>(s, step, w, w, x, x_stride, y, y_stride,
-                                                    max_tokens, nullptr, 0);
+        return launch_pass_tiles<false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                               max_tokens, nullptr, 0);
       default:
         return hipErrorInvalidValue;
     }
@@ -718,6 +981,34 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
   }
 }
 
+// Splitting pays where a tile's chains are long and the tiles few: down's
+// 72 tiles of 216 groups would keep one workgroup of 8 waves on each of 72
+// CUs, two chains a SIMD; split, 144 workgroups of 4 waves take one a SIMD.
+bool gemv_splits(const QMatrix& w, int max_tokens) {
+  return max_tokens > 1 && pass_tiles(w, max_tokens) && (w.cols >> 5) >= 4 * kRanges &&
+         w.rows <= 256 * Mfma<4>::kDim && !has_members(w);
+}
+
+hipError_t launch_gemv_split(hipStream_t s, const DevStep* step, QMatrix w, const float* x,
+                             int x_stride, float* y, int y_stride, int max_tokens, float* parts,
+                             size_t parts_stride) {
+  if (!gemv_splits(w, max_tokens) || !parts)
+    return launch_gemv(s, step, w, x, x_stride, y, y_stride, max_tokens, false);
+  switch (w.format) {
+    case kQ4_0:
+      return launch_pass_tiles<false, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                             nullptr, 0, 0, parts, parts_stride);
+    case kQ4_1:
+      return launch_pass_tiles<false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                             nullptr, 0, 0, parts, parts_stride);
+    case kQ8_0:
+      return launch_pass_tiles<false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+                                             nullptr, 0, 0, parts, parts_stride);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
                         QMatrix up, const float* x, float* act,
                         int max_tokens, const uint32_t* edits, int layer, uint32_t edit_stride) {
@@ -729,9 +1020,9 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
     in.x = x;
     return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
   }
-  if (split_passes(gate, max_tokens)) {
-    return launch_ranges<4, true, kQ4_0, true>(s, step, gate, up, x, gate.cols, act, gate.rows,
-                                               max_tokens, edits, layer, edit_stride);
+  if (pass_tiles(gate, max_tokens)) {
+    return launch_pass_tiles<true, kQ4_0>(s, step, gate, up, x, gate.cols, act, gate.rows,
+                                          max_tokens, edits, layer, edit_stride);
   }
   return launch_ranges<2, true>(s, step, gate, up, x, gate.cols, act, gate.rows, max_tokens, edits,
                                layer, edit_stride);

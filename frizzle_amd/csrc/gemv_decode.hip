@@ -235,19 +235,6 @@ __device__ __forceinline__ bool norm_thread() {
 // six across the wave), so every thread gets the total with no second
 // barrier. `red` is 256 floats the call owns: a second tree uses another.
 
-// The halving tree's last six levels over a wave's 64 sums: lane l adds
-// lane l + stride for strides 32 .. 1 (strides 32 and 16 by lane swaps,
-// 8 .. 1 by DPP); lane 0's total, broadcast.
-__device__ __forceinline__ float wave_tree(float s) {
-  s = s + lane_plus32(s);
-  s = s + lane_plus16(s);
-  s = s + row_shl<8>(s);
-  s = s + row_shl<4>(s);
-  s = s + row_shl<2>(s);
-  s = s + row_shl<1>(s);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
-}
-
 template <int T>
 __device__ __forceinline__ float tree_total(float* red, const float (&lanes)[Shape<T>::kLanesPer]) {
   constexpr int LP = Shape<T>::kLanesPer;

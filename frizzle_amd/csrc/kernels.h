@@ -9,6 +9,8 @@
 namespace frz {
 
 constexpr int kRanges = 32;        // a row's K-ranges (matmul.h:88-97)
+constexpr int kSplitParts = kRanges / 2;  // range sums a split product leaves apart
+constexpr int kSplitRows = 16;            // most rows a split product takes
 constexpr int kChunkKeys = 64;     // attention chunk (attention.wgsl:60)
 constexpr int kTileKeys = 8;       // attention tile at d = 256
 constexpr int kCandidates = 64;    // top-k kept (residency/plan.h:195)
@@ -95,6 +97,15 @@ inline bool has_members(const QMatrix& w) { return w.split[0] != 0; }
 hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
                        const float* x, int x_stride, float* y, int y_stride,
                        int max_tokens, bool last_token);
+// A step of at most 16 rows over a long K may split each output's 32 ranges
+// over two workgroups: y then holds the in-order prefix of ranges 0..15 and
+// parts + j * parts_stride (y's row layout) range 16 + j's sum, for the
+// consumer to add in order (NormArgs::parts). gemv_splits says whether
+// launch_gemv_split takes that form; when it does not, it writes y whole.
+bool gemv_splits(const QMatrix& w, int max_tokens);
+hipError_t launch_gemv_split(hipStream_t s, const DevStep* step, QMatrix w, const float* x,
+                             int x_stride, float* y, int y_stride, int max_tokens, float* parts,
+                             size_t parts_stride);
 // act[t][j] = gelu_tanh(gate_j) * up_j, then layer `layer`'s pins at the
 // row's position (edit table in the reference's layout; null for none).
 // A variants step gives row r the table at edits + r * edit_stride words.
@@ -153,6 +164,11 @@ struct NormArgs {
   // (the block's output after its post-norm), written there too.
   float* store_x = nullptr;
   float* store_added = nullptr;
+  // Not null: `output` holds a split product's prefix, to which the
+  // kSplitParts range sums at parts + j * parts_stride (same row layout)
+  // are added in order.
+  const float* parts = nullptr;
+  size_t parts_stride = 0;
 };
 hipError_t launch_norm(hipStream_t s, const DevStep* step, const NormArgs& a,
                        int max_tokens);
@@ -228,7 +244,15 @@ struct DecodeAttentionArgs {
   // max_chunks (the fold's layout).
   int qkv_stride = 0;
   size_t cache_stride = 0;
+  // Chunk slots launched, when the host knows the step's position (at least
+  // the chunks live there; 0: max_chunks). The states keep max_chunks' layout.
+  int grid_chunks = 0;
 };
+// The chunks a query at position p reads under `window` (chunk_range's count).
+inline int live_chunks(uint32_t p, int window) {
+  const uint32_t earliest = p + 1 > (uint32_t)window ? p + 1 - (uint32_t)window : 0;
+  return (int)(p / kChunkKeys - earliest / kChunkKeys + 1);
+}
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
                                    const DecodeAttentionArgs& a, int rows = 1);
 

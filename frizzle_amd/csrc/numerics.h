@@ -182,6 +182,19 @@ __device__ __forceinline__ float lane_plus16(float v) {
   return b;  // rows 0 and 2: lane l + 16; rows 1 and 3: their own
 }
 
+// The last six levels of a halving tree over a wave's 64 sums (norm.wgsl:
+// 75-85): lane l adds lane l + stride for strides 32 .. 1 (32 and 16 by lane
+// swaps, 8 .. 1 by DPP); lane 0's total, broadcast.
+__device__ __forceinline__ float wave_tree(float s) {
+  s = s + lane_plus32(s);
+  s = s + lane_plus16(s);
+  s = s + row_shl<8>(s);
+  s = s + row_shl<4>(s);
+  s = s + row_shl<2>(s);
+  s = s + row_shl<1>(s);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
+}
+
 // F16 to f32, exact, subnormals kept.
 FRZ_HD float f16_unpack(uint32_t h) {
   const uint32_t sign = (h & 0x8000u) << 16;
