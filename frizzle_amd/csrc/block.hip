@@ -40,26 +40,25 @@ __device__ __forceinline__ float norm_reduce(float* partial, float v) {
 __global__ __launch_bounds__(kNormThreads) void norm_kernel(
     const DevStep* __restrict__ step, NormArgs a) {
   __shared__ float partial[2][kNormThreads];
-  const int tokens = (int)step->tokens;
-  const int row = a.last_token ? tokens - 1 : (int)blockIdx.x;
-  if (row >= tokens) return;
+  // Every load is issued first: rows of the launch past the step's are
+  // still inside the buffers (the grid is the step's most rows) and leave
+  // once their loads are out.
+  const int row = a.last_token ? (int)step->tokens - 1 : (int)blockIdx.x;
   const int vec4s = a.width / 4;
   const size_t base = (size_t)row * a.width;
   const float n = (float)a.width;
   const int i = threadIdx.x;
-  float4 x[kNormMaxVec4], y[kNormMaxVec4];
+  float4 x[kNormMaxVec4], y[kNormMaxVec4], pg[kNormMaxVec4], g[kNormMaxVec4];
   const int per = (vec4s + kNormThreads - 1) / kNormThreads;
 #pragma unroll
   for (int k = 0; k < kNormMaxVec4; ++k) {
     const int q = i + k * kNormThreads;
-    if (k < per && q < vec4s) x[k] = ld4(a.hidden + base + 4 * q);
-  }
-  if (a.post_gain) {
-#pragma unroll
-    for (int k = 0; k < kNormMaxVec4; ++k) {
-      const int q = i + k * kNormThreads;
-      if (k < per && q < vec4s) {
+    if (k < per && q < vec4s) {
+      x[k] = ld4(a.hidden + base + 4 * q);
+      g[k] = ld4(a.gain + 4 * q);
+      if (a.post_gain) {
         y[k] = ld4(a.output + base + 4 * q);
+        pg[k] = ld4(a.post_gain + 4 * q);
         // A split product's output: the prefix of its first ranges, then
         // the later range sums added in range order.
         if (a.parts) {
@@ -74,6 +73,10 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
         }
       }
     }
+  }
+  const int tokens = (int)step->tokens;
+  if (row >= tokens) return;
+  if (a.post_gain) {
     float squares = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNormMaxVec4; ++k) {
@@ -84,12 +87,11 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
     for (int k = 0; k < kNormMaxVec4; ++k) {
       const int q = i + k * kNormThreads;
       if (k < per && q < vec4s) {
-        const float4 g = ld4(a.post_gain + 4 * q);
         // ((y * r) * post_gain) * post_scale, post_scale 1 (norm.wgsl:149).
-        y[k].x = ((y[k].x * r) * g.x) * 1.0f;
-        y[k].y = ((y[k].y * r) * g.y) * 1.0f;
-        y[k].z = ((y[k].z * r) * g.z) * 1.0f;
-        y[k].w = ((y[k].w * r) * g.w) * 1.0f;
+        y[k].x = ((y[k].x * r) * pg[k].x) * 1.0f;
+        y[k].y = ((y[k].y * r) * pg[k].y) * 1.0f;
+        y[k].z = ((y[k].z * r) * pg[k].z) * 1.0f;
+        y[k].w = ((y[k].w * r) * pg[k].w) * 1.0f;
         x[k].x = x[k].x + y[k].x;
         x[k].y = x[k].y + y[k].y;
         x[k].z = x[k].z + y[k].z;
@@ -126,12 +128,11 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
   for (int k = 0; k < kNormMaxVec4; ++k) {
     const int q = i + k * kNormThreads;
     if (k < per && q < vec4s) {
-      const float4 g = ld4(a.gain + 4 * q);
       float4 o;
-      o.x = (x[k].x * r) * g.x;
-      o.y = (x[k].y * r) * g.y;
-      o.z = (x[k].z * r) * g.z;
-      o.w = (x[k].w * r) * g.w;
+      o.x = (x[k].x * r) * g[k].x;
+      o.y = (x[k].y * r) * g[k].y;
+      o.z = (x[k].z * r) * g[k].z;
+      o.w = (x[k].w * r) * g[k].w;
       st4(a.normed + base + 4 * q, o);
     }
   }

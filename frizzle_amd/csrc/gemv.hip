@@ -591,26 +591,38 @@ template <bool GATED, int F>
 struct PassLane {
   static constexpr int kMats = GATED ? 2 : 1;
   __amdgpu_buffer_rsrc_t x, codes[kMats], scales[kMats];
-  uint32_t x_tok[2];  // offsets of float4 l % 8 of tokens l / 8 and 8 + l / 8
+  uint32_t x_off[2];  // what lane l moves to LDS: tokens l / 8 and 8 + l / 8, its float4
   int lo[4], len[4];  // the pass's ranges, block by block (wave-uniform)
   uint32_t blk0;      // the lane's row's block of its range's first group
   int my_len;         // its range's groups
-  float4* x_put;      // where it stages its loads (+ 8 kXLine i)
-  const float4* x_get;  // its own line
+  uint32_t x_read;    // its own line in a wave's slot, XOR-swizzled by float4
 };
 
-// Step s's inputs, coalesced: instruction i reads lines 8 i .. 8 i + 7 of
-// the step (line L: block L / 16, token L % 16), 16 bytes a lane; a block
-// past its range's end reads zeros.
+// A step's inputs in a wave's LDS slot: line L (block L / 16, token L % 16,
+// the 32 inputs of the block's group) at L * 128 bytes, its float4 f at
+// 16 (f ^ (L % 8)) within, so that the lanes' reads of float4 f fall in
+// distinct banks. The loads go straight to LDS: instruction i writes the
+// slot's bytes 1024 i + 16 l from lane l, which is line 8 i + l / 8 (block
+// i / 2, token 8 (i % 2) + l / 8), float4 (l % 8) ^ (l / 8).
+constexpr int kSlotFloat4s = 64 * 8;
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+// 16 bytes a lane from r at voffset + soffset to lds + 16 lane.
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t r, float4* lds, uint32_t voffset,
+                                            uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voffset, (int)soffset, 0, 0);
+}
+
+// Step s's inputs into the wave's slot; a block past its range's end reads
+// zeros.
 template <bool GATED, int F>
 __device__ __forceinline__ void load_pass_inputs(const PassLane<GATED, F>& L, int s,
-                                                 float4 (&G)[8]) {
+                                                 float4* slot) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int b = i >> 1;
     const uint32_t at = s < L.len[b] ? 128u * (uint32_t)(L.lo[b] + s) : kPastEnd;
-    G[i] = __builtin_bit_cast(
-        float4, __builtin_amdgcn_raw_buffer_load_b128(L.x, L.x_tok[i & 1], (int)at, 0));
+    load_to_lds(L.x, slot + 64 * i, L.x_off[i & 1], at);
   }
 }
 
@@ -640,23 +652,24 @@ __device__ __forceinline__ void load_pass_weights(const PassLane<GATED, F>& L, i
   }
 }
 
-// One step: the inputs loaded for it pass through the wave's LDS lines to
-// the lanes that multiply them (a wave's LDS accesses run in order), then
-// the 32 products per block.
+// One step: the lane's line from the wave's slot, then the 32 products per
+// block.
 template <bool GATED, int F>
-__device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const float4 (&G)[8],
+__device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const float4* slot,
                                           const Weights<GATED, F>& W,
                                           typename Mfma<4>::Acc (&acc)[GATED ? 2 : 1]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) L.x_put[8 * kXLine * i] = G[i];
-  wave_sync();
+  const char* line = reinterpret_cast<const char*>(slot);
   float4 xv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) xv[i] = L.x_get[i];
-  wave_sync();
+  for (int f = 0; f < 8; ++f)
+    xv[f] = *reinterpret_cast<const float4*>(line + (L.x_read ^ (16u * (uint32_t)f)));
   chain_half<4, GATED, F, 0>(xv, W, acc);
   chain_half<4, GATED, F, 1>(xv, W, acc);
 }
+
+// Waits for the LDS reads in flight (lgkmcnt 0, every other count left
+// free): a slot's reads are done before new loads are aimed at it.
+__device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Grid: x = 16-row tiles; y = the halves of a split tile (HALVES = 2: the
 // workgroup of half h takes passes 4 h .. 4 h + 3, which hold ranges
@@ -666,9 +679,9 @@ __device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const flo
 // groups (every pass is that long or one shorter), or 0 for a loop over any
 // length.
 template <bool GATED, int F, int STEPS, int HALVES>
-__global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
+__global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_tiles_kernel(
     const DevStep* __restrict__ step, QMatrix w, QMatrix up, const float* __restrict__ x,
-    int x_stride, uint32_t x_bytes, float* __restrict__ y, int y_stride,
+    int x_stride, int max_tokens, float* __restrict__ y, int y_stride,
     const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride, PassOrder order,
     float* __restrict__ parts, size_t parts_stride) {
   using M = Mfma<4>;
@@ -676,21 +689,29 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
   constexpr int kMats = GATED ? 2 : 1;
   constexpr int kWaves = kPassWaves / HALVES, kHalfRanges = kRanges / HALVES;
   static_assert(!GATED || HALVES == 1, "a gated product combines in its workgroup");
-  // The waves' staging lines; once every chain is done, the range sums.
-  constexpr int kStageFloats = kWaves * kXBuf * 4;
-  constexpr int kSumFloats = kMats * kHalfRanges * D * D;
-  __shared__ __align__(16) float lds[kStageFloats > kSumFloats ? kStageFloats : kSumFloats];
-  float* sums = lds;
+  // Input slots, a wave's 8 KB each: one when a pass is at most two steps
+  // (the second reuses it), else a ring of three for four waves or two for
+  // eight (the CU's 160 KB). Separate arrays, so that a read of one waits
+  // only for its own loads.
+  constexpr int kSlots = STEPS >= 1 && STEPS <= 2 ? 1 : kWaves == 4 && STEPS > 0 ? 3 : 2;
+  __shared__ __align__(16) float4 slot0[kWaves * kSlotFloat4s];
+  __shared__ __align__(16) float4 slot1[kSlots > 1 ? kWaves * kSlotFloat4s : 1];
+  __shared__ __align__(16) float4 slot2[kSlots > 2 ? kWaves * kSlotFloat4s : 1];
+  // Once every chain is done, slot 0 holds the range sums.
+  static_assert(kMats * kHalfRanges * D * D <= 4 * kWaves * kSlotFloat4s, "sums exceed a slot");
+  float* sums = reinterpret_cast<float*>(slot0);
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int tokens = (int)step->tokens;
   const int groups = w.cols >> 5;
   const int row0 = (int)blockIdx.x * D;
+  float4* const slots[3] = {slot0 + wave * kSlotFloat4s, slot1 + (kSlots > 1 ? wave : 0) * kSlotFloat4s,
+                            slot2 + (kSlots > 2 ? wave : 0) * kSlotFloat4s};
 
   // The combining thread's output (row i / D, token i % D) and, gated, its
-  // table's pin words for the layer, read now and used at the end.
+  // table's pin words for the layer, read now and used at the end. Rows of
+  // the buffers past the step's tokens are read, not stored.
   const int i_out = t & (D * D - 1);
-  const int tk_out = min(i_out % D, tokens - 1);
+  const int tk_out = min(i_out % D, max_tokens - 1);
   const uint32_t* table = edits && step->variants ? edits + (size_t)tk_out * edit_stride : edits;
   uint2 pins = make_uint2(0u, 0u);
   if (GATED) {
@@ -732,15 +753,14 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
     L.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
     L.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
   }
-  L.x = buffer_of(x, x_bytes);
+  L.x = buffer_of(x, 4u * (uint32_t)x_stride * (uint32_t)max_tokens);
+  const uint32_t f_moved = (uint32_t)((lane & 7) ^ (lane >> 3));
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int tok = min(8 * h + (lane >> 3), tokens - 1);
-    L.x_tok[h] = 4u * ((uint32_t)tok * (uint32_t)x_stride + 4u * (uint32_t)(lane & 7));
+    const int tok = min(8 * h + (lane >> 3), max_tokens - 1);
+    L.x_off[h] = 4u * (uint32_t)tok * (uint32_t)x_stride + 16u * f_moved;
   }
-  float4* staged = reinterpret_cast<float4*>(lds) + wave * kXBuf;
-  L.x_put = staged + (lane >> 3) * kXLine + (lane & 7);
-  L.x_get = staged + lane * kXLine;
+  L.x_read = 128u * (uint32_t)lane + 16u * (uint32_t)(lane & 7);
 
   typename M::Acc acc[kMats];
 #pragma unroll
@@ -749,40 +769,61 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
     for (int i = 0; i < 4 * SL; ++i) acc[m][i] = 0.0f;
   }
   if constexpr (STEPS > 0) {
-    // Straight-line steps over a ring of kDepth operand sets: every load is
-    // issued unconditionally, so each wait is for the oldest loads only; a
-    // pass one step shorter skips its last step.
+    // Straight-line steps; every load is issued unconditionally, so each
+    // wait is for the oldest loads only. Weights ride a ring of STEPS sets
+    // (three at most); inputs a ring of kSlots slots. A pass one step
+    // shorter skips its last step's products.
     constexpr int kDepth = STEPS < 3 ? STEPS : 3;
-    float4 G[kDepth][8];
     Weights<GATED, F> W[kDepth];
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      load_pass_inputs(L, d, G[d]);
-      load_pass_weights(L, d, W[d]);
-    }
+    for (int d = 0; d < kSlots; ++d) load_pass_inputs(L, d, slots[d]);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_pass_weights(L, d, W[d]);
 #pragma unroll
     for (int k = 0; k < STEPS; ++k) {
-      if (k + 1 < STEPS || k < steps) pass_step(L, G[k % kDepth], W[k % kDepth], acc);
-      if (k + kDepth < STEPS) {
-        load_pass_inputs(L, k + kDepth, G[k % kDepth]);
-        load_pass_weights(L, k + kDepth, W[k % kDepth]);
+      const bool live = k + 1 < STEPS || k < steps;
+      if constexpr (kSlots == 1) {
+        // One slot: the next step's inputs are aimed at it once its line
+        // is read (a wave's loads complete in order of issue).
+        if (k + 1 < STEPS) {
+          const char* line = reinterpret_cast<const char*>(slots[0]);
+          float4 xv[8];
+#pragma unroll
+          for (int f = 0; f < 8; ++f)
+            xv[f] = *reinterpret_cast<const float4*>(line + (L.x_read ^ (16u * (uint32_t)f)));
+          lds_reads_done();
+          load_pass_inputs(L, k + 1, slots[0]);
+          if (live) {
+            chain_half<4, GATED, F, 0>(xv, W[k % kDepth], acc);
+            chain_half<4, GATED, F, 1>(xv, W[k % kDepth], acc);
+          }
+        } else if (live) {
+          pass_step(L, slots[0], W[k % kDepth], acc);
+        }
+      } else {
+        if (live) pass_step(L, slots[k % kSlots], W[k % kDepth], acc);
+        if (k + kSlots < STEPS) {
+          lds_reads_done();
+          load_pass_inputs(L, k + kSlots, slots[k % kSlots]);
+        }
       }
+      if (k + kDepth < STEPS) load_pass_weights(L, k + kDepth, W[k % kDepth]);
     }
   } else {
-    // Any length: two operand sets, one step ahead.
-    float4 G[2][8];
+    // Any length: two slots and two weight sets, one step ahead.
     Weights<GATED, F> W[2];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      load_pass_inputs(L, d, G[d]);
+      load_pass_inputs(L, d, slots[d]);
       load_pass_weights(L, d, W[d]);
     }
     for (int k = 0; k < steps; k += 2) {
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
         if (k + d >= steps) break;
-        pass_step(L, G[d], W[d], acc);
-        load_pass_inputs(L, k + d + 2, G[d]);
+        pass_step(L, slots[d], W[d], acc);
+        lds_reads_done();
+        load_pass_inputs(L, k + d + 2, slots[d]);
         load_pass_weights(L, k + d + 2, W[d]);
       }
     }
@@ -805,7 +846,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64) void pass_tiles_kernel(
   __syncthreads();
   if (t >= D * D) return;
   const int tk = i_out % D, n = row0 + i_out / D;
-  if (tk >= tokens || n >= w.rows) return;
+  if (tk >= (int)step->tokens || n >= w.rows) return;
   if (HALVES == 2 && half == 1) {
 #pragma unroll
     for (int j = 0; j < kHalfRanges; ++j)
@@ -867,9 +908,8 @@ hipError_t launch_pass_tiles(hipStream_t s, const DevStep* step, QMatrix w, QMat
   // 1,152 and 6,912); a loop for the others.
   const int longest = (groups + kRanges - 1) / kRanges;
   auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, step, w, up, x, x_stride,
-                       (uint32_t)x_bytes, y, y_stride, edits, layer, edit_stride, order, parts,
-                       parts_stride);
+    hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, step, w, up, x, x_stride, max_tokens, y,
+                       y_stride, edits, layer, edit_stride, order, parts, parts_stride);
   };
   if constexpr (!GATED) {
     if (parts) {
