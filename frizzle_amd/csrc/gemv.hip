@@ -593,9 +593,9 @@ struct PassLane {
   __amdgpu_buffer_rsrc_t x, codes[kMats], scales[kMats];
   uint32_t x_off[2];  // what lane l moves to LDS: tokens l / 8 and 8 + l / 8, its float4
   int lo[4], len[4];  // the pass's ranges, block by block (wave-uniform)
-  uint32_t blk0;      // the lane's row's block of its range's first group
-  int my_len;         // its range's groups
-  uint32_t x_read;    // its own line in a wave's slot, XOR-swizzled by float4
+  uint32_t blk0[kMats];  // each matrix's block of the lane's row's range's first group
+  int my_len;            // its range's groups
+  uint32_t x_read;       // its own line in a wave's slot, XOR-swizzled by float4
 };
 
 // A step's inputs in a wave's LDS slot: line L (block L / 16, token L % 16,
@@ -631,9 +631,9 @@ template <bool GATED, int F>
 __device__ __forceinline__ void load_pass_weights(const PassLane<GATED, F>& L, int s,
                                                   Weights<GATED, F>& W) {
   const bool live = s < L.my_len;
-  const uint32_t blk = L.blk0 + (uint32_t)s;
 #pragma unroll
   for (int m = 0; m < PassLane<GATED, F>::kMats; ++m) {
+    const uint32_t blk = L.blk0[m] + (uint32_t)s;
     if constexpr (F == kQ8_0) {
       const uint32_t co = live ? 32u * blk : kPastEnd;
       W.c[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(L.codes[m], co, 0, 0));
@@ -671,24 +671,30 @@ __device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const flo
 // free): a slot's reads are done before new loads are aimed at it.
 __device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Grid: x = 16-row tiles; y = the halves of a split tile (HALVES = 2: the
-// workgroup of half h takes passes 4 h .. 4 h + 3, which hold ranges
-// 16 h .. 16 h + 15; half 0 writes their prefix to y, half 1 each range's
-// sum to parts). Rows past the end are read clamped and not stored; tokens
-// past the step's read clamped and not stored. STEPS: the longest range's
-// groups (every pass is that long or one shorter), or 0 for a loop over any
-// length.
-template <bool GATED, int F, int STEPS, int HALVES>
+// What a pass kernel's two chains a lane are, when it has two: the gate and
+// up rows of one neuron (GELU and pins to close), or rows n and n + 16 of
+// one matrix (a pair of tiles on the same inputs).
+constexpr int kPlainKind = 0, kGatedKind = 1, kPairKind = 2;
+
+// Grid: x = 16-row tiles (32-row pairs); y = the halves of a split tile
+// (HALVES = 2: the workgroup of half h takes passes 4 h .. 4 h + 3, which
+// hold ranges 16 h .. 16 h + 15; half 0 writes their prefix to y, half 1
+// each range's sum to parts). Rows past the end are read clamped and not
+// stored; tokens past the step's read clamped and not stored. STEPS: the
+// longest range's groups (every pass is that long or one shorter), or 0 for
+// a loop over any length.
+template <int KIND, int F, int STEPS, int HALVES>
 __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_tiles_kernel(
     const DevStep* __restrict__ step, QMatrix w, QMatrix up, const float* __restrict__ x,
     int x_stride, int max_tokens, float* __restrict__ y, int y_stride,
     const uint32_t* __restrict__ edits, int layer, uint32_t edit_stride, PassOrder order,
     float* __restrict__ parts, size_t parts_stride) {
   using M = Mfma<4>;
+  constexpr bool GATED = KIND == kGatedKind, PAIR = KIND == kPairKind, TWO = KIND != kPlainKind;
   constexpr int D = M::kDim, SL = M::kSlots;
-  constexpr int kMats = GATED ? 2 : 1;
+  constexpr int kMats = TWO ? 2 : 1;
   constexpr int kWaves = kPassWaves / HALVES, kHalfRanges = kRanges / HALVES;
-  static_assert(!GATED || HALVES == 1, "a gated product combines in its workgroup");
+  static_assert(!TWO || HALVES == 1, "two chains a lane combine in their workgroup");
   // Input slots, a wave's 8 KB each: one when a pass is at most two steps
   // (the second reuses it), else a ring of three for four waves or two for
   // eight (the CU's 160 KB). Separate arrays, so that a read of one waits
@@ -703,7 +709,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int groups = w.cols >> 5;
-  const int row0 = (int)blockIdx.x * D;
+  const int row0 = (int)blockIdx.x * D * (PAIR ? 2 : 1);
   float4* const slots[3] = {slot0 + wave * kSlotFloat4s, slot1 + (kSlots > 1 ? wave : 0) * kSlotFloat4s,
                             slot2 + (kSlots > 2 ? wave : 0) * kSlotFloat4s};
 
@@ -724,7 +730,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   // The pass: its four ranges and its steps, the longest of them.
   const int half = HALVES == 1 ? 0 : (int)blockIdx.y;
   const uint32_t word = pass_word(order, wave + kWaves * half);
-  PassLane<GATED, F> L;
+  PassLane<TWO, F> L;
   int steps = 0;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
@@ -746,12 +752,20 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
                           : w.split[0] != 0 ? w.split[0]
                                             : w.rows;
   const uint32_t blocks = (uint32_t)member_rows * (uint32_t)groups;
-  L.blk0 = (uint32_t)(row - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
+  L.blk0[0] = (uint32_t)(row - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
   L.codes[0] = buffer_of(mr.codes, (uint32_t)code_bytes(F) * blocks);
   L.scales[0] = buffer_of(mr.scales, 2u * (uint32_t)scale_halves(F) * blocks);
   if (GATED) {
     L.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
     L.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
+    L.blk0[kMats - 1] = L.blk0[0];
+  } else if (PAIR) {
+    // The second tile's row, in the same member (members split at multiples
+    // of 32 rows).
+    const int row_b = min(row0 + D + (lane & (D - 1)), w.rows - 1);
+    L.codes[kMats - 1] = L.codes[0];
+    L.scales[kMats - 1] = L.scales[0];
+    L.blk0[kMats - 1] = (uint32_t)(row_b - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
   }
   L.x = buffer_of(x, 4u * (uint32_t)x_stride * (uint32_t)max_tokens);
   const uint32_t f_moved = (uint32_t)((lane & 7) ^ (lane >> 3));
@@ -774,7 +788,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     // (three at most); inputs a ring of kSlots slots. A pass one step
     // shorter skips its last step's products.
     constexpr int kDepth = STEPS < 3 ? STEPS : 3;
-    Weights<GATED, F> W[kDepth];
+    Weights<TWO, F> W[kDepth];
 #pragma unroll
     for (int d = 0; d < kSlots; ++d) load_pass_inputs(L, d, slots[d]);
 #pragma unroll
@@ -794,8 +808,8 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
           lds_reads_done();
           load_pass_inputs(L, k + 1, slots[0]);
           if (live) {
-            chain_half<4, GATED, F, 0>(xv, W[k % kDepth], acc);
-            chain_half<4, GATED, F, 1>(xv, W[k % kDepth], acc);
+            chain_half<4, TWO, F, 0>(xv, W[k % kDepth], acc);
+            chain_half<4, TWO, F, 1>(xv, W[k % kDepth], acc);
           }
         } else if (live) {
           pass_step(L, slots[0], W[k % kDepth], acc);
@@ -811,7 +825,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     }
   } else {
     // Any length: two slots and two weight sets, one step ahead.
-    Weights<GATED, F> W[2];
+    Weights<TWO, F> W[2];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       load_pass_inputs(L, d, slots[d]);
@@ -847,6 +861,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   if (t >= D * D) return;
   const int tk = i_out % D, n = row0 + i_out / D;
   if (tk >= (int)step->tokens || n >= w.rows) return;
+  float* yr = y + (size_t)tk * y_stride;
   if (HALVES == 2 && half == 1) {
 #pragma unroll
     for (int j = 0; j < kHalfRanges; ++j)
@@ -861,8 +876,10 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     for (int r2 = 0; r2 < kHalfRanges; ++r2)
       tot[m] = tot[m] + sums[(m * kHalfRanges + r2) * D * D + i_out];
   }
-  float* yr = y + (size_t)tk * y_stride;
-  if (!GATED) {
+  if (PAIR) {
+    yr[n] = tot[0];
+    if (n + D < w.rows) yr[n + D] = tot[1];
+  } else if (!GATED) {
     yr[n] = tot[0];
   } else {
     const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tk);
@@ -887,7 +904,7 @@ PassOrder pass_order(int groups, int halves) {
   return o;
 }
 
-template <bool GATED, int F>
+template <int KIND, int F>
 hipError_t launch_pass_tiles(hipStream_t s, const DevStep* step, QMatrix w, QMatrix up,
                              const float* x, int x_stride, float* y, int y_stride, int max_tokens,
                              const uint32_t* edits, int layer, uint32_t edit_stride = 0,
@@ -902,7 +919,8 @@ hipError_t launch_pass_tiles(hipStream_t s, const DevStep* step, QMatrix w, QMat
   }
   const int halves = parts ? 2 : 1;
   const PassOrder order = pass_order(groups, halves);
-  const dim3 grid((w.rows + Mfma<4>::kDim - 1) / Mfma<4>::kDim, halves);
+  const int rows_a_block = Mfma<4>::kDim * (KIND == kPairKind ? 2 : 1);
+  const dim3 grid((w.rows + rows_a_block - 1) / rows_a_block, halves);
   const int threads = kPassWaves / halves * 64;
   // Straight-line forms for the lengths of the model's products (K = 1,024,
   // 1,152 and 6,912); a loop for the others.
@@ -911,28 +929,28 @@ hipError_t launch_pass_tiles(hipStream_t s, const DevStep* step, QMatrix w, QMat
     hipLaunchKernelGGL(kernel, grid, dim3(threads), 0, s, step, w, up, x, x_stride, max_tokens, y,
                        y_stride, edits, layer, edit_stride, order, parts, parts_stride);
   };
-  if constexpr (!GATED) {
+  if constexpr (KIND == kPlainKind) {
     if (parts) {
       if (F == kQ4_0 && longest == 7) {
-        launch(pass_tiles_kernel<GATED, F, 7, 2>);
+        launch(pass_tiles_kernel<KIND, F, 7, 2>);
       } else {
-        launch(pass_tiles_kernel<GATED, F, 0, 2>);
+        launch(pass_tiles_kernel<KIND, F, 0, 2>);
       }
       return hipGetLastError();
     }
   }
   if (longest == 1) {
-    launch(pass_tiles_kernel<GATED, F, 1, 1>);
+    launch(pass_tiles_kernel<KIND, F, 1, 1>);
   } else if (longest == 2) {
-    launch(pass_tiles_kernel<GATED, F, 2, 1>);
+    launch(pass_tiles_kernel<KIND, F, 2, 1>);
   } else {
-    if constexpr (!GATED && F == kQ4_0) {
+    if constexpr (KIND == kPlainKind && F == kQ4_0) {
       if (longest == 7) {
-        launch(pass_tiles_kernel<GATED, F, 7, 1>);
+        launch(pass_tiles_kernel<KIND, F, 7, 1>);
         return hipGetLastError();
       }
     }
-    launch(pass_tiles_kernel<GATED, F, 0, 1>);
+    launch(pass_tiles_kernel<KIND, F, 0, 1>);
   }
   return hipGetLastError();
 }
@@ -985,14 +1003,19 @@ hipError_t launch_gemv(hipStream_t s, const DevStep* step, QMatrix w,
   if (pass_tiles(w, max_tokens)) {
     switch (w.format) {
       case kQ4_0:
-        return launch_pass_tiles<false, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride,
-                                               max_tokens, nullptr, 0);
+        // Thousands of tiles (a vocabulary's head) go a pair to a wave: half
+        // the input traffic, two chains in flight.
+        if (w.rows >= 2048 * Mfma<4>::kDim)
+          return launch_pass_tiles<kPairKind, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                                     max_tokens, nullptr, 0);
+        return launch_pass_tiles<kPlainKind, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
       case kQ4_1:
-        return launch_pass_tiles<false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride,
-                                               max_tokens, nullptr, 0);
+        return launch_pass_tiles<kPlainKind, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
       case kQ8_0:
-        return launch_pass_tiles<false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride,
-                                               max_tokens, nullptr, 0);
+        return launch_pass_tiles<kPlainKind, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride,
+                                                    max_tokens, nullptr, 0);
       default:
         return hipErrorInvalidValue;
     }
@@ -1036,13 +1059,13 @@ hipError_t launch_gemv_split(hipStream_t s, const DevStep* step, QMatrix w, cons
     return launch_gemv(s, step, w, x, x_stride, y, y_stride, max_tokens, false);
   switch (w.format) {
     case kQ4_0:
-      return launch_pass_tiles<false, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+      return launch_pass_tiles<kPlainKind, kQ4_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
                                              nullptr, 0, 0, parts, parts_stride);
     case kQ4_1:
-      return launch_pass_tiles<false, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+      return launch_pass_tiles<kPlainKind, kQ4_1>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
                                              nullptr, 0, 0, parts, parts_stride);
     case kQ8_0:
-      return launch_pass_tiles<false, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
+      return launch_pass_tiles<kPlainKind, kQ8_0>(s, step, w, w, x, x_stride, y, y_stride, max_tokens,
                                              nullptr, 0, 0, parts, parts_stride);
     default:
       return hipErrorInvalidValue;
@@ -1061,7 +1084,7 @@ hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
     return launch_gated_decode(s, step, gate, up, in, 0, act, edits, layer);
   }
   if (pass_tiles(gate, max_tokens)) {
-    return launch_pass_tiles<true, kQ4_0>(s, step, gate, up, x, gate.cols, act, gate.rows,
+    return launch_pass_tiles<kGatedKind, kQ4_0>(s, step, gate, up, x, gate.cols, act, gate.rows,
                                           max_tokens, edits, layer, edit_stride);
   }
   return launch_ranges<2, true>(s, step, gate, up, x, gate.cols, act, gate.rows, max_tokens, edits,

@@ -172,11 +172,14 @@ def test_gemv_tiled_is_decode_bits(device, rows, cols, tokens):
 
 
 @pytest.mark.parametrize("rows,cols,tokens", [(1152, 6912, 16), (1152, 1024, 2), (100, 1152, 1),
-                                               (16384 + 40, 1152, 16), (1536, 1152, 9)])
+                                               (16384 + 40, 1152, 16), (1536, 1152, 9),
+                                               (32768 + 40, 1152, 16), (32768 + 8, 1152, 3)])
 def test_gemv_split_passes_bit_exact(device, rows, cols, tokens):
     # Steps of at most 16 rows split each tile's passes over a workgroup's
     # waves; the range sums meet in LDS and are added in range order. The
-    # tokens = 1 case is the decode form (last_token).
+    # tokens = 1 case is the decode form (last_token). From 32,768 rows a
+    # wave chains two tiles over the same inputs (the last pair ragged or
+    # past the end).
     rng = np.random.default_rng(rows + 3 * tokens)
     w = q4_blocks(rng, rows, cols)
     x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
