@@ -125,9 +125,10 @@ struct Mfma<4> {
 //   fma(1024 + q, d, -1032 d) = (q - 8) d  and
 //   fma(1024 + 16 q, d / 16, -72 d) = (q - 8) d,
 // both exact: every operand and the result fit in 24 bits.
-// Half H of a group: weights 16 H .. 16 H + 15.
-template <int H>
-__device__ __forceinline__ void decode_half(uint4 c, uint16_t dbits, float (&wk)[16]) {
+// Half H of a group: weights 16 H .. 16 H + 15; words W0 .. W0 + N - 1 of
+// it (4 weights a word) into wk[0 .. 4 N - 1].
+template <int H, int W0 = 0, int N = 4>
+__device__ __forceinline__ void decode_half(uint4 c, uint16_t dbits, float (&wk)[4 * N]) {
   const float d = half_to_float(dbits);
   const float scale = H == 0 ? d : 0.0625f * d;
   const float bias = H == 0 ? -1032.0f * d : -72.0f * d;
@@ -138,14 +139,15 @@ __device__ __forceinline__ void decode_half(uint4 c, uint16_t dbits, float (&wk)
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kExp));
   constexpr uint32_t kMask = H == 0 ? 0x000F000Fu : 0x00F000F0u;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int j = 0; j < N; ++j) {
+    const uint32_t word = words[W0 + j];
     // even: bytes 0 and 2 of the word; odd: bytes 1 and 3.
-    const half2v e = __builtin_bit_cast(half2v, (words[w] & kMask) | (kExp & ~kMask));
-    const half2v o = __builtin_bit_cast(half2v, ((words[w] >> 8) & kMask) | (kExp & ~kMask));
-    wk[4 * w + 0] = __builtin_fmaf((float)e.x, scale, bias);
-    wk[4 * w + 1] = __builtin_fmaf((float)o.x, scale, bias);
-    wk[4 * w + 2] = __builtin_fmaf((float)e.y, scale, bias);
-    wk[4 * w + 3] = __builtin_fmaf((float)o.y, scale, bias);
+    const half2v e = __builtin_bit_cast(half2v, (word & kMask) | (kExp & ~kMask));
+    const half2v o = __builtin_bit_cast(half2v, ((word >> 8) & kMask) | (kExp & ~kMask));
+    wk[4 * j + 0] = __builtin_fmaf((float)e.x, scale, bias);
+    wk[4 * j + 1] = __builtin_fmaf((float)o.x, scale, bias);
+    wk[4 * j + 2] = __builtin_fmaf((float)e.y, scale, bias);
+    wk[4 * j + 3] = __builtin_fmaf((float)o.y, scale, bias);
   }
 }
 
@@ -369,6 +371,37 @@ __device__ __forceinline__ void chain_half(const float4 (&xv)[8], const Weights<
   }
 }
 
+// Two Q4_0 chains on the same inputs (gate and up, or two tiles), quarter Q
+// (8 k) of half H of a step: each chain's 8 weights decoded, then their
+// products alternating, so that neither chain waits on its own last product.
+template <int H, int Q>
+__device__ __forceinline__ void chain_quarter_two(const float4 (&xv)[8],
+                                                  const Weights<true, kQ4_0>& W,
+                                                  typename Mfma<4>::Acc (&acc)[2]) {
+  float wa[8], wb[8];
+  decode_half<H, 2 * Q, 2>(W.c[0], W.d[0], wa);
+  decode_half<H, 2 * Q, 2>(W.c[1], W.d[1], wb);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float4 x4 = xv[4 * H + 2 * Q + i];
+    const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[0] = Mfma<4>::op(wa[4 * i + j], xs[j], acc[0]);
+      acc[1] = Mfma<4>::op(wb[4 * i + j], xs[j], acc[1]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int H>
+__device__ __forceinline__ void chain_half_two(const float4 (&xv)[8], const Weights<true, kQ4_0>& W,
+                                               typename Mfma<4>::Acc (&acc)[2]) {
+  chain_quarter_two<H, 0>(xv, W, acc);
+  chain_quarter_two<H, 1>(xv, W, acc);
+}
+
 // One step: read this step's inputs from the wave's LDS buffer, then stage
 // step t + 1's there (loaded a step ago; a wave's LDS accesses run in
 // order), start the loads of step t + 2's inputs and t + 1's weights, and
@@ -574,7 +607,8 @@ constexpr int kPassWaves = kRanges / 4;
 constexpr uint32_t kPastEnd = 0x40000000u;  // an offset past every buffer here
 
 struct PassOrder {
-  uint32_t word[kPassWaves];  // byte b of word p: the range in block b of pass p
+  uint32_t word[kPassWaves];    // byte b of word p: the range in block b of pass p
+  uint32_t where[kRanges / 4];  // byte r % 4 of word r / 4: 4 p + b for range r
 };
 
 // Pass p's word, p wave-uniform (the selects stay scalar).
@@ -652,6 +686,19 @@ __device__ __forceinline__ void load_pass_weights(const PassLane<GATED, F>& L, i
   }
 }
 
+// A step's 32 products per block and chain.
+template <bool GATED, int F>
+__device__ __forceinline__ void pass_products(const float4 (&xv)[8], const Weights<GATED, F>& W,
+                                              typename Mfma<4>::Acc (&acc)[GATED ? 2 : 1]) {
+  if constexpr (GATED && F == kQ4_0) {
+    chain_half_two<0>(xv, W, acc);
+    chain_half_two<1>(xv, W, acc);
+  } else {
+    chain_half<4, GATED, F, 0>(xv, W, acc);
+    chain_half<4, GATED, F, 1>(xv, W, acc);
+  }
+}
+
 // One step: the lane's line from the wave's slot, then the 32 products per
 // block.
 template <bool GATED, int F>
@@ -663,8 +710,7 @@ __device__ __forceinline__ void pass_step(const PassLane<GATED, F>& L, const flo
 #pragma unroll
   for (int f = 0; f < 8; ++f)
     xv[f] = *reinterpret_cast<const float4*>(line + (L.x_read ^ (16u * (uint32_t)f)));
-  chain_half<4, GATED, F, 0>(xv, W, acc);
-  chain_half<4, GATED, F, 1>(xv, W, acc);
+  pass_products(xv, W, acc);
 }
 
 // Waits for the LDS reads in flight (lgkmcnt 0, every other count left
@@ -703,8 +749,8 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   __shared__ __align__(16) float4 slot0[kWaves * kSlotFloat4s];
   __shared__ __align__(16) float4 slot1[kSlots > 1 ? kWaves * kSlotFloat4s : 1];
   __shared__ __align__(16) float4 slot2[kSlots > 2 ? kWaves * kSlotFloat4s : 1];
-  // Once every chain is done, slot 0 holds the range sums.
-  static_assert(kMats * kHalfRanges * D * D <= 4 * kWaves * kSlotFloat4s, "sums exceed a slot");
+  // Once a wave's chains are done, its slot-0 region holds its range sums.
+  static_assert(kMats * 4 * D * D <= 4 * kSlotFloat4s, "a wave's sums exceed its slot");
   float* sums = reinterpret_cast<float*>(slot0);
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -713,11 +759,11 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   float4* const slots[3] = {slot0 + wave * kSlotFloat4s, slot1 + (kSlots > 1 ? wave : 0) * kSlotFloat4s,
                             slot2 + (kSlots > 2 ? wave : 0) * kSlotFloat4s};
 
-  // The combining thread's output (row i / D, token i % D) and, gated, its
+  // The combining thread's output (row i % D, token i / D) and, gated, its
   // table's pin words for the layer, read now and used at the end. Rows of
   // the buffers past the step's tokens are read, not stored.
   const int i_out = t & (D * D - 1);
-  const int tk_out = min(i_out % D, max_tokens - 1);
+  const int tk_out = min(i_out / D, max_tokens - 1);
   const uint32_t* table = edits && step->variants ? edits + (size_t)tk_out * edit_stride : edits;
   uint2 pins = make_uint2(0u, 0u);
   if (GATED) {
@@ -807,10 +853,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
             xv[f] = *reinterpret_cast<const float4*>(line + (L.x_read ^ (16u * (uint32_t)f)));
           lds_reads_done();
           load_pass_inputs(L, k + 1, slots[0]);
-          if (live) {
-            chain_half<4, TWO, F, 0>(xv, W[k % kDepth], acc);
-            chain_half<4, TWO, F, 1>(xv, W[k % kDepth], acc);
-          }
+          if (live) pass_products(xv, W[k % kDepth], acc);
         } else if (live) {
           pass_step(L, slots[0], W[k % kDepth], acc);
         }
@@ -843,29 +886,37 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     }
   }
 
-  // Range r's sum for output (row o, token j) at
-  // sums[(m kHalfRanges + r - half kHalfRanges) D^2 + o D + j].
-  __syncthreads();
+  // Each wave's range sums in its own slot-0 region (whose loads are all
+  // spent), block b of matrix m at (m 4 + b) D^2, output (row o, token j)
+  // at j D + o: a lane's four rows are one 16-byte write. Pending loads past
+  // a pass's end (the loop form's) land first.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  float* mine = sums + wave * 4 * kSlotFloat4s;
 #pragma unroll
   for (int m = 0; m < kMats; ++m) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int rb = ((word >> (8 * b)) & 0xFF) - half * kHalfRanges;
-#pragma unroll
-      for (int o = 0; o < SL; ++o)
-        sums[(m * kHalfRanges + rb) * D * D + M::slot_row(lane, o) * D + (lane & (D - 1))] =
-            acc[m][SL * b + o];
+      const float4 v = make_float4(acc[m][SL * b], acc[m][SL * b + 1], acc[m][SL * b + 2],
+                                   acc[m][SL * b + 3]);
+      *reinterpret_cast<float4*>(mine + (m * 4 + b) * D * D + (lane & (D - 1)) * D +
+                                 M::slot_row(lane, 0)) = v;
     }
   }
   __syncthreads();
   if (t >= D * D) return;
-  const int tk = i_out % D, n = row0 + i_out / D;
+  const int tk = i_out / D, n = row0 + i_out % D;
   if (tk >= (int)step->tokens || n >= w.rows) return;
   float* yr = y + (size_t)tk * y_stride;
+  // Range r's sum for the thread's output: wave p - kWaves half, block b.
+  auto range_sum = [&](int m, int r) {
+    const int e = (order.where[r >> 2] >> (8 * (r & 3))) & 0xFF;
+    const int p = (e >> 2) - kWaves * half, b = e & 3;
+    return sums[p * 4 * kSlotFloat4s + (m * 4 + b) * D * D + tk * D + i_out % D];
+  };
   if (HALVES == 2 && half == 1) {
 #pragma unroll
     for (int j = 0; j < kHalfRanges; ++j)
-      parts[j * parts_stride + (size_t)tk * y_stride + n] = sums[j * D * D + i_out];
+      parts[j * parts_stride + (size_t)tk * y_stride + n] = range_sum(0, kHalfRanges + j);
     return;
   }
   float tot[kMats];
@@ -873,8 +924,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   for (int m = 0; m < kMats; ++m) {
     tot[m] = 0.0f;
 #pragma unroll
-    for (int r2 = 0; r2 < kHalfRanges; ++r2)
-      tot[m] = tot[m] + sums[(m * kHalfRanges + r2) * D * D + i_out];
+    for (int r2 = 0; r2 < kHalfRanges; ++r2) tot[m] = tot[m] + range_sum(m, r2);
   }
   if (PAIR) {
     yr[n] = tot[0];
@@ -900,7 +950,10 @@ PassOrder pass_order(int groups, int halves) {
     std::stable_sort(idx + h * per, idx + (h + 1) * per,
                      [&](int a, int b) { return len(a) > len(b); });
   PassOrder o{};
-  for (int e = 0; e < kRanges; ++e) o.word[e / 4] |= (uint32_t)idx[e] << (8 * (e % 4));
+  for (int e = 0; e < kRanges; ++e) {
+    o.word[e / 4] |= (uint32_t)idx[e] << (8 * (e % 4));
+    o.where[idx[e] / 4] |= (uint32_t)e << (8 * (idx[e] % 4));
+  }
   return o;
 }
 
