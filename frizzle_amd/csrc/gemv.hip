@@ -914,17 +914,28 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     return sums[p * 4 * kSlotFloat4s + (m * 4 + b) * D * D + tk * D + i_out % D];
   };
   if (HALVES == 2 && half == 1) {
+    float sum[kHalfRanges];
 #pragma unroll
-    for (int j = 0; j < kHalfRanges; ++j)
-      parts[j * parts_stride + (size_t)tk * y_stride + n] = range_sum(0, kHalfRanges + j);
+    for (int j = 0; j < kHalfRanges; ++j) sum[j] = range_sum(0, kHalfRanges + j);
+#pragma unroll
+    for (int j = 0; j < kHalfRanges; ++j) parts[j * parts_stride + (size_t)tk * y_stride + n] = sum[j];
     return;
   }
+  // Every sum read before the first add: the reads overlap, the adds wait
+  // once.
+  float part[kMats][kHalfRanges];
+#pragma unroll
+  for (int m = 0; m < kMats; ++m) {
+#pragma unroll
+    for (int r2 = 0; r2 < kHalfRanges; ++r2) part[m][r2] = range_sum(m, r2);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float tot[kMats];
 #pragma unroll
   for (int m = 0; m < kMats; ++m) {
     tot[m] = 0.0f;
 #pragma unroll
-    for (int r2 = 0; r2 < kHalfRanges; ++r2) tot[m] = tot[m] + range_sum(m, r2);
+    for (int r2 = 0; r2 < kHalfRanges; ++r2) tot[m] = tot[m] + part[m][r2];
   }
   if (PAIR) {
     yr[n] = tot[0];
