@@ -425,6 +425,249 @@ attention_decode_kernel(const DevStep* __restrict__ step, DecodeAttentionArgs a)
   a.partials[slot_at * D + q * kDims + t] = o;
 }
 
+// ---- a variants step: a workgroup per (chunk, row), a wave per head --------
+// Each row of a variants step has its own caches, and the four query heads
+// share the one key/value head. A workgroup per (chunk, row) loads the
+// chunk's key and value rows straight to LDS once; wave h ropes query head h
+// (wave 0 also the step's key and value, appended to the cache by the
+// workgroup holding p), then scores head h with a lane a key: the key's 64
+// vec4 dots chained in order by its own lane, the one-token kernel's chain.
+// Its weights, state and output chains follow the one-token kernel step for
+// step, a lane four output dimensions. Rows past the chunk's end read as
+// zeros; the step's own rows sit in a spare row 64.
+namespace rows {
+constexpr int kRowBytes = D * 2;            // an F16 row
+constexpr int kGranules = kRowBytes / 16;   // its 16-byte granules
+struct Shared {
+  alignas(16) float q[QH][D];  // roped queries, times scale * log2(e)
+  alignas(16) float cosine[D / 2];
+  alignas(16) float sine[D / 2];
+};
+typedef __attribute__((address_space(3))) void* LdsPtr;
+
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsPtr)lds, 16, voffset, 0, 0, 0);
+}
+}  // namespace rows
+
+__global__ __launch_bounds__(kThreads) void attention_rows_kernel(const DevStep* __restrict__ step,
+                                                                  DecodeAttentionArgs a) {
+  using rows::kRowBytes;
+  __shared__ rows::Shared S;
+  // Key row r's granule g at r * kRowBytes + 16 (g ^ (r % 32)), so that the
+  // lanes' reads of one granule fall in distinct banks; value rows plain.
+  // Row 64 holds the step's own key and value.
+  __shared__ __align__(16) uint16_t keys[(kChunkKeys + 1) * D];
+  __shared__ __align__(16) uint16_t values[(kChunkKeys + 1) * D];
+  const int cs = blockIdx.x, row = blockIdx.y;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  a.qkv += (size_t)row * a.qkv_stride;
+  a.key_cache += (size_t)row * a.cache_stride;
+  a.value_cache += (size_t)row * a.cache_stride;
+  const bool key_lane = lane >= 32;
+  const int l = lane & 31;
+  float2 turn;
+  float4 va, vb, xa, xb, ga, gb;
+  if (w == 1) turn = ld2f(a.turns + 2 * lane);
+  {
+    const float* src = a.qkv + (key_lane ? QH : w) * D;
+    va = ld4f(src + 4 * l);
+    vb = ld4f(src + D / 2 + 4 * l);
+    const float* gain = key_lane ? a.key_gain : a.query_gain;
+    ga = ld4f(gain + 4 * l);
+    gb = ld4f(gain + D / 2 + 4 * l);
+  }
+  if (w == 0) {
+    xa = ld4f(a.qkv + (QH + 1) * D + 4 * l);
+    xb = ld4f(a.qkv + (QH + 1) * D + D / 2 + 4 * l);
+  }
+  __asm__ volatile("" ::: "memory");
+  const int p = (int)step->position;
+  const ChunkRange r = chunk_range(p, a.window, cs);
+  if (cs >= r.count) return;
+  const int valid = r.k_end - r.k_begin;
+  const bool holds_p = r.c == (p >> 6);
+  const int own = holds_p ? valid - 1 : -1;
+  const int cached = holds_p ? valid - 1 : valid;
+  const int base = ring_slot(r.k_begin, a.slots);
+  // The chunk's rows to LDS: instruction i writes rows 2 i and 2 i + 1, lane
+  // l row 2 i + l / 32's slot l % 32; each wave issues 8 for keys and 8 for
+  // values.
+  {
+    const __amdgpu_buffer_rsrc_t kres = cache_resource(a.key_cache, a.slots);
+    const __amdgpu_buffer_rsrc_t vres = cache_resource(a.value_cache, a.slots);
+    int at[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int rr = 2 * (8 * w + n) + (lane >> 5);
+      int slot = base + rr;
+      slot = slot >= a.slots ? slot - a.slots : slot;
+      at[n] = rr < cached ? slot * kRowBytes : kPastEnd;
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int i = 8 * w + n, rr = 2 * i + (lane >> 5);
+      rows::load_to_lds(kres, reinterpret_cast<char*>(keys) + 1024 * i,
+                        at[n] + 16 * ((lane & 31) ^ (rr & 31)));
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int i = 8 * w + n;
+      rows::load_to_lds(vres, reinterpret_cast<char*>(values) + 1024 * i, at[n] + 16 * (lane & 31));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (w == 1) {
+    float s0, c0, s1, c1;
+    rope_angle(turn.x, (uint32_t)p, &s0, &c0);
+    rope_angle(turn.y, (uint32_t)p, &s1, &c1);
+    *reinterpret_cast<float2*>(&S.sine[2 * lane]) = make_float2(s0, s1);
+    *reinterpret_cast<float2*>(&S.cosine[2 * lane]) = make_float2(c0, c1);
+  }
+  {
+    float sum = rope_lane_squares(va, vb);
+    sum = sum + lane_plus16(sum);
+    sum = sum + row_shl<8>(sum);
+    sum = sum + row_shl<4>(sum);
+    sum = sum + row_shl<2>(sum);
+    sum = sum + row_shl<1>(sum);
+    const int b = __builtin_bit_cast(int, sum);
+    const int lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
+    sum = __builtin_bit_cast(float, key_lane ? hi : lo);
+    rope_normalize(va, vb, sum, D, a.epsilon, ga, gb);
+  }
+  __syncthreads();  // the angles
+  rope_rotate(va, vb, l, S.cosine, S.sine);
+  if (!key_lane) {
+    const float sc = a.scale_log2e;
+    *reinterpret_cast<float4*>(&S.q[w][4 * l]) =
+        make_float4(va.x * sc, va.y * sc, va.z * sc, va.w * sc);
+    *reinterpret_cast<float4*>(&S.q[w][D / 2 + 4 * l]) =
+        make_float4(vb.x * sc, vb.y * sc, vb.z * sc, vb.w * sc);
+  } else if (w == 0 && holds_p) {
+    // The step's key and value rows to the spare row (row 64: no swizzle),
+    // and to the cache at slot p.
+    const ushort4 ka = pack4_f16(va), kb = pack4_f16(vb);
+    const ushort4 pa = pack4_f16(xa), pb = pack4_f16(xb);
+    *reinterpret_cast<ushort4*>(keys + kChunkKeys * D + 4 * l) = ka;
+    *reinterpret_cast<ushort4*>(keys + kChunkKeys * D + D / 2 + 4 * l) = kb;
+    *reinterpret_cast<ushort4*>(values + kChunkKeys * D + 4 * l) = pa;
+    *reinterpret_cast<ushort4*>(values + kChunkKeys * D + D / 2 + 4 * l) = pb;
+    const size_t at = (size_t)ring_slot(p, a.slots) * D;
+    *reinterpret_cast<ushort4*>(a.key_cache + at + 4 * l) = ka;
+    *reinterpret_cast<ushort4*>(a.key_cache + at + D / 2 + 4 * l) = kb;
+    *reinterpret_cast<ushort4*>(a.value_cache + at + 4 * l) = pa;
+    *reinterpret_cast<ushort4*>(a.value_cache + at + D / 2 + 4 * l) = pb;
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's rows landed (vmcnt 0)
+  __syncthreads();  // every wave's rows, the queries and the step's rows
+  // Key `lane`'s score for head w (attention.wgsl:277-297): s = sum over
+  // vec4s j in order of dot(q_j, k_j).
+  const float nz = negative_zero();
+  const int krow = lane == own ? kChunkKeys : lane;
+  const char* kline = reinterpret_cast<const char*>(keys) + krow * kRowBytes;
+  // Eight granules' reads at a time, then their dots.
+  float sl = 0.0f;
+#pragma unroll
+  for (int g8 = 0; g8 < rows::kGranules; g8 += 8) {
+    uint4 kk[8];
+    float4 qq[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int gi = g8 + i;
+      kk[i] = *reinterpret_cast<const uint4*>(kline + 16 * (gi ^ (krow & 31)));
+      qq[2 * i] = ld4f(&S.q[w][8 * gi]);
+      qq[2 * i + 1] = ld4f(&S.q[w][8 * gi + 4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float dd[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      dd[2 * i] = dot4_halves(qq[2 * i], kk[i].x, kk[i].y, nz);
+      dd[2 * i + 1] = dot4_halves(qq[2 * i + 1], kk[i].z, kk[i].w, nz);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sl = sl + dd[i];
+  }
+  // The weights, tile factors and l: the one-token kernel's steps.
+  const bool live = lane < valid && r.k_begin + lane + a.window > p;
+  const uint64_t live_bits = __ballot(live);
+  const int tile = lane >> 3;
+  uint64_t any = live_bits | (live_bits >> 4);
+  any |= any >> 2;
+  any |= any >> 1;
+  const uint32_t seen_tiles =
+      (uint32_t)(((any & 0x0101010101010101ull) * 0x0102040810204080ull) >> 56);
+  const bool tile_seen = (seen_tiles >> tile) & 1u;
+  const bool seen_before = (seen_tiles & ((1u << tile) - 1u)) != 0;
+  const float none = __builtin_bit_cast(float, 0x7FC00000u);
+  const float top = max8(live ? sl : none);
+  float run = tile_seen ? top : none;
+  run = __builtin_fmaxf(run, dpp_or<0x118, 0xF>(run, none));
+  run = __builtin_fmaxf(run, dpp_or<0x142, 0xA>(run, none));
+  run = __builtin_fmaxf(run, dpp_or<0x143, 0xC>(run, none));
+  const float back8 = dpp_or<0x118, 0xF>(run, none), back_row = dpp_or<0x142, 0xE>(run, none);
+  __asm__ volatile("" ::"v"(back8), "v"(back_row));
+  const float prev = (lane & 8) ? back8 : back_row;
+  const float my_top = run;
+  const float my_old = seen_before ? prev : top;
+  const bool chunk_live = seen_tiles != 0;
+  const float cm = chunk_live ? lane_value(run, 63) : 0.0f;
+  const float e = exp2_select(live ? sl - my_top : -200.0f);
+  const float fa = exp2_select(tile_seen && my_old != my_top ? my_old - my_top : 0.0f);
+  float tsum = 0.0f;
+  tsum = tsum + e;
+  tsum = tsum + row_shl<1>(e);
+  tsum = tsum + row_shl<2>(e);
+  tsum = tsum + row_shl<3>(e);
+  tsum = tsum + row_shl<4>(e);
+  tsum = tsum + row_shl<5>(e);
+  tsum = tsum + row_shl<6>(e);
+  tsum = tsum + row_shl<7>(e);
+  float cl = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < kTiles; ++tt) {
+    const float next = cl * lane_value(fa, 8 * tt) + lane_value(tsum, 8 * tt);
+    cl = (seen_tiles >> tt) & 1u ? next : cl;
+  }
+  const size_t slot_at = ((size_t)row * a.max_chunks + cs) * QH + w;
+  if (lane == 0) {
+    *reinterpret_cast<float4*>(a.stats + slot_at * 4) =
+        make_float4(cm, cl, chunk_live ? 1.0f : 0.0f, 0.0f);
+  }
+  // Output dimensions 4 lane .. 4 lane + 3: o = o a + sum_b e_b v_b per tile
+  // over all 8 tiles (keys past the chunk's end have zero weights and rows).
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int tt = 0; tt < kTiles; ++tt) {
+    // The tile's eight value rows read at once.
+    uint2 hvs[kTileKeys];
+#pragma unroll
+    for (int b = 0; b < kTileKeys; ++b) {
+      const int key = tt * kTileKeys + b;
+      const int vrow = key == own ? kChunkKeys : key;
+      hvs[b] = *reinterpret_cast<const uint2*>(values + vrow * D + 4 * lane);
+    }
+    const float at = lane_value(fa, 8 * tt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = o[j] * at;
+#pragma unroll
+    for (int b = 0; b < kTileKeys; ++b) {
+      const int key = tt * kTileKeys + b;
+      const float ek = lane_value(e, key);
+      const uint2 hv = hvs[b];
+      const _Float16 h[4] = {__builtin_bit_cast(_Float16, (uint16_t)(hv.x & 0xFFFFu)),
+                             __builtin_bit_cast(_Float16, (uint16_t)(hv.x >> 16)),
+                             __builtin_bit_cast(_Float16, (uint16_t)(hv.y & 0xFFFFu)),
+                             __builtin_bit_cast(_Float16, (uint16_t)(hv.y >> 16))};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = o[j] + __builtin_fmaf(ek, (float)h[j], nz);
+    }
+  }
+  *reinterpret_cast<float4*>(a.partials + slot_at * D + 4 * lane) =
+      make_float4(o[0], o[1], o[2], o[3]);
+}
+
 }  // namespace
 
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
@@ -436,7 +679,11 @@ hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
   // A grid of a few dozen workgroups (a sliding window, one row) is split
   // four ways by output dimension, to spread the value rows over more CUs;
   // a longer one already fills the chip.
-  if (chunks * rows <= 16) {
+  if (rows > 1 && a.qkv_stride > 0) {
+    // A variants step: a workgroup per (chunk, row), the heads sharing its
+    // rows.
+    hipLaunchKernelGGL(attention_rows_kernel, dim3(chunks, rows), dim3(kThreads), 0, s, step, a);
+  } else if (chunks * rows <= 16) {
     hipLaunchKernelGGL(attention_decode_kernel<4>, dim3(chunks, QH * 4, rows), dim3(kThreads), 0,
                        s, step, a);
   } else {

@@ -174,3 +174,29 @@ def test_timed_decode_forgets_the_prompt(device):
     assert np.array_equal(got, want), (got, want)
     model.close()
     oracle.close()
+
+
+def test_window_512_variants_bit_exact(device):
+    # Variants steps at the real window: every sliding layer reads 9 chunks
+    # (the workgroup-per-(chunk, row) attention and the 16-row products),
+    # and the ring of window + 512 slots wraps during the replies. The
+    # original and a steered variant equal the oracle's greedy runs.
+    from test_gpu_variants import seeded_variants
+    from test_gpu_model import placed
+    cfg = fz.gemma3_1b_config(layers=3, vocab=4096, window=512, pattern=3, context=2048,
+                              local_slots=1024)
+    model, oracle = build_pair(device, cfg, seed=31)
+    rng = np.random.default_rng(32)
+    prompt = rng.integers(0, cfg.vocab, 1030).astype(np.uint32)
+    variants = seeded_variants(cfg, rng, 4)
+    steps = 16
+    got = model.generate_variants(prompt, variants, max_tokens=steps)
+    for v in (0, 1):
+        o = orc.OracleModel(cfg.as_dict(), oracle.tensors)
+        o.set_edits(placed(cfg, variants[v], len(prompt) - 1))
+        end = _oracle_prompt(o, prompt)
+        want, _ = _oracle_greedy(o, end, len(prompt), steps)
+        assert np.array_equal(got[v], want), (v, got[v], want)
+        o.close()
+    model.close()
+    oracle.close()
