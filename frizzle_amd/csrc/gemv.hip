@@ -790,17 +790,22 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   L.my_len = range_lo(r + 1, groups) - lo;
   const int row = min(row0 + (lane & (D - 1)), w.rows - 1);
   // The tile's member (a product fused over members placed apart): members
-  // split at multiples of 32 rows, so a tile lies in one.
-  const MemberRow mr = member_row(w, row0);
-  const int member_rows = w.split[1] != 0 && row0 >= w.split[1] ? w.rows - w.split[1]
-                          : w.split[0] != 0 && row0 >= w.split[0]
-                              ? (w.split[1] != 0 ? w.split[1] : w.rows) - w.split[0]
-                          : w.split[0] != 0 ? w.split[0]
-                                            : w.rows;
-  const uint32_t blocks = (uint32_t)member_rows * (uint32_t)groups;
-  L.blk0[0] = (uint32_t)(row - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
-  L.codes[0] = buffer_of(mr.codes, (uint32_t)code_bytes(F) * blocks);
-  L.scales[0] = buffer_of(mr.scales, 2u * (uint32_t)scale_halves(F) * blocks);
+  // split at multiples of 32 rows, so a tile lies in one. Every candidate is
+  // read, then selected, so that the arguments' loads are one batch.
+  const int s0 = w.split[0], s1 = w.split[1], rows = w.rows;
+  const uint8_t* const codes_in[3] = {w.codes, w.member_codes[0], w.member_codes[1]};
+  const uint16_t* const scales_in[3] = {w.scales, w.member_scales[0], w.member_scales[1]};
+  const int member = s1 != 0 && row0 >= s1 ? 2 : s0 != 0 && row0 >= s0 ? 1 : 0;
+  const int member_first = member == 2 ? s1 : member == 1 ? s0 : 0;
+  const int member_end = member == 2 ? rows : member == 1 ? (s1 != 0 ? s1 : rows)
+                                     : (s0 != 0 ? s0 : rows);
+  const uint8_t* member_codes = member == 2 ? codes_in[2] : member == 1 ? codes_in[1] : codes_in[0];
+  const uint16_t* member_scales =
+      member == 2 ? scales_in[2] : member == 1 ? scales_in[1] : scales_in[0];
+  const uint32_t blocks = (uint32_t)(member_end - member_first) * (uint32_t)groups;
+  L.blk0[0] = (uint32_t)(row - member_first) * (uint32_t)groups + (uint32_t)lo;
+  L.codes[0] = buffer_of(member_codes, (uint32_t)code_bytes(F) * blocks);
+  L.scales[0] = buffer_of(member_scales, 2u * (uint32_t)scale_halves(F) * blocks);
   if (GATED) {
     L.codes[kMats - 1] = buffer_of(up.codes, 16 * blocks);
     L.scales[kMats - 1] = buffer_of(up.scales, 2 * blocks);
@@ -811,7 +816,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
     const int row_b = min(row0 + D + (lane & (D - 1)), w.rows - 1);
     L.codes[kMats - 1] = L.codes[0];
     L.scales[kMats - 1] = L.scales[0];
-    L.blk0[kMats - 1] = (uint32_t)(row_b - (row0 - mr.row)) * (uint32_t)groups + (uint32_t)lo;
+    L.blk0[kMats - 1] = (uint32_t)(row_b - member_first) * (uint32_t)groups + (uint32_t)lo;
   }
   L.x = buffer_of(x, 4u * (uint32_t)x_stride * (uint32_t)max_tokens);
   const uint32_t f_moved = (uint32_t)((lane & 7) ^ (lane >> 3));
