@@ -1,42 +1,52 @@
-// The step's chunk states for every row (a workgroup per chunk, row and
-// head), and the fold of each row's chunk states in chunk order
-// (attention.wgsl:403-438), which also serves the decode path when a row has
-// more chunks than the O product's prologue folds.
+// The step's chunk states for every row (a workgroup per chunk and row, a
+// wave per query head over the chunk's rows staged once in LDS), and the
+// fold of each row's chunk states in chunk order (attention.wgsl:403-438),
+// which also serves the decode path when a row has more chunks than the O
+// product's prologue folds.
 
-#include "attention_common.h"
+#include "attention_rows.h"
 
 namespace frz {
 namespace {
 using namespace attn;
 
-__global__ __launch_bounds__(kThreads) void attention_chunk_kernel(
+// Row `row` of the step (attention.wgsl:95-438 for one query): its query
+// heads were roped by the rope launch, and its own key and value appended,
+// so every key it reads comes from the cache. The chunk's key and value rows
+// go straight to LDS; wave w computes head w's chunk state.
+__global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
     const DevStep* __restrict__ step, AttentionArgs a) {
-  __shared__ ChunkShared S;
-  const int row = blockIdx.y;
-  if (row >= (int)step->tokens) return;
+  __shared__ __align__(16) float q[QH * D];  // the row's queries, times scale * log2(e)
+  __shared__ __align__(16) uint16_t keys[kChunkKeys * D];
+  __shared__ __align__(16) uint16_t values[kChunkKeys * D];
+  const int cs = blockIdx.x, row = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tokens = (int)step->tokens;
+  if (row >= tokens) return;
   // A variants step: every row at the step's position, over its own caches.
-  const int p = (int)step->position + (step->variants ? 0 : row);
-  const size_t cache_at = step->variants ? (size_t)row * a.cache_stride : 0;
-  const ChunkRange r = chunk_range(p, a.window, blockIdx.x);
-  if ((int)blockIdx.x >= r.count) return;
-  const int h = blockIdx.z, t = threadIdx.x;
-  uint4 kr[kKeyLoads], vr[kValueLoads];
-  float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (t < D / 4) q = ld4f(a.query + (size_t)row * a.q_stride + h * D + 4 * t);
-  key_load(kr, a.key_cache + cache_at, a.slots, r, -1);
-  value_load(vr, a.value_cache + cache_at, a.slots, r, -1);
-  if (t < D / 4) {
-    const float sc = a.scale_log2e;
-    *reinterpret_cast<float4*>(S.q + 4 * t) = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
-  }
-  value_store(S, vr, r, -1);
-  __syncthreads();
-  const size_t slot = ((size_t)row * a.max_chunks + blockIdx.x) * QH + h;
+  const bool variants = step->variants != 0;
+  const int p = (int)step->position + (variants ? 0 : row);
+  const ChunkRange r = chunk_range(p, a.window, cs);
+  if (cs >= r.count) return;
+  const size_t cache_at = variants ? (size_t)row * a.cache_stride : 0;
+  const float4 qv = ld4f(a.query + (size_t)row * a.q_stride + w * D + 4 * lane);
+  const int valid = r.k_end - r.k_begin;
+  rows::stage(a.key_cache + cache_at, a.value_cache + cache_at, a.slots, r.k_begin, valid, keys,
+              values);
+  const float sc = a.scale_log2e;
+  *reinterpret_cast<float4*>(q + w * D + 4 * lane) =
+      make_float4(qv.x * sc, qv.y * sc, qv.z * sc, qv.w * sc);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's rows landed (vmcnt 0)
+  __syncthreads();                     // every wave's rows and queries
+  const size_t slot = ((size_t)row * a.max_chunks + cs) * QH + w;
   // The last row's scores, for the capture store: keys earliest .. p.
-  const bool store = a.store_scores && row == (int)step->tokens - 1;
-  const int earliest = p + 1 - min(p + 1, a.keys);
-  chunk_state(S, kr, p, a.window, r, a.partials + slot * D, a.stats + slot * 4,
-              store ? a.store_scores + (size_t)h * a.keys : nullptr, earliest);
+  float* scores = nullptr;
+  if (a.store_scores && row == tokens - 1) {
+    const int earliest = p + 1 - min(p + 1, a.keys);
+    scores = a.store_scores + (size_t)w * a.keys + (r.k_begin - earliest);
+  }
+  rows::head_state(keys, values, q + w * D, -1, valid, r.k_begin, p, a.window,
+                   a.stats + slot * 4, a.partials + slot * D, scores);
 }
 
 // ---- fold ------------------------------------------------------------------
@@ -251,8 +261,10 @@ hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldA
 hipError_t launch_attention(hipStream_t s, const DevStep* step, const AttentionArgs& a,
                             int max_tokens) {
   if (a.head_dim != D || a.query_heads != QH || a.kv_heads != 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_chunk_kernel, dim3(a.max_chunks, max_tokens, QH), dim3(kThreads), 0,
-                     s, step, a);
+  if (a.grid_chunks < 0 || a.grid_chunks > a.max_chunks) return hipErrorInvalidValue;
+  const int chunks = a.grid_chunks > 0 ? a.grid_chunks : a.max_chunks;
+  hipLaunchKernelGGL(attention_prefill_kernel, dim3(chunks, max_tokens), dim3(kThreads), 0, s, step,
+                     a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_attention_fold(

@@ -280,6 +280,11 @@ hipError_t enqueue_readouts(frz_model* m) {
   return e;
 }
 
+// The first and last positions of a rows step's rows (-1: not known).
+struct RowSpan {
+  int64_t first = -1, last = -1;
+};
+
 // A step of several rows, in the graph's order (graph.cpp:290-470): the
 // embedding; per layer the attention norm (adding the last block's
 // post-normed output), Q/K/V, rope and the cache append, attention, O; the
@@ -288,8 +293,10 @@ hipError_t enqueue_readouts(frz_model* m) {
 // positions (the final norm and head on the last row only), or with `v` a
 // variants step: each row its own sequence over its own caches and edit
 // table, every row's logits drawn from, the residual entering each layer
-// captured.
-int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Variants* v) {
+// captured. `span`: the positions of the step's rows, when the host knows
+// them; the attention grids then cover only the chunks those rows read.
+int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Variants* v,
+                 RowSpan span = {}) {
   const frz_model_config& c = m->c;
   hipStream_t s = m->dev->stream;
   const int H = c.hidden, qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
@@ -362,6 +369,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                         m->partials, m->partials + m->partial_floats, L.slots, L.window,
                         c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
                         cache_stride};
+        if (span.first >= 0) {
+          a.grid_chunks = std::min(
+              L.max_chunks,
+              live_chunks_over((uint32_t)span.first, (uint32_t)span.last, L.window));
+        }
         if (cap) {
           a.store_scores = slot(l, &frz_capture_slots::weights);
           a.store_stats = slot(l, &frz_capture_slots::stats);
@@ -528,14 +540,15 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
 
 // `advance`: a fed decode step (logits drawn), whose last kernel advances
 // the step parameters for the next.
-int enqueue_step(frz_model* m, int max_tokens, bool logits, bool advance = false) {
+int enqueue_step(frz_model* m, int max_tokens, bool logits, bool advance = false,
+                 RowSpan span = {}) {
   // A one-token step that ends a prompt (logits, not a fed decode step that
   // advances) takes the rows path when the capture store is on: its kernels
   // write the store, and the bits are the same either way.
   const bool ends_prompt = logits && !advance;
   return max_tokens == 1 && !(ends_prompt && m->capture_on)
              ? enqueue_decode(m, logits, advance)
-             : enqueue_rows(m, max_tokens, logits, nullptr);
+             : enqueue_rows(m, max_tokens, logits, nullptr, span);
 }
 
 int build_decode_graph(frz_model* m) {
@@ -1181,7 +1194,8 @@ static int model_step(frz_model* m, uint32_t position, uint32_t tokens, const ui
   fill_sampling(s, sampling);
   std::memcpy(s.ids, ids, tokens * 4);
   if (int rc = put_step(m)) return rc;
-  return enqueue_step(m, (int)tokens, logits != 0);
+  return enqueue_step(m, (int)tokens, logits != 0, false,
+                      RowSpan{(int64_t)position, (int64_t)position + tokens - 1});
 }
 
 static int model_decode(frz_model* m, uint32_t position, uint32_t steps, const frz_sampling* sampling,
@@ -1361,7 +1375,12 @@ int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback) {
   if (decode) {
     if (int rc = launch_decode_step(m)) return rc;
   } else {
-    if (int rc = enqueue_step(m, (int)st.tokens, st.logits != 0, false)) return rc;
+    // The record is host memory, written before this call: its positions
+    // are known here.
+    const int64_t last = (int64_t)st.position + (st.variants ? 0 : (int64_t)st.tokens - 1);
+    if (int rc = enqueue_step(m, (int)st.tokens, st.logits != 0, false,
+                              RowSpan{(int64_t)st.position, last}))
+      return rc;
   }
   if (st.logits != 0 && readback) {
     return check_hip(hipMemcpyAsync(readback, m->sampled, 16, hipMemcpyDeviceToHost, s),

@@ -216,6 +216,10 @@ struct AttentionArgs {
   float* store_scores = nullptr;
   float* store_stats = nullptr;
   int keys = 0;
+  // Chunks the grid covers, when the caller knows the step's positions (0:
+  // max_chunks); rows reading more would be left out, so it must be at
+  // least live_chunks_over of the step's positions.
+  int grid_chunks = 0;
 };
 hipError_t launch_attention(hipStream_t s, const DevStep* step,
                             const AttentionArgs& a, int max_tokens);
@@ -252,6 +256,17 @@ struct DecodeAttentionArgs {
 inline int live_chunks(uint32_t p, int window) {
   const uint32_t earliest = p + 1 > (uint32_t)window ? p + 1 - (uint32_t)window : 0;
   return (int)(p / kChunkKeys - earliest / kChunkKeys + 1);
+}
+// The most chunks a query at any of positions first..last reads: a window's
+// chunk count never falls from p to p + 64 (the chunk of p + 64 is one
+// further, its earliest key's at most one), so the last 64 positions decide.
+inline int live_chunks_over(uint32_t first, uint32_t last, int window) {
+  int most = 0;
+  for (uint32_t p = last >= first + 63 ? last - 63 : first; p <= last; ++p) {
+    const int n = live_chunks(p, window);
+    most = n > most ? n : most;
+  }
+  return most;
 }
 hipError_t launch_attention_decode(hipStream_t s, const DevStep* step,
                                    const DecodeAttentionArgs& a, int rows = 1);
