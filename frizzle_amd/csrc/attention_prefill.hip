@@ -50,9 +50,8 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
 }
 
 // ---- fold ------------------------------------------------------------------
-// A workgroup folds one row's chunks for kFoldDims dimensions of one head
-// (16 for steps of up to 16 rows, whose few workgroups gain from more; 64
-// for longer steps, whose many rows would each repeat the scan 16 times). The
+// For one row (a decode token's global layers, many chunks): a workgroup
+// folds its chunks for kFoldDims dimensions of one head. The
 // chunk states are staged into LDS; the running maximum and liveness before
 // each chunk come from a wave-wide prefix scan (a maximum and an or, exact
 // in any order while no chunk maximum is NaN; with one, lane 0 replays the
@@ -239,6 +238,61 @@ __global__ __launch_bounds__(kThreads) void attention_fold_kernel(const DevStep*
   }
 }
 
+// A row's chunk states for head h folded in chunk order by one wave (lane l
+// dimensions 4 l .. 4 l + 3), the recursion replayed as written:
+// chunk c's factors (a, b) from the maximum and liveness before it
+// (fold_factors), then l = l a + l_c b and o = o a + o_c b; the output is
+// o / l, or 0 when no key was live (attention.wgsl:403-438). Steps of
+// several rows fill the chip with their rows; each lane reads its chunks'
+// states kRowBatch at a time (a 512-key window's 9 chunks in one batch).
+constexpr int kRowBatch = 16;
+__global__ __launch_bounds__(64) void attention_fold_rows_kernel(const DevStep* __restrict__ step,
+                                                                 FoldArgs f) {
+  const int row = blockIdx.x;
+  const int tokens = (int)step->tokens;
+  if (row >= tokens) return;
+  const int p = (int)step->position + (step->variants ? 0 : row);
+  const int count = chunk_range(p, f.window, 0).count;
+  const int w = blockIdx.y, lane = threadIdx.x;
+  const float* part = f.partials + (size_t)row * f.max_chunks * QH * D + w * D + 4 * lane;
+  const float* stats = f.stats + (size_t)row * f.max_chunks * QH * 4 + w * 4;
+  bool live = false;
+  float m = 0.0f, l = 0.0f;
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < count; c0 += kRowBatch) {
+    float4 st[kRowBatch], po[kRowBatch];
+#pragma unroll
+    for (int k = 0; k < kRowBatch; ++k) {
+      const int c = min(c0 + k, count - 1);
+      st[k] = ld4f(stats + (size_t)c * QH * 4);
+      po[k] = ld4f(part + (size_t)c * QH * D);
+    }
+#pragma unroll
+    for (int k = 0; k < kRowBatch; ++k) {
+      if (c0 + k < count) {
+        const bool chunk_live = st[k].z != 0.0f;
+        const Fold g = fold_factors(live, m, chunk_live, st[k].x);
+        l = l * g.a + st[k].y * g.b;
+        o[0] = o[0] * g.a + po[k].x * g.b;
+        o[1] = o[1] * g.a + po[k].y * g.b;
+        o[2] = o[2] * g.a + po[k].z * g.b;
+        o[3] = o[3] * g.a + po[k].w * g.b;
+        m = g.m;
+        live = live || chunk_live;
+      }
+    }
+  }
+  float* out = f.out + (size_t)row * QH * D + w * D + 4 * lane;
+  *reinterpret_cast<float4*>(out) = live ? make_float4(o[0] / l, o[1] / l, o[2] / l, o[3] / l)
+                                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // The last row's (m, l), for the capture store: m as the last chunk's
+  // fold leaves it.
+  if (f.store_stats && lane == 0 && row == tokens - 1) {
+    f.store_stats[2 * w] = m;
+    f.store_stats[2 * w + 1] = l;
+  }
+}
+
 }  // namespace
 
 template <int kFoldDims>
@@ -254,8 +308,14 @@ hipError_t launch_fold(hipStream_t s, const DevStep* step, const FoldArgs& f, in
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens) {
   if (f.max_chunks <= 0 || f.max_chunks > kMaxContextChunks) return hipErrorInvalidValue;
-  return max_tokens <= 16 ? launch_fold<16>(s, step, f, max_tokens)
-                          : launch_fold<64>(s, step, f, max_tokens);
+  // One row (a decode token's global layers): its chunks' factors by a
+  // scan, its dimensions over many workgroups. Several rows: a wave a row
+  // and head.
+  if (max_tokens > 1) {
+    hipLaunchKernelGGL(attention_fold_rows_kernel, dim3(max_tokens, QH), dim3(64), 0, s, step, f);
+    return hipGetLastError();
+  }
+  return launch_fold<16>(s, step, f, max_tokens);
 }
 
 hipError_t launch_attention(hipStream_t s, const DevStep* step, const AttentionArgs& a,
