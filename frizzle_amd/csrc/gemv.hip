@@ -607,8 +607,12 @@ constexpr int kPassWaves = kRanges / 4;
 constexpr uint32_t kPastEnd = 0x40000000u;  // an offset past every buffer here
 
 struct PassOrder {
-  uint32_t word[kPassWaves];    // byte b of word p: the range in block b of pass p
-  uint32_t where[kRanges / 4];  // byte r % 4 of word r / 4: 4 p + b for range r
+  uint32_t word[kPassWaves];  // byte b of word p: the range in block b of pass p
+  // Where range r's sums lie in the workgroup's LDS, in floats from the
+  // sums' base (matrix 0, output 0): pass p's block b, p within the tile's
+  // half, its wave's slot-0 region. The host computes them, so that the
+  // combine adds each range's offset to its output's.
+  uint32_t sum_at[kRanges];
 };
 
 // Pass p's word, p wave-uniform (the selects stay scalar).
@@ -764,7 +768,20 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   // the buffers past the step's tokens are read, not stored.
   const int i_out = t & (D * D - 1);
   const int tk_out = min(i_out / D, max_tokens - 1);
-  const uint32_t* table = edits && step->variants ? edits + (size_t)tk_out * edit_stride : edits;
+  // The step's fields the combine uses, loaded now through vector
+  // registers: scalar loads return out of order, so a scalar read of the
+  // step would be waited for with the arguments', before the first weight
+  // load; these land with the passes' loads, which the combine waits for.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const uint32_t* step_words = reinterpret_cast<const uint32_t*>(step) + zero;
+  const uint2 step_pt = *reinterpret_cast<const uint2*>(step_words);  // position, tokens
+  const uint32_t step_variants = GATED ? step_words[offsetof(DevStep, variants) / 4] : 0u;
+  static_assert(offsetof(DevStep, position) == 0 && offsetof(DevStep, tokens) == 4,
+                "position and tokens lead the step record");
+  // A variants step's rows each have an edit table (edit_stride apart; the
+  // stride is 0 for any other step).
+  const uint32_t* table = edits ? edits + (size_t)tk_out * edit_stride : nullptr;
   uint2 pins = make_uint2(0u, 0u);
   if (GATED) {
     int at = 2 * layer;
@@ -910,14 +927,11 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   __syncthreads();
   if (t >= D * D) return;
   const int tk = i_out / D, n = row0 + i_out % D;
-  if (tk >= (int)step->tokens || n >= w.rows) return;
+  if (tk >= (int)step_pt.y || n >= w.rows) return;
   float* yr = y + (size_t)tk * y_stride;
-  // Range r's sum for the thread's output: wave p - kWaves half, block b.
-  auto range_sum = [&](int m, int r) {
-    const int e = (order.where[r >> 2] >> (8 * (r & 3))) & 0xFF;
-    const int p = (e >> 2) - kWaves * half, b = e & 3;
-    return sums[p * 4 * kSlotFloat4s + (m * 4 + b) * D * D + tk * D + i_out % D];
-  };
+  // Range r's sum for the thread's output (token tk, row i_out % D: at
+  // i_out in a block).
+  auto range_sum = [&](int m, int r) { return sums[order.sum_at[r] + m * 4 * D * D + i_out]; };
   if (HALVES == 2 && half == 1) {
     float sum[kHalfRanges];
 #pragma unroll
@@ -948,7 +962,7 @@ __global__ __launch_bounds__(kPassWaves / HALVES * 64, 4 / HALVES) void pass_til
   } else if (!GATED) {
     yr[n] = tot[0];
   } else {
-    const uint32_t position = step->position + (step->variants ? 0u : (uint32_t)tk);
+    const uint32_t position = step_pt.x + (step_variants ? 0u : (uint32_t)tk);
     float v = gelu_tanh(tot[0]) * tot[kMats - 1];
     if (table && pins.y) v = apply_pin_words(table, pins.x, pins.y, (uint32_t)n, position, v);
     yr[n] = v;
@@ -966,9 +980,14 @@ PassOrder pass_order(int groups, int halves) {
     std::stable_sort(idx + h * per, idx + (h + 1) * per,
                      [&](int a, int b) { return len(a) > len(b); });
   PassOrder o{};
+  const int waves = kPassWaves / halves;  // a tile's workgroup: one half's passes
   for (int e = 0; e < kRanges; ++e) {
     o.word[e / 4] |= (uint32_t)idx[e] << (8 * (e % 4));
-    o.where[idx[e] / 4] |= (uint32_t)e << (8 * (idx[e] % 4));
+    // Pass e / 4 is wave (e / 4) % waves of its half's workgroup; each
+    // wave's sums sit in its slot-0 region (4 kSlotFloat4s floats), block b
+    // of matrix m at (m 4 + b) D x D.
+    o.sum_at[idx[e]] =
+        (uint32_t)(((e / 4) % waves) * 4 * kSlotFloat4s + (e % 4) * Mfma<4>::kDim * Mfma<4>::kDim);
   }
   return o;
 }

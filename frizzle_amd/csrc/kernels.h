@@ -108,7 +108,8 @@ hipError_t launch_gemv_split(hipStream_t s, const DevStep* step, QMatrix w, cons
                              size_t parts_stride);
 // act[t][j] = gelu_tanh(gate_j) * up_j, then layer `layer`'s pins at the
 // row's position (edit table in the reference's layout; null for none).
-// A variants step gives row r the table at edits + r * edit_stride words.
+// A variants step gives row r the table at edits + r * edit_stride words;
+// edit_stride is 0 for every other step.
 hipError_t launch_gated(hipStream_t s, const DevStep* step, QMatrix gate,
                         QMatrix up, const float* x, float* act,
                         int max_tokens, const uint32_t* edits, int layer,
