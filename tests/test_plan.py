@@ -296,3 +296,25 @@ def test_file_that_is_no_gemma3_is_refused():
     with pytest.raises(fp.PlanRefused) as e:
         fp.Plan(gguf.Index.read(front, size), webgpu())
     assert e.value.error == "NotDescribed" and "context_length" in e.value.subject
+
+
+def test_context_at_the_rings_edges(index, plan):
+    # The cost bends where the context reaches the sliding rings' 5,120
+    # slots: budgets a byte either side of each side of the bend, and of the
+    # trained context's whole cost.
+    fixed = _fixed(plan)
+    for c in (5119, 5120, 5121, 32767, 32768):
+        cost = fixed + 2 * 512 * (22 * min(c, 5120) + 4 * c)
+        for budget in (cost - 1, cost, cost + 1):
+            got = fp.Plan(index, webgpu(), fp.policy(memory_budget=budget))
+            assert got.context_offered == _context_for(fixed, budget), (c, budget)
+
+
+def test_context_held_to_what_a_binding_holds(index):
+    # With 15 MiB bindings a global layer's keys (512 bytes a slot) hold at
+    # most 30,720 slots, whatever the budget allows; the sliding rings' 5,120
+    # slots (2.5 MiB) are unaffected.
+    p = fp.Plan(index, fp.limits(300 * MIB, 15 * MIB, 16), fp.policy(memory_budget=8 << 30))
+    assert p.context_offered == 30720
+    assert p.cache(5)[2] == 30720 and p.cache(5)[0][2] == 15 * MIB
+    assert p.cache(0)[2] == 5120
