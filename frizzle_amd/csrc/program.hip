@@ -14,7 +14,9 @@
 // event; poll reports settled steps in run order on the caller's thread.
 
 #include <algorithm>
+#include <cstddef>
 #include <cstring>
+#include <type_traits>
 #include <string>
 #include <vector>
 
@@ -236,6 +238,24 @@ bool launch_ok(const frz_launch& l, uint32_t i, const std::vector<uint64_t>& siz
   if (l.binding_count > 0 && !l.bindings) {
     why = at + ": bindings missing";
     return false;
+  }
+  if (l.override_count > 0 && !l.overrides) {
+    why = at + ": overrides missing";
+    return false;
+  }
+  for (uint32_t o = 0; o < l.override_count; ++o) {
+    const char* name = l.overrides[o].name;
+    if (!name) {
+      why = at + ": override " + std::to_string(o) + " has no name";
+      return false;
+    }
+    bool twice = false;
+    for (uint32_t e = 0; e < o && !twice; ++e)
+      twice = l.overrides[e].name && std::strcmp(l.overrides[e].name, name) == 0;
+    if (twice || std::strcmp(name, "workgroup_size") == 0 || std::strcmp(name, "last_token") == 0) {
+      why = at + ": override " + name + (twice ? " given twice" : " is the program's to set");
+      return false;
+    }
   }
   for (uint32_t b = 0; b < l.binding_count; ++b) {
     const frz_binding& x = l.bindings[b];
@@ -483,6 +503,31 @@ int frz_program_build(frz_model* upload, const frz_plan* plan, const frz_launch*
   return FRZ_OK;
 }
 
+// The step record's 64-byte head (interface.h:163-188) is copied whole into
+// DevStep's first 64 bytes: the fields must lie alike, with the ids at 64.
+#define FRZ_SAME_FIELD(f)                                                        \
+  static_assert(offsetof(DevStep, f) == offsetof(frz_step_record, f) &&         \
+                    sizeof(DevStep::f) == sizeof(frz_step_record::f),            \
+                "DevStep and frz_step_record differ at " #f)
+FRZ_SAME_FIELD(position);
+FRZ_SAME_FIELD(tokens);
+FRZ_SAME_FIELD(logits);
+FRZ_SAME_FIELD(fed);
+FRZ_SAME_FIELD(seed);
+FRZ_SAME_FIELD(top_k);
+FRZ_SAME_FIELD(temperature);
+FRZ_SAME_FIELD(top_p);
+FRZ_SAME_FIELD(min_p);
+FRZ_SAME_FIELD(log_min_p);
+FRZ_SAME_FIELD(ids);
+#undef FRZ_SAME_FIELD
+static_assert(offsetof(DevStep, log_min_p) == 40 && offsetof(DevStep, ids) == 64,
+              "the step head is 64 bytes, log_min_p its eleventh word");
+static_assert(std::is_same<decltype(DevStep::temperature), decltype(frz_step_record::temperature)>::value &&
+                  std::is_same<decltype(DevStep::log_min_p), decltype(frz_step_record::log_min_p)>::value &&
+                  std::is_same<decltype(DevStep::top_k), decltype(frz_step_record::top_k)>::value,
+              "the step head's fields have the record's types");
+
 int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_input* inputs,
                     uint32_t input_count, frz_step_callback done, void* userdata) {
   if (!p || !step) return fail(FRZ_ERR_ARGUMENT, "frz_program_run: null argument");
@@ -507,6 +552,12 @@ int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_i
       (uint64_t)step->position + step->tokens > p->context) {
     s.status = FRZ_ERR_STEP;
     s.message = "a step past the context";
+    return FRZ_OK;
+  }
+  if (step->fed && step->tokens != 1) {
+    s.status = FRZ_ERR_STEP;
+    s.message = "a fed step of " + std::to_string(step->tokens) +
+                " tokens (a fed step is one token, the last step's draw)";
     return FRZ_OK;
   }
   size_t input_bytes = 0;

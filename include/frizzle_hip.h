@@ -774,6 +774,15 @@ typedef struct frz_binding {
   uint64_t offset;
   uint64_t size;
 } frz_binding;
+/* kernels::Override (interface.h:310-314): a WGSL override constant and its
+ * value. This backend's kernels are compiled for the Gemma 3 shapes and take
+ * none: a build makes Program::build's checks of a launch's overrides
+ * (program.cpp:432-444: "workgroup_size" and "last_token" are the program's
+ * to set, and no name is given twice), then ignores them by name. */
+typedef struct frz_override {
+  const char* name;
+  double value;
+} frz_override;
 /* kernels::Launch. `role` and `layer` are the graph's names (graph.h). */
 typedef struct frz_launch {
   int kernel;              /* frz_kernel */
@@ -794,6 +803,8 @@ typedef struct frz_launch {
   uint32_t tokens_least, tokens_most; /* the steps it runs in, by token count */
   const char* role;
   uint32_t layer;          /* FRZ_NO_LAYER for the embedding and the output */
+  const frz_override* overrides; /* Launch::overrides, interface.h:335 */
+  uint32_t override_count;
 } frz_launch;
 /* kernels::Step: the 64-byte head (sampler::apply's settings and seed) and
  * the step's token ids. */

@@ -149,6 +149,15 @@ def test_program_refusals_and_order(device, setup):
     assert [(r[0], r[3]) for r in prog.reports[n:]] == [(fprog.STEP, 4), (fprog.STEP, 5)]
     assert "past the context" in prog.reports[n][1]
     assert "outside its buffer" in prog.reports[n + 1][1]
+    # a fed step is one token, the last step's draw: a fed step of 3 tokens
+    # fails, reported in order, nothing run
+    n = len(prog.reports)
+    rec = fprog.step_record(20, fed=True, logits=True)
+    rec.tokens = 3
+    assert prog.run(rec, tag=6) == 0
+    prog.poll(wait=True)
+    assert [(r[0], r[3]) for r in prog.reports[n:]] == [(fprog.STEP, 6)]
+    assert "a fed step of 3 tokens" in prog.reports[n][1]
     prog.close()
     a.close()
 

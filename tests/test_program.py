@@ -120,3 +120,25 @@ def test_an_ungrouped_plan_is_refused(launches):
     p = fp.Plan(pinned_index(q_format=8), fp.limits(1 << 40, 1 << 40, 256))
     ls, rb = launches
     _refused(p, ls, rb, "did not group Q, K and V of layer 0")
+
+
+def test_overrides_are_accepted_and_checked(plan, launches):
+    # kernels::Launch::overrides (interface.h:310-338): the graph's
+    # launches carry the launchers' shape and tile overrides, which this
+    # backend accepts and ignores by name; Program::build's refusals
+    # (program.cpp:432-444) hold: the program's own names, a name twice.
+    ls, rb = copy.deepcopy(launches)
+    assert sum(len(l.overrides) for l in ls) > 0
+    assert fprog.check_launches(plan, ls, rb) == (0, "")
+    i = _index(ls, "ffn.down", 2)
+    ls[i].overrides = [("columns", 6912.0), ("anything_else", 1.5)]
+    assert fprog.check_launches(plan, ls, rb) == (0, "")
+    for bad, match in (([("workgroup_size", 64.0)], "override workgroup_size is the program's to set"),
+                       ([("last_token", 1.0)], "override last_token is the program's to set"),
+                       ([("columns", 1.0), ("tile_tokens", 8.0), ("columns", 2.0)],
+                        "override columns given twice"),
+                       ([(None, 1.0)], "override 0 has no name")):
+        ls2 = copy.deepcopy(ls)
+        ls2[i].overrides = bad
+        msg = _refused(plan, ls2, rb, match)
+        assert msg.startswith(f"launch {i}")
