@@ -510,3 +510,138 @@ def test_model_block_is_token_by_token(window, slots, pattern, blocks):
         at += n
     a.close()
     b.close()
+
+
+# ---- which layers are global, their windows and rope bases ----------------------------
+#
+# gemma3.cpp:79-85: layer l attends to the whole context, with rope base 1e6,
+# when l % pattern == pattern - 1; every other layer attends to the last
+# `window` keys with base 1e4. The cases below recompute a layer's attention
+# in f64 from already pinned primitives (the product, the norm, F16
+# rounding) and the closed forms of QK-norm, rope and softmax, and require
+# the oracle to agree within a tolerance far below what the other window or
+# base would change.
+
+def _f16(x):
+    return np.clip(np.asarray(x, np.float64), -65504, 65504).astype(np.float16).astype(np.float64)
+
+
+def _qk_norm_rope(x, gain, position, base, eps=1e-6):
+    """One head's QK-norm and rope in f64: pairs (k, k + d/2) turned by
+    position * base^(-2k/d)."""
+    x = np.asarray(x, np.float64)
+    d = x.size
+    y = x / np.sqrt(np.mean(x * x) + eps) * np.asarray(gain, np.float64)
+    ang = position * np.power(float(base), -2.0 * np.arange(d // 2) / d)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = y[:d // 2], y[d // 2:]
+    return np.concatenate([a * c - b * s, a * s + b * c])
+
+
+def _attention_f64(cfg, t, layer, xs, position, base, window):
+    """Layer `layer`'s attention output (before O) at `position`, in f64,
+    from the residuals `xs[j]` entering it at positions 0..position: the
+    keys read are j in (position - window, position]."""
+    d, H = cfg.head_dim, cfg.query_heads
+    qs, ks, vs = [], [], []
+    for j in range(position + 1):
+        _, n = orc.norm_row(t[(layer, "attn_norm")], xs[j])
+        q = orc.gemv(t[(layer, "q")], H * d, cfg.hidden, n)
+        k = orc.gemv(t[(layer, "k")], d, cfg.hidden, n)
+        v = orc.gemv(t[(layer, "v")], d, cfg.hidden, n)
+        ks.append(_f16(_qk_norm_rope(k, t[(layer, "k_norm")], j, base)))
+        vs.append(_f16(v))
+        qs.append(q)
+    lo = max(0, position - window + 1)
+    K, V = np.array(ks[lo:]), np.array(vs[lo:])
+    out = []
+    for h in range(H):
+        q = _qk_norm_rope(qs[position][h * d:(h + 1) * d], t[(layer, "q_norm")], position, base)
+        s = K @ q / 16.0
+        w = np.exp(s - s.max())
+        out.append((w / w.sum()) @ V)
+    return np.concatenate(out).astype(F)
+
+
+def _block_residual(cfg, t, layer, x, attn):
+    """The residual after `layer`'s attention block: O of `attn`,
+    post-normed, added at the feed-forward norm."""
+    o = orc.gemv(t[(layer, "o")], cfg.hidden, cfg.query_heads * cfg.head_dim, attn)
+    h, _ = orc.norm_row(t[(layer, "ffn_norm")], x, o, t[(layer, "post_attn_norm")])
+    return h
+
+
+def _close(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / np.max(np.abs(b)))
+
+
+def test_model_local_window_and_global_context():
+    # Pattern 2: layer 0 slides over 64 keys, layer 1 (l % 2 == 1) reads the
+    # whole context. V and O live in both, Q and K zero, so each attention
+    # averages the F16 values it reads. At position 100 the local layer must
+    # average the last 64 values and the global layer all 101.
+    cfg = _cfg()
+    t = _tensors(cfg, 54, live={(0, "v"), (0, "o"), (1, "v"), (1, "o")})
+    # the last block's output seen through the logits, not hidden under the
+    # residual's own embedding row
+    t[(1, "post_attn_norm")] = (t[(1, "post_attn_norm")] * F(32.0)).astype(F)
+    m = orc.OracleModel(cfg.as_dict(), t)
+    m.set_edits(np.zeros(2 * cfg.layers, np.uint32))
+    ids = np.random.default_rng(55).integers(0, cfg.vocab, 101)
+    xs, h1s = [], []
+    for p, tok in enumerate(ids):
+        got = m.token(int(tok), p)
+        xs.append(_embed(cfg, t, int(tok)))
+        h1s.append(m.residuals()[1])
+    P = 100
+
+    def layer0(window):
+        return _block_residual(cfg, t, 0, xs[P], _attention_f64(cfg, t, 0, xs, P, 1e4, window))
+
+    want, other = layer0(64), layer0(101)
+    assert _close(h1s[P], want) < 1e-5
+    assert _close(other, want) > 1e-2  # the window is visible
+    # the global layer over the oracle's own residuals entering it
+
+    def logits(window):
+        h2 = _block_residual(cfg, t, 1, h1s[P], _attention_f64(cfg, t, 1, h1s, P, 1e6, window))
+        return _head(cfg, t, h2, np.zeros(cfg.hidden, F), t[(1, "post_ffn_norm")])
+
+    want, other = logits(101), logits(64)
+    assert _close(got, want) < 1e-4
+    assert _close(other, want) > 1e-2
+    m.close()
+
+
+@pytest.mark.parametrize("layer,base,wrong", [(0, 1e4, 1e6), (1, 1e6, 1e4)])
+def test_model_rope_base_by_layer(layer, base, wrong):
+    # Only `layer`'s Q, K, V and O are live (every score depends on the
+    # positions through rope): the local layer turns by base 1e4, the global
+    # one by 1e6, and the other base moves the output far past the
+    # tolerance.
+    cfg = _cfg()
+    t = _tensors(cfg, 56, live={(layer, r) for r in ("q", "k", "v", "o")})
+    t[(1, "post_attn_norm")] = (t[(1, "post_attn_norm")] * F(32.0)).astype(F)
+    m = orc.OracleModel(cfg.as_dict(), t)
+    m.set_edits(np.zeros(2 * cfg.layers, np.uint32))
+    ids = np.random.default_rng(57).integers(0, cfg.vocab, 41)
+    xs = []
+    for p, tok in enumerate(ids):
+        got = m.token(int(tok), p)
+        xs.append(_embed(cfg, t, int(tok)))
+    P = 40
+    if layer == 0:
+        res = m.residuals()[1]
+
+        def check(b):
+            return _block_residual(cfg, t, 0, xs[P], _attention_f64(cfg, t, 0, xs, P, b, 64))
+    else:
+        res = got
+
+        def check(b):
+            h2 = _block_residual(cfg, t, 1, xs[P], _attention_f64(cfg, t, 1, xs, P, b, 512))
+            return _head(cfg, t, h2, np.zeros(cfg.hidden, F), t[(1, "post_ffn_norm")])
+    want = check(base)
+    assert _close(res, want) < 1e-4
+    assert _close(check(wrong), want) > 1e-2
+    m.close()
