@@ -89,7 +89,9 @@ def parse():
                         "graph-replayed) and streaming reads of each decode product's "
                         "weight bytes (one JSON line)")
     p.add_argument("--gemv-stream", action="store_true",
-                   help="time the GEMV launches on the stream, not replayed from a graph")
+                   help="with --roofline-only, time the GEMV launches back to back on the "
+                        "stream (not each between its own events); with --probes, the "
+                        "floors on the stream (not graph-replayed)")
     return p.parse_args()
 
 
@@ -127,7 +129,12 @@ def synth_all(fz, cfg, seed):
     return t
 
 
-def gemv_roofline(fz, dev, copies, iters, seed, graph=True):
+# frz_bench_gemv's timing modes: launches replayed from a graph, or launched
+# on the stream, back to back either way.
+GRAPH, STREAM = 1, 0
+
+
+def gemv_roofline(fz, dev, copies, iters, seed, mode=STREAM):
     import ctypes
     rng = np.random.default_rng(seed + 1)
     blocks = GEMV_ROWS * GEMV_COLS // 32
@@ -142,8 +149,7 @@ def gemv_roofline(fz, dev, copies, iters, seed, graph=True):
     sp = (ctypes.c_void_p * copies)(*[s.ptr for s in scales])
     us = ctypes.c_double()
     fz._lib.check(fz.load().frz_bench_gemv(dev.handle, cp, sp, copies, GEMV_ROWS, GEMV_COLS,
-                                          x.ptr, y.ptr, iters, 1 if graph else 0,
-                                          ctypes.byref(us)))
+                                          x.ptr, y.ptr, iters, mode, ctypes.byref(us)))
     for a in codes + scales + [x, y]:
         a.free()
     return us.value
@@ -385,12 +391,14 @@ def main():
     if args.roofline_only:
         dev = fz.Device(0)
         us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
-                           not args.gemv_stream)
+                           STREAM if args.gemv_stream else GRAPH)
         calibration_copy(fz, dev)
         dev.close()
         achieved = GEMV_BYTES / (us * 1e-6) / 1e9
         print(json.dumps({"roofline_only": True, "us_per_launch": us, "achieved_gbs": achieved,
-                          "frac": achieved / HBM_PEAK_GBS}))
+                          "frac": achieved / HBM_PEAK_GBS,
+                          "timing": "back to back on the stream" if args.gemv_stream
+                                    else "graph-replayed back to back"}))
         return
 
     if args.gguf_load:
@@ -515,15 +523,14 @@ def main():
                   "tok_per_s": args.steps / pwall, "us_per_step_hip_events": pus}
         log(f"pinned formats: {args.steps / pwall:.1f} tok/s, {pus:.1f} us/step events")
 
-    us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed,
-                       not args.gemv_stream)
-    # The same launches one by one on the stream, as the profiler sees them
-    # (its trace does not follow graph launches).
-    us_stream = gemv_roofline(fz, dev, args.gemv_copies, min(args.gemv_iters, 640), args.seed,
-                              False)
+    # The roofline's time: the launches back to back on the stream, timed
+    # with HIP events there (the launches the profiler's trace of
+    # --roofline-only --gemv-stream sees); beside it the graph-replayed rate.
+    us = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed, STREAM)
+    us_graph = gemv_roofline(fz, dev, args.gemv_copies, args.gemv_iters, args.seed, GRAPH)
     achieved = GEMV_BYTES / (us * 1e-6) / 1e9
-    log(f"gemv 6912x1152: {us:.3f} us/launch, {achieved:.0f} GB/s "
-        f"({us_stream:.3f} us a launch on the stream)")
+    log(f"gemv 6912x1152: {us:.3f} us a launch on the stream, {achieved:.0f} GB/s "
+        f"({us_graph:.3f} us graph-replayed)")
     model.close()
     dev.close()
     if cpu_baseline is not None:
@@ -554,11 +561,13 @@ def main():
                                        "+ WRITE_SIZE a dispatch, scaled by a 256 MiB copy's "
                                        "counters), not measured in this run",
                      "kernel": "Q4_0 decode GEMV 6912x1152 (gemv_pair_kernel<0, 4>: 18 lanes a row, 14 rows a workgroup)",
-                     "launch_mode": "graph replay of 64 launches over 64 weight copies"
-                                    if not args.gemv_stream else "launches on the stream",
-                     "us_per_launch": us, "us_per_launch_stream": us_stream,
-                     "profile": "profiles/q4_0_gemv_6912x1152_kernel_stats.md (rocprofv3, "
-                                "launches on the stream: compare us_per_launch_stream)",
+                     "launch_mode": "launches over 64 weight copies in turn (288 MiB), back "
+                                    "to back on the stream, HIP events on that stream",
+                     "us_per_launch": us,
+                     "us_per_launch_graph": us_graph,
+                     "profile": "profiles/q4_0_gemv_6912x1152_kernel_stats.md (rocprofv3 "
+                                "per-dispatch durations of the same launches, which the "
+                                "profiler runs apart)",
                      "algorithmic_bytes": GEMV_BYTES},
         "cpu_baseline": cpu_baseline,
         "parity": parity,

@@ -775,6 +775,8 @@ orc_model* orc_model_create(const orc_config* config,
 
 void orc_model_destroy(orc_model* m) { delete m; }
 
+orc_model* orc_model_clone(const orc_model* m) { return new orc_model(*m); }
+
 void orc_model_set_edits(orc_model* m, const uint32_t* table, int words) {
   m->edits.assign(table, table + words);
 }

@@ -189,6 +189,9 @@ orc_model* orc_model_create(const orc_config* config,
                             const orc_layer_weights* layers,
                             const uint8_t* embedding, const float* output_norm);
 void orc_model_destroy(orc_model* m);
+/* A second model in the same state (caches, edits, last token's values),
+ * over the same weights: many continuations of one prompt run it once. */
+orc_model* orc_model_clone(const orc_model* m);
 /* The edit table (u32 words, the reference's layout) used from now on. */
 void orc_model_set_edits(orc_model* m, const uint32_t* table, int words);
 /* One token at `position` through every layer; writes the logits

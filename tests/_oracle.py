@@ -70,6 +70,7 @@ _SIGS = {
     "orc_model_create": (c_void_p, [POINTER(OrcConfig), POINTER(OrcLayer), _P,
                                     _P]),
     "orc_model_destroy": (None, [_P]),
+    "orc_model_clone": (c_void_p, [_P]),
     "orc_model_set_edits": (None, [_P, _P, c_int]),
     "orc_model_token": (None, [_P, c_uint32, c_int, _P]),
     "orc_model_block": (None, [_P, _P, c_int, c_int, _P]),
@@ -231,6 +232,13 @@ class OracleModel:
             ctypes.byref(self.cfg), self.layers,
             tensors[(-1, "embedding")].ctypes.data,
             tensors[(-1, "output_norm")].ctypes.data)
+
+    def clone(self):
+        """A second model in this one's state over the same weights."""
+        other = OracleModel.__new__(OracleModel)
+        other.cfg, other.tensors, other.layers = self.cfg, self.tensors, self.layers
+        other.handle = lib().orc_model_clone(self.handle)
+        return other
 
     def set_edits(self, table):
         self._edits = np.ascontiguousarray(table, dtype=np.uint32)
