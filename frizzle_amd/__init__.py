@@ -6,7 +6,8 @@ package does not load the library; the first call that needs it does, and
 raises if it has not been built.
 """
 from ._lib import FrzError, exported_symbols, load
-from .runtime import (CAPTURE_SLOTS, Q4_0, Q4_1, Q8_0, TO_THE_END, Device,
+from .runtime import (CAPTURE_SLOTS, PREFILL_BF16, PREFILL_EXACT, Q4_0, Q4_1, Q8_0,
+                      TO_THE_END, Device,
                       DeviceArray, Edit, EditError, EditKind, Model, block_split,
                       capture_layout, capture_words,
                       edit_apply, edit_check, edit_table, gemma3_1b_config,
@@ -14,7 +15,8 @@ from .runtime import (CAPTURE_SLOTS, Q4_0, Q4_1, Q8_0, TO_THE_END, Device,
                       tensor_bytes)
 
 __all__ = [
-    "FrzError", "exported_symbols", "load", "CAPTURE_SLOTS", "Q4_0", "Q4_1", "Q8_0",
+    "FrzError", "exported_symbols", "load", "CAPTURE_SLOTS", "PREFILL_BF16", "PREFILL_EXACT",
+    "Q4_0", "Q4_1", "Q8_0",
     "capture_layout", "capture_words",
     "TO_THE_END", "Device", "block_split",
     "DeviceArray", "Edit", "EditError", "EditKind", "Model", "edit_apply",

@@ -118,6 +118,10 @@ _SIGS = {
                             c_uint32, c_int]),
     "frz_op_gated": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P, _P,
                              c_uint32, c_uint32, _P, c_int]),
+    "frz_op_gemm_bf16": (c_int, [_P, c_int, _P, _P, c_int, c_int, _P, c_int, _P, c_int,
+                                 c_uint32, c_int]),
+    "frz_op_gated_bf16": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, _P, _P, c_uint32,
+                                  c_uint32, _P, c_int]),
     "frz_op_norm": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_float, c_uint32,
                             c_int]),
     "frz_op_rope": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, _P, _P,
@@ -163,6 +167,7 @@ _SIGS = {
     "frz_model_synthesize": (c_int, [_P, c_uint64]),
     "frz_model_set_edits": (c_int, [_P, _P, c_uint32]),
     "frz_model_set_graphs": (c_int, [_P, c_int]),
+    "frz_model_set_prefill": (c_int, [_P, c_int]),
     "frz_model_step": (c_int, [_P, c_uint32, c_uint32, _P, c_int,
                                POINTER(Sampling)]),
     "frz_model_decode": (c_int, [_P, c_uint32, c_uint32, POINTER(Sampling),

@@ -306,6 +306,85 @@ int frz_op_gated(frz_device* dev, const void* gate_codes, const void* gate_scale
       "frz_op_gated");
 }
 
+// The fast prefill mode's products through the ABI: x split into bf16
+// pair planes, then the product (K split as the model splits it).
+int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void* scales,
+                     int rows, int cols, const float* x, int x_stride, float* y, int y_stride,
+                     uint32_t tokens, int splits) {
+  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock || splits < 0 ||
+      splits > 8 || x_stride < cols || y_stride < rows || x_stride % 4 || y_stride % 4) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gemm_bf16: bad shape, tokens or splits");
+  }
+  const QMatrix w = q4(codes, scales, rows, cols, format);
+  if (!bf16_gemm_shape_ok(w, cols, y_stride)) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gemm_bf16: format or shape");
+  }
+  if (int rc = device_put_step(dev, host_step(0, tokens))) return rc;
+  if (splits == 0) splits = bf16_splits_for(w, (int)tokens, false);
+  uint16_t *hi = nullptr, *lo = nullptr;
+  float* parts = nullptr;
+  const size_t plane = (size_t)tokens * cols, stride = (size_t)tokens * y_stride;
+  hipError_t e = hipMalloc(&hi, plane * 2);
+  if (e == hipSuccess) e = hipMalloc(&lo, plane * 2);
+  if (e == hipSuccess) e = hipMalloc(&parts, stride * splits * sizeof(float));
+  if (e == hipSuccess)
+    e = launch_split_rows(dev->stream, dev->step, x, x_stride, cols, hi, lo, cols, (int)tokens);
+  if (e == hipSuccess) {
+    Bf16Gemm g;
+    g.w = w;
+    g.x_hi = hi;
+    g.x_lo = lo;
+    g.ldx = cols;
+    g.y = parts;
+    g.ldy = y_stride;
+    g.part_stride = stride;
+    e = launch_gemm_bf16(dev->stream, dev->step, g, (int)tokens, splits);
+  }
+  if (e == hipSuccess)
+    e = launch_sum_parts(dev->stream, dev->step, parts, stride, splits, rows, y_stride, y,
+                         (int)tokens);
+  if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+  if (hi) (void)hipFree(hi);
+  if (lo) (void)hipFree(lo);
+  if (parts) (void)hipFree(parts);
+  return check_hip(e, "frz_op_gemm_bf16");
+}
+
+int frz_op_gated_bf16(frz_device* dev, const void* gate_codes, const void* gate_scales,
+                      const void* up_codes, const void* up_scales, int rows, int cols,
+                      const float* x, float* act, uint32_t tokens, uint32_t position,
+                      const uint32_t* edits_dev, int layer) {
+  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+    return fail(FRZ_ERR_ARGUMENT, "frz_op_gated_bf16: bad shape or tokens");
+  }
+  if (int rc = device_put_step(dev, host_step(position, tokens))) return rc;
+  uint16_t *hi = nullptr, *lo = nullptr;
+  const size_t in = (size_t)tokens * cols, out = (size_t)tokens * rows;
+  hipError_t e = hipMalloc(&hi, (in + out) * 2);
+  if (e == hipSuccess) e = hipMalloc(&lo, (in + out) * 2);
+  if (e == hipSuccess)
+    e = launch_split_rows(dev->stream, dev->step, x, cols, cols, hi, lo, cols, (int)tokens);
+  if (e == hipSuccess) {
+    Bf16Gemm g;
+    g.w = q4(gate_codes, gate_scales, rows, cols);
+    g.up = q4(up_codes, up_scales, rows, cols);
+    g.x_hi = hi;
+    g.x_lo = lo;
+    g.ldx = cols;
+    g.y = act;
+    g.ldy = rows;
+    g.y_hi = hi + in;
+    g.y_lo = lo + in;
+    g.edits = edits_dev;
+    g.layer = layer;
+    e = launch_gemm_bf16(dev->stream, dev->step, g, (int)tokens, 1);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+  if (hi) (void)hipFree(hi);
+  if (lo) (void)hipFree(lo);
+  return check_hip(e, "frz_op_gated_bf16");
+}
+
 int frz_op_norm(frz_device* dev, const float* gain, const float* post_gain, const float* output,
                 float* hidden, float* normed, int width, float epsilon, uint32_t tokens,
                 int last_token) {

@@ -62,8 +62,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
         // A split product's output: the prefix of its first ranges, then
         // the later range sums added in range order.
         if (a.parts) {
-#pragma unroll
-          for (int j = 0; j < kSplitParts; ++j) {
+          for (int j = 0; j < a.part_count; ++j) {
             const float4 s = ld4(a.parts + j * a.parts_stride + base + 4 * q);
             y[k].x = y[k].x + s.x;
             y[k].y = y[k].y + s.y;
@@ -134,6 +133,21 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
       o.z = (x[k].z * r) * g[k].z;
       o.w = (x[k].w * r) * g[k].w;
       st4(a.normed + base + 4 * q, o);
+      if (a.normed_hi) {
+        const float v[4] = {o.x, o.y, o.z, o.w};
+        uint32_t hw[2], lw[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const __bf16 p = (__bf16)v[2 * e], u = (__bf16)v[2 * e + 1];
+          const __bf16 c = (__bf16)(v[2 * e] - (float)p), d = (__bf16)(v[2 * e + 1] - (float)u);
+          hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, p) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, u) << 16);
+          lw[e] = (uint32_t)__builtin_bit_cast(uint16_t, c) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
+        }
+        *reinterpret_cast<uint2*>(a.normed_hi + base + 4 * q) = make_uint2(hw[0], hw[1]);
+        *reinterpret_cast<uint2*>(a.normed_lo + base + 4 * q) = make_uint2(lw[0], lw[1]);
+      }
     }
   }
 }
@@ -161,7 +175,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
   const int kv = is_value ? h - a.query_heads - a.kv_heads : h - a.query_heads;
   const float* src;
   if (is_query) {
-    src = a.query + (size_t)row * a.q_stride + (size_t)h * a.head_dim;
+    src = (a.query_in ? a.query_in : a.query) + (size_t)row * a.q_stride +
+          (size_t)h * a.head_dim;
   } else if (is_value) {
     src = a.value + (size_t)row * a.kv_stride + (size_t)kv * a.head_dim;
   } else {
@@ -171,6 +186,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
   if (active) {
     va = ld4(src + 4 * lane);
     vb = ld4(src + half + 4 * lane);
+    // A K-split product's later partial sums, added in split order.
+    for (int z = 1; z < a.part_count; ++z) {
+      const float4 pa = ld4(src + z * a.part_stride + 4 * lane);
+      const float4 pb = ld4(src + z * a.part_stride + half + 4 * lane);
+      va = make_float4(va.x + pa.x, va.y + pa.y, va.z + pa.z, va.w + pa.w);
+      vb = make_float4(vb.x + pb.x, vb.y + pb.y, vb.z + pb.z, vb.w + pb.w);
+    }
   }
   partial[t] = rope_lane_squares(va, vb);
   __syncthreads();

@@ -113,6 +113,13 @@ struct frz_model {
   hipGraphExec_t decode_exec = nullptr;
   hipGraph_t decode_graph = nullptr;
   bool use_graphs = true;  // false: decode steps launch their kernels one by one
+  // The fast prefill mode (frz_model_set_prefill): steps of several rows run
+  // their products on the bf16 matrix cores, their activations as pair
+  // planes (widest row x 512 rows each) and K-split partial sums in `parts`.
+  int prefill_mode = FRZ_PREFILL_EXACT;
+  uint16_t *planes_hi = nullptr, *planes_lo = nullptr;
+  float* parts = nullptr;
+  size_t parts_stride = 0;  // floats a split's partial sums take
   // generation state: the tokens whose keys and values the caches hold, and
   // the placed edit table they were computed under
   std::vector<uint32_t> cached;
@@ -312,13 +319,36 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   const float* pending = nullptr;
   // Where the last down product left its later range sums, when it split.
   const float* pending_parts = nullptr;
-  const size_t parts_stride = (size_t)kSplitRows * H;
+  size_t parts_stride = (size_t)kSplitRows * H;
+  int pending_count = kSplitParts;
+  // The fast prefill mode: the products on bf16 pair operands, each K-split
+  // product's partial sums in m->parts, added by the norm that reads them.
+  const bool fast = !v && m->prefill_mode == FRZ_PREFILL_BF16;
+  const float* block_out = m->output;  // where the last block's output lies
+  auto fast_product = [&](const QMatrix& w, int ldx, float* y, int ldy, int* splits) {
+    Bf16Gemm g;
+    g.w = w;
+    g.x_hi = m->planes_hi;
+    g.x_lo = m->planes_lo;
+    g.ldx = ldx;
+    g.y = y;
+    g.ldy = ldy;
+    g.part_stride = m->parts_stride;
+    *splits = y == m->parts ? bf16_splits_for(w, max_tokens, false) : 1;
+    return launch_gemm_bf16(s, m->step, g, max_tokens, *splits);
+  };
+  if (fast) parts_stride = m->parts_stride;
   for (int l = 0; l < c.layers && e == hipSuccess; ++l) {
     const Layer& L = m->layers[l];
-    NormArgs attn_norm{L.gains[0], pending, m->output, m->hidden, m->normed,
+    NormArgs attn_norm{L.gains[0], pending, block_out, m->hidden, m->normed,
                        c.epsilon, H, false};
     attn_norm.parts = pending_parts;
     attn_norm.parts_stride = parts_stride;
+    attn_norm.part_count = pending_count;
+    if (fast) {
+      attn_norm.normed_hi = m->planes_hi;
+      attn_norm.normed_lo = m->planes_lo;
+    }
     if (cap) {
       attn_norm.store_x = slot(l, &frz_capture_slots::residual);
       if (l > 0) attn_norm.store_added = slot(l - 1, &frz_capture_slots::mlp_added);
@@ -332,8 +362,12 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     uint16_t* vcache = v ? v->vcache[l] : L.vcache;
     const size_t cache_stride = v ? (size_t)L.slots * kvw : 0;
     e = launch_norm(s, m->step, attn_norm, max_tokens);
-    if (e == hipSuccess)
-      e = launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens, false);
+    int qkv_splits = 1;
+    if (e == hipSuccess) {
+      e = fast ? fast_product(L.qkv, H, m->parts, qkv_stride, &qkv_splits)
+               : launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens,
+                             false);
+    }
     if (v) {
       // Each variant's row is one decode token: the fused rope and attention
       // a (chunk, head, row), then each row's fold.
@@ -355,16 +389,43 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
       }
     } else {
       if (e == hipSuccess) {
-        RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     m->qkv + qw,
-                   m->qkv + qw + kvw, qkv_stride, qkv_stride, kcache, vcache,
+        // The fast mode's Q/K/V are the product's partial sums, the rope
+        // adding them (its queries then go to m->qkv).
+        const float* src = fast ? m->parts : m->qkv;
+        RopeArgs r{L.turns,     L.gains[1],  L.gains[2],   m->qkv,     src + qw,
+                   src + qw + kvw, qkv_stride, qkv_stride, kcache, vcache,
                    L.slots,     c.head_dim,  c.query_heads, c.kv_heads, c.epsilon, cache_stride};
+        if (fast) {
+          r.query_in = m->parts;
+          r.part_stride = m->parts_stride;
+          r.part_count = qkv_splits;
+        }
         e = launch_rope(s, m->step, r, max_tokens);
       }
       if (cap && e == hipSuccess) {
         e = launch_capture_copy(s, m->step, m->qkv, qkv_stride, qw,
                                 slot(l, &frz_capture_slots::query));
       }
-      if (e == hipSuccess) {
+      // The fast mode's chunk states on the matrix cores, folded as the
+      // exact path folds them (the capture store's scores come from the
+      // exact path: a step that captures runs it).
+      const bool fast_attention = fast && !cap && span.first >= 0;
+      if (fast_attention && e == hipSuccess) {
+        FastAttentionArgs fa{m->qkv,      qkv_stride,  kcache,        vcache,
+                             m->partials, m->partials + m->partial_floats, L.slots, L.window,
+                             c.head_dim,  c.query_heads, c.kv_heads,  L.max_chunks,
+                             scale_log2e};
+        e = launch_attention_fast(
+            s, m->step, fa, max_tokens,
+            fast_attention_chunks((uint32_t)span.first, (uint32_t)span.last, L.window));
+        if (e == hipSuccess) {
+          e = launch_attention_fold(
+              s, m->step,
+              FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window,
+                       L.max_chunks},
+              max_tokens);
+        }
+      } else if (e == hipSuccess) {
         AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
                         m->partials, m->partials + m->partial_floats, L.slots, L.window,
                         c.head_dim, c.query_heads, c.kv_heads, L.max_chunks, scale_log2e,
@@ -386,20 +447,74 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
         }
       }
     }
-    if (e == hipSuccess)
+    int o_splits = 1;
+    if (fast && e == hipSuccess) {
+      e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo, qw,
+                            max_tokens);
+      if (e == hipSuccess) e = fast_product(L.o, qw, m->parts, H, &o_splits);
+    } else if (e == hipSuccess) {
       e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);
+    }
     if (e == hipSuccess) {
-      NormArgs ffn_norm{L.gains[4], L.gains[3], m->output, m->hidden, m->normed,
-                        c.epsilon, H, false};
+      NormArgs ffn_norm{L.gains[4], L.gains[3], fast ? m->parts : m->output, m->hidden,
+                        m->normed, c.epsilon, H, false};
+      if (fast && o_splits > 1) {
+        ffn_norm.parts = m->parts + m->parts_stride;
+        ffn_norm.parts_stride = m->parts_stride;
+        ffn_norm.part_count = o_splits - 1;
+      }
+      if (fast) {
+        ffn_norm.normed_hi = m->planes_hi;
+        ffn_norm.normed_lo = m->planes_lo;
+      }
       if (cap) ffn_norm.store_added = slot(l, &frz_capture_slots::attention_added);
       e = launch_norm(s, m->step, ffn_norm, max_tokens);
     }
-    if (e == hipSuccess)
+    if (fast && e == hipSuccess) {
+      Bf16Gemm g;
+      g.w = L.gate;
+      g.up = L.up;
+      g.x_hi = m->planes_hi;
+      g.x_lo = m->planes_lo;
+      g.ldx = H;
+      g.y = m->act;
+      g.ldy = c.ffn;
+      g.y_hi = m->planes_hi;
+      g.y_lo = m->planes_lo;
+      g.edits = m->edits;
+      g.layer = l;
+      // The planes hold the normed rows this product reads: the activation
+      // planes go after them.
+      g.y_hi = m->planes_hi + (size_t)kPrefillBlock * H;
+      g.y_lo = m->planes_lo + (size_t)kPrefillBlock * H;
+      e = launch_gemm_bf16(s, m->step, g, max_tokens, 1);
+    } else if (e == hipSuccess) {
       e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens,
                        v ? v->edits : m->edits, l, v ? v->edit_stride : 0);
+    }
     if (cap && e == hipSuccess) {
       e = launch_capture_copy(s, m->step, m->act, c.ffn, c.ffn,
                               slot(l, &frz_capture_slots::neurons));
+    }
+    if (fast) {
+      int splits = 1;
+      if (e == hipSuccess) {
+        Bf16Gemm g;
+        g.w = L.down;
+        g.x_hi = m->planes_hi + (size_t)kPrefillBlock * H;
+        g.x_lo = m->planes_lo + (size_t)kPrefillBlock * H;
+        g.ldx = c.ffn;
+        g.y = m->parts;
+        g.ldy = H;
+        g.part_stride = m->parts_stride;
+        splits = bf16_splits_for(L.down, max_tokens, false);
+        e = launch_gemm_bf16(s, m->step, g, max_tokens, splits);
+      }
+      pending = L.gains[5];
+      block_out = m->parts;
+      pending_parts = splits > 1 ? m->parts + m->parts_stride : nullptr;
+      pending_count = splits - 1;
+      continue;
     }
     // Down over a step of few rows splits its tiles' ranges in halves; the
     // next norm adds the later half's sums.
@@ -413,10 +528,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     pending_parts = split ? m->split_parts : nullptr;
   }
   if (e == hipSuccess) {
-    NormArgs final_norm{m->output_norm, pending, m->output, m->hidden, m->normed,
+    NormArgs final_norm{m->output_norm, pending, block_out, m->hidden, m->normed,
                         c.epsilon, H, v == nullptr};
     final_norm.parts = pending_parts;
     final_norm.parts_stride = parts_stride;
+    final_norm.part_count = pending_count;
     if (cap) final_norm.store_added = slot(c.layers - 1, &frz_capture_slots::mlp_added);
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
@@ -1108,6 +1224,32 @@ int frz_model_read_capture(frz_model* m, uint32_t* out, uint64_t words) {
 }
 
 uint32_t frz_model_reused(const frz_model* m) { return m ? m->reused : 0; }
+
+int frz_model_set_prefill(frz_model* m, int mode) {
+  if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_prefill: null model");
+  if (mode != FRZ_PREFILL_EXACT && mode != FRZ_PREFILL_BF16)
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_set_prefill: mode " + std::to_string(mode));
+  const frz_model_config& c = m->c;
+  if (mode == FRZ_PREFILL_BF16 && !m->planes_hi) {
+    const int qw = c.query_heads * c.head_dim, qkv = qw + 2 * c.kv_heads * c.head_dim;
+    for (const Layer& L : m->layers) {
+      if (!bf16_gemm_shape_ok(L.qkv, c.hidden, qkv) || !bf16_gemm_shape_ok(L.o, qw, c.hidden) ||
+          !bf16_gemm_shape_ok(L.gate, c.hidden, c.ffn) ||
+          !bf16_gemm_shape_ok(L.down, c.ffn, c.hidden))
+        return fail(FRZ_ERR_ARGUMENT, "frz_model_set_prefill: a shape the bf16 products refuse");
+    }
+    // Planes: the normed rows (hidden wide) then the activation rows (ffn
+    // wide), which the gated product writes while reading the first.
+    const size_t plane = (size_t)kPrefillBlock * (c.hidden + std::max(c.ffn, qw));
+    m->parts_stride = (size_t)kPrefillBlock * std::max(c.hidden, qkv);
+    if (int rc = alloc(m, &m->planes_hi, plane * 2)) return rc;
+    if (int rc = alloc(m, &m->planes_lo, plane * 2)) return rc;
+    if (int rc = alloc(m, &m->parts, m->parts_stride * 8 * sizeof(float))) return rc;
+  }
+  if (mode != m->prefill_mode) forget_prefix(m);
+  m->prefill_mode = mode;
+  return FRZ_OK;
+}
 
 int frz_model_set_graphs(frz_model* m, int enabled) {
   if (!m) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_graphs: null model");

@@ -147,6 +147,67 @@ hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix
                                const QMatrix& up, const GemvInput& in, int mode, float* act,
                                const uint32_t* edits, int layer);
 
+// ---- the fast prefill mode: products on the bf16 matrix cores ------------
+// A product over bf16 pair operands (prefill_bf16.hip): each weight and each
+// activation as hi + lo bf16, y within about 2^-16 of each product of the
+// exact sum (not the reference's order of addition). Activations come as
+// planes x_hi[t][ldx], x_lo[t][ldx]. With `up`, the gated product: act =
+// gelu(gate) * up, then layer `layer`'s pins, written as fp32 to y (when
+// not null) and as pair planes to y_hi, y_lo. Without, y[t][ldy] fp32; with
+// K split over `splits`, split z's partial sums at y + z * part_stride.
+struct Bf16Gemm {
+  QMatrix w;
+  QMatrix up{};
+  const uint16_t* x_hi = nullptr;
+  const uint16_t* x_lo = nullptr;
+  int ldx = 0;
+  float* y = nullptr;
+  int ldy = 0;
+  size_t part_stride = 0;
+  uint16_t* y_hi = nullptr;
+  uint16_t* y_lo = nullptr;
+  const uint32_t* edits = nullptr;
+  int layer = 0;
+  int k_blocks = 0;  // set by the launcher
+};
+bool bf16_gemm_shape_ok(const QMatrix& w, int ldx, int ldy);
+// The K splits a product of this shape takes to fill the device.
+int bf16_splits_for(const QMatrix& w, int max_tokens, bool gated);
+hipError_t launch_gemm_bf16(hipStream_t s, const DevStep* step, Bf16Gemm g, int max_tokens,
+                            int splits);
+// y[t][o] = the `count` splits' partial sums (stride floats apart) in order.
+hipError_t launch_sum_parts(hipStream_t s, const DevStep* step, const float* parts,
+                            size_t stride, int count, int width, int ld, float* y,
+                            int max_tokens);
+// Rows of fp32 values into bf16 pair planes (hi = bf16(x), lo = bf16(x - hi)).
+hipError_t launch_split_rows(hipStream_t s, const DevStep* step, const float* x, int ldx,
+                             int width, uint16_t* hi, uint16_t* lo, int ldo, int max_tokens);
+
+// The fast prefill mode's attention (attention_fast.hip): each (32-row
+// block, 64-key chunk) of a step's rows as chunk states on the f16 matrix
+// cores, in the layout attention_fold reads (partials, stats; a row's chunk
+// index from its earliest key's chunk), within a stated tolerance of the
+// reference's tile recursion.
+struct FastAttentionArgs {
+  const float* query;  // token t's roped heads at query + t * q_stride
+  int q_stride;
+  const uint16_t* key_cache;
+  const uint16_t* value_cache;
+  float* partials;
+  float* stats;
+  int slots;
+  int window;
+  int head_dim;
+  int query_heads;
+  int kv_heads;
+  int max_chunks;
+  float scale_log2e;
+};
+// Chunks the grid spans for a step whose rows sit at positions first..last.
+int fast_attention_chunks(uint32_t first, uint32_t last, int window);
+hipError_t launch_attention_fast(hipStream_t s, const DevStep* step, const FastAttentionArgs& a,
+                                 int max_tokens, int grid_chunks);
+
 // ---- per-row kernels ---------------------------------------------------
 struct NormArgs {
   const float* gain;
@@ -166,10 +227,15 @@ struct NormArgs {
   float* store_x = nullptr;
   float* store_added = nullptr;
   // Not null: `output` holds a split product's prefix, to which the
-  // kSplitParts range sums at parts + j * parts_stride (same row layout)
-  // are added in order.
+  // part_count range sums (or K-split partial sums) at
+  // parts + j * parts_stride (same row layout) are added in order.
   const float* parts = nullptr;
   size_t parts_stride = 0;
+  int part_count = kSplitParts;
+  // Not null: the normed row is also written as bf16 pair planes (the fast
+  // prefill products' inputs), row t at t * width.
+  uint16_t* normed_hi = nullptr;
+  uint16_t* normed_lo = nullptr;
 };
 hipError_t launch_norm(hipStream_t s, const DevStep* step, const NormArgs& a,
                        int max_tokens);
@@ -191,6 +257,13 @@ struct RopeArgs {
   int kv_heads;
   float epsilon;
   size_t cache_stride = 0;  // elements from one variant's cache to the next
+  // Not null: the queries are read from here (same layout), roped into
+  // `query`. With part_count > 1, query_in, key and value hold a K-split
+  // product's first partial sums, the rest part_stride floats apart each,
+  // added in split order.
+  const float* query_in = nullptr;
+  size_t part_stride = 0;
+  int part_count = 1;
 };
 hipError_t launch_rope(hipStream_t s, const DevStep* step, const RopeArgs& a,
                        int max_tokens);

@@ -122,6 +122,8 @@ def q4_0_split(blocks):
 
 # GGUF format numbers of the weight formats the library computes in.
 Q4_0, Q4_1, Q8_0 = 2, 3, 8
+# How steps of several rows compute their products (frz_prefill_mode).
+PREFILL_EXACT, PREFILL_BF16 = 0, 1
 _BLOCK = {Q4_0: (18, 16, 2), Q4_1: (20, 16, 4), Q8_0: (34, 32, 2)}  # bytes, codes, scales
 
 
@@ -304,6 +306,12 @@ class Model:
 
     def set_graphs(self, enabled):
         check(self.lib.frz_model_set_graphs(self.handle, int(enabled)))
+
+    def set_prefill(self, mode):
+        """PREFILL_EXACT (the reference's order, bit for bit) or PREFILL_BF16
+        (products on the bf16 matrix cores over split operands, logits
+        within 1e-3 relative) for steps of several rows."""
+        check(self.lib.frz_model_set_prefill(self.handle, int(mode)))
 
     def set_edits(self, table):
         t = np.ascontiguousarray(table, dtype=np.uint32)

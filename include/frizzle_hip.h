@@ -113,6 +113,19 @@ int frz_op_gated(frz_device* dev, const void* gate_codes,
                  const void* up_scales, int rows, int cols, const float* x,
                  float* act, uint32_t tokens, uint32_t position,
                  const uint32_t* edits_dev, int layer);
+/* The fast prefill mode's products (FRZ_PREFILL_BF16), op by op: y = W x
+ * over bf16 pair operands, K split over `splits` (1 to 8; 0: as the model
+ * splits it) and the splits added in order; and the gated product with its
+ * pins. x is split into pair planes first. Within about 2^-16 of each
+ * product of the exact sum, not the reference's order (no counterpart in
+ * the reference, which computes in fp32). */
+int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void* scales,
+                     int rows, int cols, const float* x, int x_stride, float* y, int y_stride,
+                     uint32_t tokens, int splits);
+int frz_op_gated_bf16(frz_device* dev, const void* gate_codes, const void* gate_scales,
+                      const void* up_codes, const void* up_scales, int rows, int cols,
+                      const float* x, float* act, uint32_t tokens, uint32_t position,
+                      const uint32_t* edits_dev, int layer);
 /* RMSNorm with the residual add and post-norm (kernels/norm/norm.wgsl:96-198).
  * post_gain null: no add; otherwise hidden += postnorm(output). last_token:
  * the step's last row only. */
@@ -453,6 +466,18 @@ int frz_model_read_capture(frz_model* model, uint32_t* out, uint64_t words);
  * position, end position] per edit), used by every later step. */
 int frz_model_set_edits(frz_model* model, const uint32_t* table,
                         uint32_t words);
+
+/* How steps of several rows (prefill) compute their products. EXACT, the
+ * default: in the reference's order of addition on the fp32 matrix cores,
+ * bit for bit the reference's arithmetic. BF16: on the bf16 matrix cores
+ * over split operands (each weight and activation as a pair hi + lo of
+ * bf16), each product within about 2^-16 of the exact one, so logits agree
+ * with the reference's within 1e-3 relative but not bit for bit; the caches
+ * it writes then differ in their last bits too. Single-token decode steps
+ * are EXACT either way. No counterpart in the reference (whose WGSL runs
+ * fp32 only); switching forgets the cached prompt. */
+enum frz_prefill_mode { FRZ_PREFILL_EXACT = 0, FRZ_PREFILL_BF16 = 1 };
+int frz_model_set_prefill(frz_model* model, int mode);
 
 /* Whether fed decode steps replay one captured HIP graph (1, the default)
  * or launch their kernels one by one (0: the same kernels, for tools that
