@@ -312,7 +312,8 @@ int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void*
                      int rows, int cols, const float* x, int x_stride, float* y, int y_stride,
                      uint32_t tokens, int splits) {
   if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock || splits < 0 ||
-      splits > 8 || x_stride < cols || y_stride < rows || x_stride % 4 || y_stride % 4) {
+      splits > kMaxBf16Splits || x_stride < cols || y_stride < rows || x_stride % 4 ||
+      y_stride % 4) {
     return fail(FRZ_ERR_ARGUMENT, "frz_op_gemm_bf16: bad shape, tokens or splits");
   }
   const QMatrix w = q4(codes, scales, rows, cols, format);

@@ -419,11 +419,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
             s, m->step, fa, max_tokens,
             fast_attention_chunks((uint32_t)span.first, (uint32_t)span.last, L.window));
         if (e == hipSuccess) {
-          e = launch_attention_fold(
-              s, m->step,
-              FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window,
-                       L.max_chunks},
-              max_tokens);
+          FoldArgs f{m->partials, m->partials + m->partial_floats, m->attn, L.window,
+                     L.max_chunks};
+          f.out_hi = m->planes_hi;
+          f.out_lo = m->planes_lo;
+          e = launch_attention_fold(s, m->step, f, max_tokens);
         }
       } else if (e == hipSuccess) {
         AttentionArgs a{m->qkv,     qkv_stride, kcache,       vcache,         m->attn,
@@ -449,8 +449,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     }
     int o_splits = 1;
     if (fast && e == hipSuccess) {
-      e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo, qw,
-                            max_tokens);
+      // The fast attention's fold wrote the pair planes; the exact one's
+      // output (a step that captures) is split here.
+      if (cap || span.first < 0)
+        e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo, qw,
+                              max_tokens);
       if (e == hipSuccess) e = fast_product(L.o, qw, m->parts, H, &o_splits);
     } else if (e == hipSuccess) {
       e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);
@@ -1244,7 +1247,7 @@ int frz_model_set_prefill(frz_model* m, int mode) {
     m->parts_stride = (size_t)kPrefillBlock * std::max(c.hidden, qkv);
     if (int rc = alloc(m, &m->planes_hi, plane * 2)) return rc;
     if (int rc = alloc(m, &m->planes_lo, plane * 2)) return rc;
-    if (int rc = alloc(m, &m->parts, m->parts_stride * 8 * sizeof(float))) return rc;
+    if (int rc = alloc(m, &m->parts, m->parts_stride * kMaxBf16Splits * sizeof(float))) return rc;
   }
   if (mode != m->prefill_mode) forget_prefix(m);
   m->prefill_mode = mode;

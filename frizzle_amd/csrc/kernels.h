@@ -170,6 +170,7 @@ struct Bf16Gemm {
   int layer = 0;
   int k_blocks = 0;  // set by the launcher
 };
+constexpr int kMaxBf16Splits = 16;  // K splits a bf16 product may take
 bool bf16_gemm_shape_ok(const QMatrix& w, int ldx, int ldy);
 // The K splits a product of this shape takes to fill the device.
 int bf16_splits_for(const QMatrix& w, int max_tokens, bool gated);
@@ -353,6 +354,9 @@ struct FoldArgs {
   int window;
   int max_chunks;
   float* store_stats = nullptr;  // the last row's (m, l) a head, when not null
+  // Not null (steps of several rows): the output also as bf16 pair planes.
+  uint16_t* out_hi = nullptr;
+  uint16_t* out_lo = nullptr;
 };
 hipError_t launch_attention_fold(hipStream_t s, const DevStep* step, const FoldArgs& f,
                                  int max_tokens);

@@ -37,13 +37,20 @@ namespace frz {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileRows = 128;
 constexpr int kTileTokens = 128;
 constexpr int kThreads = 256;
 
-// One K block's operands: [row or token block][k half][hi, lo][lane].
+// One K block's operands: [row or token block][k half][hi, lo][slot]. The
+// instruction's lane L (row L % 32, k sub-block L / 32) reads slot
+// 32 sub + (row ^ 4 sub): eight lanes reading eight rows of one sub-block,
+// and a pair of threads writing one row's two sub-blocks four rows at a
+// time, each touch eight distinct 16-byte bank groups.
+__device__ __forceinline__ int slot_of(int row, int sub) { return 32 * sub + (row ^ (sub << 2)); }
+
 struct Stage {
   uint4 w[4][2][2][64];
   uint4 x[4][2][2][64];
@@ -53,18 +60,24 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Eight floats as bf16 pairs: hi = bf16(v), lo = bf16(v - hi), round to
-// nearest even (v_cvt_pk_bf16_f32).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats as bf16 pairs, packed: hi = bf16(v), lo = bf16(v - hi), round
+// to nearest even (one v_cvt_pk_bf16_f32 each).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const f32x2 v = {a, b};
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  const f32x2 back = {__builtin_bit_cast(float, hi << 16),
+                      __builtin_bit_cast(float, hi & 0xFFFF0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - back, bf16x2));
+}
+
+// Eight floats as bf16 pairs.
 __device__ __forceinline__ void split8(const float (&v)[8], uint4& hi, uint4& lo) {
   uint32_t h[4], l[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const __bf16 a = (__bf16)v[2 * j], b = (__bf16)v[2 * j + 1];
-    const float ra = v[2 * j] - (float)a, rb = v[2 * j + 1] - (float)b;
-    const __bf16 c = (__bf16)ra, d = (__bf16)rb;
-    h[j] = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-    l[j] = (uint32_t)__builtin_bit_cast(uint16_t, c) | ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
-  }
+  for (int j = 0; j < 4; ++j) split2(v[2 * j], v[2 * j + 1], h[j], l[j]);
   hi = make_uint4(h[0], h[1], h[2], h[3]);
   lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
@@ -78,21 +91,39 @@ struct WeightLoad {
   uint32_t scale;  // d, and m in the high half for Q4_1
 };
 
+// A load from global memory, said so: a pointer chosen among a fused
+// product's members would otherwise load through the flat path, whose
+// waits also hold back LDS reads.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 load_global4(const void* p) {
+  const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 load_global2(const void* p) {
+  const u32x2 v = *(const __attribute__((address_space(1))) u32x2*)(p);
+  return make_uint2(v.x, v.y);
+}
+template <typename T>
+__device__ __forceinline__ T load_global(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
 template <int FORMAT>
 __device__ __forceinline__ WeightLoad<FORMAT> load_weights(const MemberRow& m, int blocks, int kb,
                                                            int h) {
   WeightLoad<FORMAT> r;
   const size_t b = (size_t)m.row * blocks + kb;
   if (FORMAT == kQ8_0) {
-    r.codes = *reinterpret_cast<const uint4*>(m.codes + b * 32 + 16 * h);
+    r.codes = load_global4(m.codes + b * 32 + 16 * h);
   } else {
-    const uint2 c = *reinterpret_cast<const uint2*>(m.codes + b * 16 + 8 * h);
+    const uint2 c = load_global2(m.codes + b * 16 + 8 * h);
     r.codes = make_uint4(c.x, c.y, 0, 0);
   }
   if (FORMAT == kQ4_1) {
-    r.scale = *reinterpret_cast<const uint32_t*>(m.scales + 2 * b);
+    r.scale = load_global<uint32_t>(m.scales + 2 * b);
   } else {
-    r.scale = m.scales[b];
+    r.scale = load_global<uint16_t>(m.scales + b);
   }
   return r;
 }
@@ -117,35 +148,45 @@ __device__ __forceinline__ void stage_weights(Stage& st, const WeightLoad<FORMAT
     }
     uint4 hi, lo;
     split8(a, hi, lo);
-    st.w[rb][h][0][lane] = hi;
-    st.w[rb][h][1][lane] = lo;
+    st.w[rb][h][0][slot_of(lane, 0)] = hi;
+    st.w[rb][h][1][slot_of(lane, 0)] = lo;
     split8(b, hi, lo);
-    st.w[rb][h][0][lane + 32] = hi;
-    st.w[rb][h][1][lane + 32] = lo;
+    st.w[rb][h][0][slot_of(lane, 1)] = hi;
+    st.w[rb][h][1][slot_of(lane, 1)] = lo;
     return;
   }
   // Q4_0, Q4_1: low nibbles are weights 8h + j (k half 0, sub h), high
-  // nibbles 16 + 8h + j (k half 1, sub h).
-  const uint32_t lo4[2] = {in.codes.x & 0x0F0F0F0Fu, in.codes.y & 0x0F0F0F0Fu};
-  const uint32_t hi4[2] = {(in.codes.x >> 4) & 0x0F0F0F0Fu, (in.codes.y >> 4) & 0x0F0F0F0Fu};
-  if (FORMAT == kQ4_1) {
-    const float mn = half_bits_to_float(in.scale >> 16);
+  // nibbles 16 + 8h + j (k half 1, sub h). A nibble masked under the
+  // exponent of f16 1024 is the half 1024 + q (two at once, from bits 0 and
+  // 16 of a shifted code word). Q4_0: fma(1024 + q, d, -1032 d) = (q - 8) d,
+  // exact; Q4_1: fma(q, d, m) = q d + m rounded once, as q4_1.wgsl:12-25
+  // computes it (q = (1024 + q) - 1024 exactly).
+  const float c = FORMAT == kQ4_1 ? 0.0f : -1032.0f * d;  // exact
+  const uint32_t w2[2] = {in.codes.x, in.codes.y};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // q d + m, one rounding (q4_1.wgsl:12-25): q d is exact.
-      a[j] = __builtin_fmaf((float)((lo4[j >> 2] >> (8 * (j & 3))) & 0xFFu), d, mn);
-      b[j] = __builtin_fmaf((float)((hi4[j >> 2] >> (8 * (j & 3))) & 0xFFu), d, mn);
-    }
-  } else {
-    const float m8 = -8.0f * d;  // exact
+  for (int wd = 0; wd < 2; ++wd) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // (q - 8) d = fma(q, d, -8 d): exact, as (q - 8) d is.
-      a[j] = __builtin_fmaf((float)((lo4[j >> 2] >> (8 * (j & 3))) & 0xFFu), d, m8);
-      b[j] = __builtin_fmaf((float)((hi4[j >> 2] >> (8 * (j & 3))) & 0xFFu), d, m8);
+    for (int sh = 0; sh < 4; ++sh) {
+      // shift 0: weights j, j + 2 (low nibbles); 4: 16 + j, 16 + j + 2;
+      // 8: j + 1, j + 3; 12: 16 + j + 1, 16 + j + 3 (j = 4 wd)
+      const uint32_t bits = ((w2[wd] >> (4 * sh)) & 0x000F000Fu) | 0x64006400u;
+      const half2v q = __builtin_bit_cast(half2v, bits);
+      float v0, v1;
+      if (FORMAT == kQ4_1) {
+        const float mn = half_bits_to_float(in.scale >> 16);
+        v0 = __builtin_fmaf((float)q.x - 1024.0f, d, mn);
+        v1 = __builtin_fmaf((float)q.y - 1024.0f, d, mn);
+      } else {
+        v0 = __builtin_fmaf((float)q.x, d, c);
+        v1 = __builtin_fmaf((float)q.y, d, c);
+      }
+      const int j = 4 * wd + (sh >> 1);
+      float* dst = (sh & 1) ? b : a;
+      dst[j] = v0;
+      dst[j + 2] = v1;
     }
   }
-  const int l = lane + 32 * h;
+  const int l = slot_of(lane, h);
   uint4 hi, lo;
   split8(a, hi, lo);
   st.w[rb][0][0][l] = hi;
@@ -155,30 +196,31 @@ __device__ __forceinline__ void stage_weights(Stage& st, const WeightLoad<FORMAT
   st.w[rb][1][1][l] = lo;
 }
 
-// A thread's share of one K block of the activations: token tk of the tile,
-// k half kh (16 values of each plane).
+// A thread's share of one K block of the activations: token tk of the
+// tile, sub-block `sub` of each k half (k 16 s + 8 sub .. + 7, s = 0, 1),
+// 8 values of each plane each.
 struct InputLoad {
   uint4 hi[2], lo[2];
 };
 
 __device__ __forceinline__ InputLoad load_inputs(const uint16_t* __restrict__ x_hi,
                                                  const uint16_t* __restrict__ x_lo, size_t row,
-                                                 int kb, int kh) {
+                                                 int kb, int sub) {
   InputLoad r;
-  const size_t at = row + (size_t)kb * 32 + 16 * kh;
-  r.hi[0] = *reinterpret_cast<const uint4*>(x_hi + at);
-  r.hi[1] = *reinterpret_cast<const uint4*>(x_hi + at + 8);
-  r.lo[0] = *reinterpret_cast<const uint4*>(x_lo + at);
-  r.lo[1] = *reinterpret_cast<const uint4*>(x_lo + at + 8);
+  const size_t at = row + (size_t)kb * 32 + 8 * sub;
+  r.hi[0] = load_global4(x_hi + at);
+  r.hi[1] = load_global4(x_hi + at + 16);
+  r.lo[0] = load_global4(x_lo + at);
+  r.lo[1] = load_global4(x_lo + at + 16);
   return r;
 }
 
-__device__ __forceinline__ void stage_inputs(Stage& st, const InputLoad& in, int tk, int kh) {
-  const int cb = tk >> 5, lane = tk & 31;
-  st.x[cb][kh][0][lane] = in.hi[0];
-  st.x[cb][kh][1][lane] = in.lo[0];
-  st.x[cb][kh][0][lane + 32] = in.hi[1];
-  st.x[cb][kh][1][lane + 32] = in.lo[1];
+__device__ __forceinline__ void stage_inputs(Stage& st, const InputLoad& in, int tk, int sub) {
+  const int cb = tk >> 5, l = slot_of(tk & 31, sub);
+  st.x[cb][0][0][l] = in.hi[0];
+  st.x[cb][0][1][l] = in.lo[0];
+  st.x[cb][1][0][l] = in.hi[1];
+  st.x[cb][1][1][l] = in.lo[1];
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -199,11 +241,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* _
   if (n0 >= tokens) return;  // the whole workgroup: past the step's rows
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
+  const int my_slot = slot_of(lane & 31, lane >> 5);
   const int blocks = g.w.cols / 32;
   const int kb0 = blockIdx.z * g.k_blocks;
   const int kb1 = min(blocks, kb0 + g.k_blocks);
 
-  // This thread's weight row (r of the tile) and its source.
+  // This thread's weight row (r of the tile) and half block h (a pair of
+  // threads reads one row's 16 code bytes).
   const int r = tid >> 1, h = tid & 1;
   int out_rows, row;
   MemberRow src;
@@ -217,7 +261,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* _
     row = min((int)blockIdx.x * kTileRows + r, out_rows - 1);
     src = member_row(g.w, row);
   }
-  // This thread's input token and k half.
+  // This thread's input token and k sub-block (a pair reads 64 bytes of a
+  // row).
   const int tk = tid >> 1, kh = tid & 1;
   const size_t x_row = (size_t)min(n0 + tk, tokens - 1) * g.ldx;
 
@@ -229,42 +274,53 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* _
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // Loads run two blocks ahead, into two register sets a, b: while block
-  // kb computes from LDS, block kb + 1 (loaded a block ago) waits in one
-  // set and block kb + 2 is requested into the other. A split past the last
-  // block (splits that do not divide the blocks) loads nothing and writes
-  // its zero partial sums.
-  WeightLoad<FORMAT> wa, wb;
-  InputLoad xa, xb;
-  if (kb0 < kb1) {
-    wa = load_weights<FORMAT>(src, blocks, kb0, h);
-    xa = load_inputs(g.x_hi, g.x_lo, x_row, kb0, kh);
+  // A split past the last block (splits that do not divide the blocks)
+  // writes zero partial sums.
+  if (kb0 >= kb1) {
+    if (!GATED) {
+      float* y = g.y + (size_t)blockIdx.z * g.part_stride;
+      for (int i = tid; i < kTileRows * kTileTokens; i += kThreads) {
+        const int o = blockIdx.x * kTileRows + (i % kTileRows), t = n0 + i / kTileRows;
+        if (o < out_rows && t < tokens) y[(size_t)t * g.ldy + o] = 0.0f;
+      }
+    }
+    return;
   }
-  if (kb0 + 1 < kb1) {
-    wb = load_weights<FORMAT>(src, blocks, kb0 + 1, h);
-    xb = load_inputs(g.x_hi, g.x_lo, x_row, kb0 + 1, kh);
-  }
-  if (kb0 < kb1) {
-    stage_weights<FORMAT>(stage[0], wa, r, h);
-    stage_inputs(stage[0], xa, tk, kh);
-  }
+  // Loads run three blocks ahead, into three register sets a, b, c: while
+  // block kb computes from one LDS buffer, block kb + 1 (loaded two blocks
+  // ago) is decoded into the other, and block kb + 3 is requested into the
+  // set block kb came from. Every load is issued whatever kb (past the last
+  // block it reloads the last), so the waits count exactly the loads they
+  // need.
+  WeightLoad<FORMAT> wa = load_weights<FORMAT>(src, blocks, kb0, h);
+  InputLoad xa = load_inputs(g.x_hi, g.x_lo, x_row, kb0, kh);
+  WeightLoad<FORMAT> wb = load_weights<FORMAT>(src, blocks, min(kb0 + 1, kb1 - 1), h);
+  InputLoad xb = load_inputs(g.x_hi, g.x_lo, x_row, min(kb0 + 1, kb1 - 1), kh);
+  WeightLoad<FORMAT> wc_ = load_weights<FORMAT>(src, blocks, min(kb0 + 2, kb1 - 1), h);
+  InputLoad xc = load_inputs(g.x_hi, g.x_lo, x_row, min(kb0 + 2, kb1 - 1), kh);
+  stage_weights<FORMAT>(stage[0], wa, r, h);
+  stage_inputs(stage[0], xa, tk, kh);
   __syncthreads();
   auto block_step = [&](int kb, const Stage& cur, Stage& next, WeightLoad<FORMAT>& w_free,
                         InputLoad& x_free, const WeightLoad<FORMAT>& w_next,
                         const InputLoad& x_next) {
-    if (kb + 2 < kb1) {
-      w_free = load_weights<FORMAT>(src, blocks, kb + 2, h);
-      x_free = load_inputs(g.x_hi, g.x_lo, x_row, kb + 2, kh);
-    }
+    // The next block is staged into the other buffer first (it was last
+    // read before the previous barrier), so its decode can run while this
+    // block's products do.
+    stage_weights<FORMAT>(next, w_next, r, h);
+    stage_inputs(next, x_next, tk, kh);
+    const int ahead = min(kb + 3, kb1 - 1);
+    w_free = load_weights<FORMAT>(src, blocks, ahead, h);
+    x_free = load_inputs(g.x_hi, g.x_lo, x_row, ahead, kh);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 ah[2], al[2], bh[2], bl[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        ah[i] = as_bf16x8(cur.w[wr + 2 * i][ks][0][lane]);
-        al[i] = as_bf16x8(cur.w[wr + 2 * i][ks][1][lane]);
-        bh[i] = as_bf16x8(cur.x[2 * wc + i][ks][0][lane]);
-        bl[i] = as_bf16x8(cur.x[2 * wc + i][ks][1][lane]);
+        ah[i] = as_bf16x8(cur.w[wr + 2 * i][ks][0][my_slot]);
+        al[i] = as_bf16x8(cur.w[wr + 2 * i][ks][1][my_slot]);
+        bh[i] = as_bf16x8(cur.x[2 * wc + i][ks][0][my_slot]);
+        bl[i] = as_bf16x8(cur.x[2 * wc + i][ks][1][my_slot]);
       }
       // The three products of each pair, four independent accumulators
       // between two that update the same one.
@@ -284,15 +340,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* _
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
     }
-    if (kb + 1 < kb1) {
-      stage_weights<FORMAT>(next, w_next, r, h);
-      stage_inputs(next, x_next, tk, kh);
-    }
     __syncthreads();
   };
-  for (int kb = kb0; kb < kb1; kb += 2) {
+  // LDS buffers alternate every block, register sets every third: six
+  // blocks a turn.
+  for (int kb = kb0; kb < kb1; kb += 6) {
     block_step(kb, stage[0], stage[1], wa, xa, wb, xb);
-    if (kb + 1 < kb1) block_step(kb + 1, stage[1], stage[0], wb, xb, wa, xa);
+    if (kb + 1 >= kb1) break;
+    block_step(kb + 1, stage[1], stage[0], wb, xb, wc_, xc);
+    if (kb + 2 >= kb1) break;
+    block_step(kb + 2, stage[0], stage[1], wc_, xc, wa, xa);
+    if (kb + 3 >= kb1) break;
+    block_step(kb + 3, stage[1], stage[0], wa, xa, wb, xb);
+    if (kb + 4 >= kb1) break;
+    block_step(kb + 4, stage[0], stage[1], wb, xb, wc_, xc);
+    if (kb + 5 >= kb1) break;
+    block_step(kb + 5, stage[1], stage[0], wc_, xc, wa, xa);
   }
 
   // Lane l's register e of a 32 x 32 block: row (e / 4) 8 + (l / 32) 4 +

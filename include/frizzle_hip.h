@@ -114,7 +114,7 @@ int frz_op_gated(frz_device* dev, const void* gate_codes,
                  float* act, uint32_t tokens, uint32_t position,
                  const uint32_t* edits_dev, int layer);
 /* The fast prefill mode's products (FRZ_PREFILL_BF16), op by op: y = W x
- * over bf16 pair operands, K split over `splits` (1 to 8; 0: as the model
+ * over bf16 pair operands, K split over `splits` (1 to 16; 0: as the model
  * splits it) and the splits added in order; and the gated product with its
  * pins. x is split into pair planes first. Within about 2^-16 of each
  * product of the exact sum, not the reference's order (no counterpart in
