@@ -289,19 +289,7 @@ __global__ __launch_bounds__(64) void attention_fold_rows_kernel(const DevStep* 
   if (f.out_hi) {
     // The fast prefill mode's O product reads the row as bf16 pairs.
     const float v[4] = {res.x, res.y, res.z, res.w};
-    uint32_t hw[2], lw[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const __bf16 a = (__bf16)v[2 * e], b = (__bf16)v[2 * e + 1];
-      const __bf16 c = (__bf16)(v[2 * e] - (float)a), d = (__bf16)(v[2 * e + 1] - (float)b);
-      hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
-              ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-      lw[e] = (uint32_t)__builtin_bit_cast(uint16_t, c) |
-              ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
-    }
-    const size_t at = (size_t)row * QH * D + w * D + 4 * lane;
-    *reinterpret_cast<uint2*>(f.out_hi + at) = make_uint2(hw[0], hw[1]);
-    *reinterpret_cast<uint2*>(f.out_lo + at) = make_uint2(lw[0], lw[1]);
+    store_pairs4(f.out_hi, f.out_lo, row, w * D + 4 * lane, QH * D, v);
   }
   // The last row's (m, l), for the capture store: m as the last chunk's
   // fold leaves it.

@@ -306,8 +306,9 @@ int frz_op_gated(frz_device* dev, const void* gate_codes, const void* gate_scale
       "frz_op_gated");
 }
 
-// The fast prefill mode's products through the ABI: x split into bf16
-// pair planes, then the product (K split as the model splits it).
+// The fast prefill mode's products through the ABI: the weights unpacked
+// into fragment planes, x split into bf16 pair planes, then the product (K
+// split as the model splits it).
 int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void* scales,
                      int rows, int cols, const float* x, int x_stride, float* y, int y_stride,
                      uint32_t tokens, int splits) {
@@ -321,18 +322,24 @@ int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void*
     return fail(FRZ_ERR_ARGUMENT, "frz_op_gemm_bf16: format or shape");
   }
   if (int rc = device_put_step(dev, host_step(0, tokens))) return rc;
-  if (splits == 0) splits = bf16_splits_for(w, (int)tokens, false);
+  if (splits == 0) splits = bf16_splits_for(rows, cols, (int)tokens, false);
   uint16_t *hi = nullptr, *lo = nullptr;
   float* parts = nullptr;
-  const size_t plane = (size_t)tokens * cols, stride = (size_t)tokens * y_stride;
+  uint4* planes = nullptr;
+  const size_t blocks_rows = (tokens + 31) / 32 * 32;  // the planes' whole token blocks
+  const size_t plane = blocks_rows * cols, stride = (size_t)tokens * y_stride;
   hipError_t e = hipMalloc(&hi, plane * 2);
   if (e == hipSuccess) e = hipMalloc(&lo, plane * 2);
   if (e == hipSuccess) e = hipMalloc(&parts, stride * splits * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&planes, bf16_planes_bytes(rows, cols, false));
+  if (e == hipSuccess) e = launch_unpack_planes(dev->stream, w, nullptr, planes);
   if (e == hipSuccess)
-    e = launch_split_rows(dev->stream, dev->step, x, x_stride, cols, hi, lo, cols, (int)tokens);
+    e = launch_split_rows(dev->stream, dev->step, x, x_stride, cols, hi, lo, (int)tokens);
   if (e == hipSuccess) {
     Bf16Gemm g;
-    g.w = w;
+    g.w = planes;
+    g.rows = rows;
+    g.cols = cols;
     g.x_hi = hi;
     g.x_lo = lo;
     g.ldx = cols;
@@ -348,6 +355,7 @@ int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void*
   if (hi) (void)hipFree(hi);
   if (lo) (void)hipFree(lo);
   if (parts) (void)hipFree(parts);
+  if (planes) (void)hipFree(planes);
   return check_hip(e, "frz_op_gemm_bf16");
 }
 
@@ -355,20 +363,28 @@ int frz_op_gated_bf16(frz_device* dev, const void* gate_codes, const void* gate_
                       const void* up_codes, const void* up_scales, int rows, int cols,
                       const float* x, float* act, uint32_t tokens, uint32_t position,
                       const uint32_t* edits_dev, int layer) {
-  if (!shape_ok(rows, cols) || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
+  if (!shape_ok(rows, cols) || rows % 16 || tokens == 0 || tokens > (uint32_t)kPrefillBlock) {
     return fail(FRZ_ERR_ARGUMENT, "frz_op_gated_bf16: bad shape or tokens");
   }
   if (int rc = device_put_step(dev, host_step(position, tokens))) return rc;
+  const QMatrix gate = q4(gate_codes, gate_scales, rows, cols);
+  const QMatrix up = q4(up_codes, up_scales, rows, cols);
   uint16_t *hi = nullptr, *lo = nullptr;
-  const size_t in = (size_t)tokens * cols, out = (size_t)tokens * rows;
+  uint4* planes = nullptr;
+  const size_t blocks_rows = (tokens + 31) / 32 * 32;  // the planes' whole token blocks
+  const size_t in = blocks_rows * cols, out = blocks_rows * rows;
   hipError_t e = hipMalloc(&hi, (in + out) * 2);
   if (e == hipSuccess) e = hipMalloc(&lo, (in + out) * 2);
+  if (e == hipSuccess) e = hipMalloc(&planes, bf16_planes_bytes(rows, cols, true));
+  if (e == hipSuccess) e = launch_unpack_planes(dev->stream, gate, &up, planes);
   if (e == hipSuccess)
-    e = launch_split_rows(dev->stream, dev->step, x, cols, cols, hi, lo, cols, (int)tokens);
+    e = launch_split_rows(dev->stream, dev->step, x, cols, cols, hi, lo, (int)tokens);
   if (e == hipSuccess) {
     Bf16Gemm g;
-    g.w = q4(gate_codes, gate_scales, rows, cols);
-    g.up = q4(up_codes, up_scales, rows, cols);
+    g.w = planes;
+    g.rows = rows;
+    g.cols = cols;
+    g.gated = true;
     g.x_hi = hi;
     g.x_lo = lo;
     g.ldx = cols;
@@ -383,6 +399,7 @@ int frz_op_gated_bf16(frz_device* dev, const void* gate_codes, const void* gate_
   if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
   if (hi) (void)hipFree(hi);
   if (lo) (void)hipFree(lo);
+  if (planes) (void)hipFree(planes);
   return check_hip(e, "frz_op_gated_bf16");
 }
 

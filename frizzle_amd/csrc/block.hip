@@ -135,18 +135,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
       st4(a.normed + base + 4 * q, o);
       if (a.normed_hi) {
         const float v[4] = {o.x, o.y, o.z, o.w};
-        uint32_t hw[2], lw[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const __bf16 p = (__bf16)v[2 * e], u = (__bf16)v[2 * e + 1];
-          const __bf16 c = (__bf16)(v[2 * e] - (float)p), d = (__bf16)(v[2 * e + 1] - (float)u);
-          hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, p) |
-                  ((uint32_t)__builtin_bit_cast(uint16_t, u) << 16);
-          lw[e] = (uint32_t)__builtin_bit_cast(uint16_t, c) |
-                  ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
-        }
-        *reinterpret_cast<uint2*>(a.normed_hi + base + 4 * q) = make_uint2(hw[0], hw[1]);
-        *reinterpret_cast<uint2*>(a.normed_lo + base + 4 * q) = make_uint2(lw[0], lw[1]);
+        store_pairs4(a.normed_hi, a.normed_lo, row, 4 * q, a.width, v);
       }
     }
   }

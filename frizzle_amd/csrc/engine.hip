@@ -118,6 +118,14 @@ struct frz_model {
   // planes (widest row x 512 rows each) and K-split partial sums in `parts`.
   int prefill_mode = FRZ_PREFILL_EXACT;
   uint16_t *planes_hi = nullptr, *planes_lo = nullptr;
+  // Each layer's weights as bf16 fragment planes (Q/K/V, O, gate and up,
+  // down), made when the mode is set and again before the next fast step
+  // after a tensor changes.
+  struct WeightPlanes {
+    uint4 *qkv, *o, *gate_up, *down;
+  };
+  std::vector<WeightPlanes> weight_planes;
+  bool planes_stale = true;
   float* parts = nullptr;
   size_t parts_stride = 0;  // floats a split's partial sums take
   // generation state: the tokens whose keys and values the caches hold, and
@@ -192,6 +200,38 @@ void release(frz_model* m, const void* p) {
 void forget_prefix(frz_model* m) {
   m->cached.clear();
   m->cached_edits.clear();
+}
+
+// Each layer's weights as the fast prefill mode's fragment planes
+// (prefill_bf16.hip): 107 MB a Gemma-3-1B layer, allocated the first time.
+int unpack_weight_planes(frz_model* m) {
+  if (m->weight_planes.empty()) {
+    std::vector<frz_model::WeightPlanes> planes;
+    for (const Layer& L : m->layers) {
+      frz_model::WeightPlanes p{};
+      if (int rc = alloc(m, &p.qkv, bf16_planes_bytes(L.qkv.rows, L.qkv.cols, false))) return rc;
+      if (int rc = alloc(m, &p.o, bf16_planes_bytes(L.o.rows, L.o.cols, false))) return rc;
+      if (int rc = alloc(m, &p.gate_up, bf16_planes_bytes(L.gate.rows, L.gate.cols, true)))
+        return rc;
+      if (int rc = alloc(m, &p.down, bf16_planes_bytes(L.down.rows, L.down.cols, false)))
+        return rc;
+      planes.push_back(p);
+    }
+    m->weight_planes = std::move(planes);
+  }
+  hipStream_t s = m->dev->stream;
+  hipError_t e = hipSuccess;
+  for (size_t l = 0; l < m->layers.size() && e == hipSuccess; ++l) {
+    const Layer& L = m->layers[l];
+    const frz_model::WeightPlanes& p = m->weight_planes[l];
+    e = launch_unpack_planes(s, L.qkv, nullptr, p.qkv);
+    if (e == hipSuccess) e = launch_unpack_planes(s, L.o, nullptr, p.o);
+    if (e == hipSuccess) e = launch_unpack_planes(s, L.gate, &L.up, p.gate_up);
+    if (e == hipSuccess) e = launch_unpack_planes(s, L.down, nullptr, p.down);
+  }
+  if (int rc = check_hip(e, "unpacking the weight planes")) return rc;
+  m->planes_stale = false;
+  return FRZ_OK;
 }
 
 // A matrix in `format`: the same one when it already is, else new buffers
@@ -325,16 +365,22 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   // product's partial sums in m->parts, added by the norm that reads them.
   const bool fast = !v && m->prefill_mode == FRZ_PREFILL_BF16;
   const float* block_out = m->output;  // where the last block's output lies
-  auto fast_product = [&](const QMatrix& w, int ldx, float* y, int ldy, int* splits) {
+  if (fast && m->planes_stale) {
+    if (int rc = unpack_weight_planes(m)) return rc;
+  }
+  auto fast_product = [&](const uint4* planes, const QMatrix& w, int ldx, float* y, int ldy,
+                          int* splits) {
     Bf16Gemm g;
-    g.w = w;
+    g.w = planes;
+    g.rows = w.rows;
+    g.cols = w.cols;
     g.x_hi = m->planes_hi;
     g.x_lo = m->planes_lo;
     g.ldx = ldx;
     g.y = y;
     g.ldy = ldy;
     g.part_stride = m->parts_stride;
-    *splits = y == m->parts ? bf16_splits_for(w, max_tokens, false) : 1;
+    *splits = y == m->parts ? bf16_splits_for(w.rows, w.cols, max_tokens, false) : 1;
     return launch_gemm_bf16(s, m->step, g, max_tokens, *splits);
   };
   if (fast) parts_stride = m->parts_stride;
@@ -364,7 +410,8 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     e = launch_norm(s, m->step, attn_norm, max_tokens);
     int qkv_splits = 1;
     if (e == hipSuccess) {
-      e = fast ? fast_product(L.qkv, H, m->parts, qkv_stride, &qkv_splits)
+      e = fast ? fast_product(m->weight_planes[l].qkv, L.qkv, H, m->parts, qkv_stride,
+                              &qkv_splits)
                : launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens,
                              false);
     }
@@ -452,9 +499,10 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
       // The fast attention's fold wrote the pair planes; the exact one's
       // output (a step that captures) is split here.
       if (cap || span.first < 0)
-        e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo, qw,
+        e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo,
                               max_tokens);
-      if (e == hipSuccess) e = fast_product(L.o, qw, m->parts, H, &o_splits);
+      if (e == hipSuccess)
+        e = fast_product(m->weight_planes[l].o, L.o, qw, m->parts, H, &o_splits);
     } else if (e == hipSuccess) {
       e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);
     }
@@ -475,15 +523,15 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     }
     if (fast && e == hipSuccess) {
       Bf16Gemm g;
-      g.w = L.gate;
-      g.up = L.up;
+      g.w = m->weight_planes[l].gate_up;
+      g.rows = L.gate.rows;
+      g.cols = L.gate.cols;
+      g.gated = true;
       g.x_hi = m->planes_hi;
       g.x_lo = m->planes_lo;
       g.ldx = H;
-      g.y = m->act;
+      g.y = cap ? m->act : nullptr;  // the down product reads the planes
       g.ldy = c.ffn;
-      g.y_hi = m->planes_hi;
-      g.y_lo = m->planes_lo;
       g.edits = m->edits;
       g.layer = l;
       // The planes hold the normed rows this product reads: the activation
@@ -503,14 +551,16 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
       int splits = 1;
       if (e == hipSuccess) {
         Bf16Gemm g;
-        g.w = L.down;
+        g.w = m->weight_planes[l].down;
+        g.rows = L.down.rows;
+        g.cols = L.down.cols;
         g.x_hi = m->planes_hi + (size_t)kPrefillBlock * H;
         g.x_lo = m->planes_lo + (size_t)kPrefillBlock * H;
         g.ldx = c.ffn;
         g.y = m->parts;
         g.ldy = H;
         g.part_stride = m->parts_stride;
-        splits = bf16_splits_for(L.down, max_tokens, false);
+        splits = bf16_splits_for(L.down.rows, L.down.cols, max_tokens, false);
         e = launch_gemm_bf16(s, m->step, g, max_tokens, splits);
       }
       pending = L.gains[5];
@@ -1111,6 +1161,7 @@ int frz_model_set_tensor_format(frz_model* m, int layer, int role, int format, c
                                 uint64_t bytes) {
   if (!m || !data) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: null argument");
   forget_prefix(m);
+  m->planes_stale = true;
   const frz_model_config& c = m->c;
   if (role < 0 || role > FRZ_ROLE_OUTPUT_NORM) return fail(FRZ_ERR_ARGUMENT, "frz_model_set_tensor: role");
   const bool ok_format = !is_matrix(role)          ? format == 0
@@ -1248,6 +1299,11 @@ int frz_model_set_prefill(frz_model* m, int mode) {
     if (int rc = alloc(m, &m->planes_hi, plane * 2)) return rc;
     if (int rc = alloc(m, &m->planes_lo, plane * 2)) return rc;
     if (int rc = alloc(m, &m->parts, m->parts_stride * kMaxBf16Splits * sizeof(float))) return rc;
+  }
+  // The weight planes are made afresh: a caller may have written the
+  // weights through the planned buffers.
+  if (mode == FRZ_PREFILL_BF16) {
+    if (int rc = unpack_weight_planes(m)) return rc;
   }
   if (mode != m->prefill_mode) forget_prefix(m);
   m->prefill_mode = mode;

@@ -150,14 +150,46 @@ hipError_t launch_gated_decode(hipStream_t s, const DevStep* step, const QMatrix
 // ---- the fast prefill mode: products on the bf16 matrix cores ------------
 // A product over bf16 pair operands (prefill_bf16.hip): each weight and each
 // activation as hi + lo bf16, y within about 2^-16 of each product of the
-// exact sum (not the reference's order of addition). Activations come as
-// planes x_hi[t][ldx], x_lo[t][ldx]. With `up`, the gated product: act =
-// gelu(gate) * up, then layer `layer`'s pins, written as fp32 to y (when
-// not null) and as pair planes to y_hi, y_lo. Without, y[t][ldy] fp32; with
-// K split over `splits`, split z's partial sums at y + z * part_stride.
+// exact sum (not the reference's order of addition). The weights come as
+// fragment planes made once by launch_unpack_planes, activations as the
+// planes below, x_hi and x_lo, ldx wide. Gated (the planes of a gate and an up
+// matrix): act = gelu(gate) * up, then layer `layer`'s pins, written as
+// fp32 to y (when not null) and as pair planes to y_hi, y_lo. Otherwise
+// y[t][ldy] fp32; with K split over `splits`, split z's partial sums at
+// y + z * part_stride.
+// Its activation planes (hi and lo, each a block of rows [t][width]) hold
+// element (t, k) in the instruction's fragment order: for each 32-token
+// block and each step of 16 k, 64 lanes x 8 values, lane 32 (k % 16 / 8) +
+// t % 32, so that a wave loads a fragment as one contiguous 1 KB run.
+// width is a multiple of 16; rows are allocated in whole 32-token blocks.
+__host__ __device__ inline size_t plane_index(int t, int k, int width) {
+  return ((((size_t)(t >> 5) * (width >> 4) + (k >> 4)) * 64 + ((k >> 3) & 1) * 32 + (t & 31))
+          << 3) +
+         (k & 7);
+}
+// Four values of row t from k (k % 4 == 0) as bf16 pairs, hi = bf16(v) and
+// lo = bf16(v - hi), both rounded to nearest even.
+__device__ inline void store_pairs4(uint16_t* hi, uint16_t* lo, int t, int k, int width,
+                                    const float (&v)[4]) {
+  uint32_t hw[2], lw[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const __bf16 a = (__bf16)v[2 * e], b = (__bf16)v[2 * e + 1];
+    const __bf16 c = (__bf16)(v[2 * e] - (float)a), d = (__bf16)(v[2 * e + 1] - (float)b);
+    hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    lw[e] = (uint32_t)__builtin_bit_cast(uint16_t, c) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
+  }
+  const size_t at = plane_index(t, k, width);
+  *reinterpret_cast<uint2*>(hi + at) = make_uint2(hw[0], hw[1]);
+  *reinterpret_cast<uint2*>(lo + at) = make_uint2(lw[0], lw[1]);
+}
 struct Bf16Gemm {
-  QMatrix w;
-  QMatrix up{};
+  const uint4* w = nullptr;  // fragment planes
+  int rows = 0;              // output rows (neurons, gated)
+  int cols = 0;              // K
+  bool gated = false;
   const uint16_t* x_hi = nullptr;
   const uint16_t* x_lo = nullptr;
   int ldx = 0;
@@ -168,21 +200,27 @@ struct Bf16Gemm {
   uint16_t* y_lo = nullptr;
   const uint32_t* edits = nullptr;
   int layer = 0;
-  int k_blocks = 0;  // set by the launcher
+  int k_blocks = 0, token_tiles = 0, splits = 1;  // set by the launcher
 };
 constexpr int kMaxBf16Splits = 16;  // K splits a bf16 product may take
 bool bf16_gemm_shape_ok(const QMatrix& w, int ldx, int ldy);
+// Bytes of a matrix's fragment planes (gated: a gate and an up matrix of
+// `rows` rows each).
+size_t bf16_planes_bytes(int rows, int cols, bool gated);
+// w's (with `up`, the gate w's and up's) weights as fragment planes at out.
+hipError_t launch_unpack_planes(hipStream_t s, const QMatrix& w, const QMatrix* up, uint4* out);
 // The K splits a product of this shape takes to fill the device.
-int bf16_splits_for(const QMatrix& w, int max_tokens, bool gated);
+int bf16_splits_for(int rows, int cols, int max_tokens, bool gated);
 hipError_t launch_gemm_bf16(hipStream_t s, const DevStep* step, Bf16Gemm g, int max_tokens,
                             int splits);
 // y[t][o] = the `count` splits' partial sums (stride floats apart) in order.
 hipError_t launch_sum_parts(hipStream_t s, const DevStep* step, const float* parts,
                             size_t stride, int count, int width, int ld, float* y,
                             int max_tokens);
-// Rows of fp32 values into bf16 pair planes (hi = bf16(x), lo = bf16(x - hi)).
+// Rows of fp32 values into bf16 pair planes (hi = bf16(x), lo = bf16(x - hi)),
+// plane_index order, width wide.
 hipError_t launch_split_rows(hipStream_t s, const DevStep* step, const float* x, int ldx,
-                             int width, uint16_t* hi, uint16_t* lo, int ldo, int max_tokens);
+                             int width, uint16_t* hi, uint16_t* lo, int max_tokens);
 
 // The fast prefill mode's attention (attention_fast.hip): each (32-row
 // block, 64-key chunk) of a step's rows as chunk states on the f16 matrix
@@ -234,7 +272,7 @@ struct NormArgs {
   size_t parts_stride = 0;
   int part_count = kSplitParts;
   // Not null: the normed row is also written as bf16 pair planes (the fast
-  // prefill products' inputs), row t at t * width.
+  // prefill products' inputs, plane_index order).
   uint16_t* normed_hi = nullptr;
   uint16_t* normed_lo = nullptr;
 };
@@ -354,7 +392,8 @@ struct FoldArgs {
   int window;
   int max_chunks;
   float* store_stats = nullptr;  // the last row's (m, l) a head, when not null
-  // Not null (steps of several rows): the output also as bf16 pair planes.
+  // Not null (steps of several rows): the output also as bf16 pair planes
+  // (plane_index order).
   uint16_t* out_hi = nullptr;
   uint16_t* out_lo = nullptr;
 };

@@ -14,20 +14,31 @@
 // fp32 accumulation adds the usual K 2^-24 (matmul.h:71-78 states the
 // reference's own bound, gamma(2K)).
 //
-// Weights are decoded from their blocks to bf16 pairs in registers and
-// staged in LDS; activations arrive as bf16 pair planes (hi and lo, each
-// [tokens][K]), written by the kernel that produced them.
+// The weights' pairs are made once (unpack_planes_kernel) into "fragment
+// planes": for each 128-row tile and each step of 16 k, four 32-row blocks
+// x (hi, lo) x 64 lanes x 16 bytes, lane L holding row L % 32's eight
+// weights from k 8 (L / 32), the order in which the instruction's lanes
+// read their operand. The gated product's tile is 64 neurons: its blocks 0
+// and 1 are their gate rows, 2 and 3 their up rows. Activations arrive as
+// bf16 pair planes (hi and lo) in the same fragment order, written by the
+// kernel that produced them (plane_index). Gemma-3-1B's weight planes take
+// 107 MB a layer, 2.8 GB in all.
 //
-// Tiles: a workgroup of four waves owns 128 output rows x 128 tokens and
-// steps K one 32-weight block at a time, double-buffered in LDS. Wave w
-// takes row blocks {w / 2, w / 2 + 2} (32 rows each) and token blocks
-// {2 (w % 2), 2 (w % 2) + 1}: for the gated product, row blocks 0 and 1 are
-// 64 neurons' gate rows and 2 and 3 the same neurons' up rows, so a wave
-// holds each neuron's gate and up sums in matching registers and applies
-// GELU and the pins in registers. LDS holds each operand in the order the
-// instruction reads it (16 bytes a lane, a wave's 64 lanes contiguous).
-// K may be split over grid z: split z writes its partial sums at
+// Tiles: a workgroup of four waves (one a SIMD) owns 128 output rows x 256
+// tokens and steps K one 32-weight block at a time. Wave w computes all
+// 128 rows for tokens 64 w .. 64 w + 63 (eight 32 x 32 accumulators): the
+// weights, which all four waves read, pass through LDS (double-buffered);
+// each wave's token fragments, which only it reads, go straight into its
+// registers. Loads run ahead and are copied as they are (no VALU). The
+// instruction takes the tokens as its A operand and the weights as B, so
+// that each output register's lanes are 32 consecutive rows of one token.
+// For the gated product, row blocks 0 and 1 are 64 neurons' gate rows and
+// 2 and 3 their up rows, so a wave holds each neuron's gate and up sums in
+// matching registers and applies GELU (fast form) and the pins in
+// registers. K may be split: split z writes its partial sums at
 // y + z * part_stride, added in split order by the consumer.
+
+#include <algorithm>
 
 #include "edit_common.h"
 #include "kernels.h"
@@ -41,20 +52,9 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileRows = 128;
-constexpr int kTileTokens = 128;
+constexpr int kTileTokens = 256;
 constexpr int kThreads = 256;
-
-// One K block's operands: [row or token block][k half][hi, lo][slot]. The
-// instruction's lane L (row L % 32, k sub-block L / 32) reads slot
-// 32 sub + (row ^ 4 sub): eight lanes reading eight rows of one sub-block,
-// and a pair of threads writing one row's two sub-blocks four rows at a
-// time, each touch eight distinct 16-byte bank groups.
-__device__ __forceinline__ int slot_of(int row, int sub) { return 32 * sub + (row ^ (sub << 2)); }
-
-struct Stage {
-  uint4 w[4][2][2][64];
-  uint4 x[4][2][2][64];
-};
+constexpr int kStepBytes = 8 * 1024;       // a tile's weights for one step: 4 blocks x 2 planes
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -91,53 +91,33 @@ struct WeightLoad {
   uint32_t scale;  // d, and m in the high half for Q4_1
 };
 
-// A load from global memory, said so: a pointer chosen among a fused
-// product's members would otherwise load through the flat path, whose
-// waits also hold back LDS reads.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint4 load_global4(const void* p) {
-  const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)(p);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint2 load_global2(const void* p) {
-  const u32x2 v = *(const __attribute__((address_space(1))) u32x2*)(p);
-  return make_uint2(v.x, v.y);
-}
-template <typename T>
-__device__ __forceinline__ T load_global(const void* p) {
-  return *(const __attribute__((address_space(1))) T*)(p);
-}
-
 template <int FORMAT>
 __device__ __forceinline__ WeightLoad<FORMAT> load_weights(const MemberRow& m, int blocks, int kb,
                                                            int h) {
   WeightLoad<FORMAT> r;
   const size_t b = (size_t)m.row * blocks + kb;
   if (FORMAT == kQ8_0) {
-    r.codes = load_global4(m.codes + b * 32 + 16 * h);
+    r.codes = *reinterpret_cast<const uint4*>(m.codes + b * 32 + 16 * h);
   } else {
-    const uint2 c = load_global2(m.codes + b * 16 + 8 * h);
+    const uint2 c = *reinterpret_cast<const uint2*>(m.codes + b * 16 + 8 * h);
     r.codes = make_uint4(c.x, c.y, 0, 0);
   }
   if (FORMAT == kQ4_1) {
-    r.scale = load_global<uint32_t>(m.scales + 2 * b);
+    r.scale = *reinterpret_cast<const uint32_t*>(m.scales + 2 * b);
   } else {
-    r.scale = load_global<uint16_t>(m.scales + b);
+    r.scale = m.scales[b];
   }
   return r;
 }
 
-// Decodes a thread's weights and writes them to the stage as bf16 pairs:
-// rows r of the tile (row block r / 32, lane r % 32 + 32 sub).
+// A thread's weights as bf16 pairs: out[0], out[1] are (hi, lo) of its
+// first eight weights, out[2], out[3] of its second eight (Q4: k 8h + j and
+// 16 + 8h + j; Q8_0: k 16h + j and 16h + 8 + j).
 template <int FORMAT>
-__device__ __forceinline__ void stage_weights(Stage& st, const WeightLoad<FORMAT>& in, int r,
-                                              int h) {
-  const int rb = r >> 5, lane = r & 31;
+__device__ __forceinline__ void decode_pairs(const WeightLoad<FORMAT>& in, uint4 (&out)[4]) {
   const float d = half_bits_to_float(in.scale & 0xFFFFu);
   float a[8], b[8];
   if (FORMAT == kQ8_0) {
-    // weights 16h..16h+15: k half h, lanes lane (first 8) and lane + 32
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t w0 = j < 4 ? in.codes.x : in.codes.y;
@@ -146,81 +126,81 @@ __device__ __forceinline__ void stage_weights(Stage& st, const WeightLoad<FORMAT
       a[j] = (float)(int)(int8_t)(w0 >> sh) * d;
       b[j] = (float)(int)(int8_t)(w1 >> sh) * d;
     }
-    uint4 hi, lo;
-    split8(a, hi, lo);
-    st.w[rb][h][0][slot_of(lane, 0)] = hi;
-    st.w[rb][h][1][slot_of(lane, 0)] = lo;
-    split8(b, hi, lo);
-    st.w[rb][h][0][slot_of(lane, 1)] = hi;
-    st.w[rb][h][1][slot_of(lane, 1)] = lo;
-    return;
-  }
-  // Q4_0, Q4_1: low nibbles are weights 8h + j (k half 0, sub h), high
-  // nibbles 16 + 8h + j (k half 1, sub h). A nibble masked under the
-  // exponent of f16 1024 is the half 1024 + q (two at once, from bits 0 and
-  // 16 of a shifted code word). Q4_0: fma(1024 + q, d, -1032 d) = (q - 8) d,
-  // exact; Q4_1: fma(q, d, m) = q d + m rounded once, as q4_1.wgsl:12-25
-  // computes it (q = (1024 + q) - 1024 exactly).
-  const float c = FORMAT == kQ4_1 ? 0.0f : -1032.0f * d;  // exact
-  const uint32_t w2[2] = {in.codes.x, in.codes.y};
+  } else {
+    // A nibble masked under the exponent of f16 1024 is the half 1024 + q
+    // (two at once, from bits 0 and 16 of a shifted code word). Q4_0:
+    // fma(1024 + q, d, -1032 d) = (q - 8) d, exact; Q4_1: fma(q, d, m) =
+    // q d + m rounded once, as q4_1.wgsl:12-25 computes it (q = (1024 + q)
+    // - 1024 exactly).
+    const float c = FORMAT == kQ4_1 ? 0.0f : -1032.0f * d;  // exact
+    const uint32_t w2[2] = {in.codes.x, in.codes.y};
 #pragma unroll
-  for (int wd = 0; wd < 2; ++wd) {
+    for (int wd = 0; wd < 2; ++wd) {
 #pragma unroll
-    for (int sh = 0; sh < 4; ++sh) {
-      // shift 0: weights j, j + 2 (low nibbles); 4: 16 + j, 16 + j + 2;
-      // 8: j + 1, j + 3; 12: 16 + j + 1, 16 + j + 3 (j = 4 wd)
-      const uint32_t bits = ((w2[wd] >> (4 * sh)) & 0x000F000Fu) | 0x64006400u;
-      const half2v q = __builtin_bit_cast(half2v, bits);
-      float v0, v1;
-      if (FORMAT == kQ4_1) {
-        const float mn = half_bits_to_float(in.scale >> 16);
-        v0 = __builtin_fmaf((float)q.x - 1024.0f, d, mn);
-        v1 = __builtin_fmaf((float)q.y - 1024.0f, d, mn);
-      } else {
-        v0 = __builtin_fmaf((float)q.x, d, c);
-        v1 = __builtin_fmaf((float)q.y, d, c);
+      for (int sh = 0; sh < 4; ++sh) {
+        // shift 0: weights j, j + 2 (low nibbles); 4: 16 + j, 16 + j + 2;
+        // 8: j + 1, j + 3; 12: 16 + j + 1, 16 + j + 3 (j = 4 wd)
+        const uint32_t bits = ((w2[wd] >> (4 * sh)) & 0x000F000Fu) | 0x64006400u;
+        const half2v q = __builtin_bit_cast(half2v, bits);
+        float v0, v1;
+        if (FORMAT == kQ4_1) {
+          const float mn = half_bits_to_float(in.scale >> 16);
+          v0 = __builtin_fmaf((float)q.x - 1024.0f, d, mn);
+          v1 = __builtin_fmaf((float)q.y - 1024.0f, d, mn);
+        } else {
+          v0 = __builtin_fmaf((float)q.x, d, c);
+          v1 = __builtin_fmaf((float)q.y, d, c);
+        }
+        const int j = 4 * wd + (sh >> 1);
+        float* dst = (sh & 1) ? b : a;
+        dst[j] = v0;
+        dst[j + 2] = v1;
       }
-      const int j = 4 * wd + (sh >> 1);
-      float* dst = (sh & 1) ? b : a;
-      dst[j] = v0;
-      dst[j + 2] = v1;
     }
   }
-  const int l = slot_of(lane, h);
-  uint4 hi, lo;
-  split8(a, hi, lo);
-  st.w[rb][0][0][l] = hi;
-  st.w[rb][0][1][l] = lo;
-  split8(b, hi, lo);
-  st.w[rb][1][0][l] = hi;
-  st.w[rb][1][1][l] = lo;
+  split8(a, out[0], out[1]);
+  split8(b, out[2], out[3]);
 }
 
-// A thread's share of one K block of the activations: token tk of the
-// tile, sub-block `sub` of each k half (k 16 s + 8 sub .. + 7, s = 0, 1),
-// 8 values of each plane each.
-struct InputLoad {
-  uint4 hi[2], lo[2];
-};
-
-__device__ __forceinline__ InputLoad load_inputs(const uint16_t* __restrict__ x_hi,
-                                                 const uint16_t* __restrict__ x_lo, size_t row,
-                                                 int kb, int sub) {
-  InputLoad r;
-  const size_t at = row + (size_t)kb * 32 + 8 * sub;
-  r.hi[0] = load_global4(x_hi + at);
-  r.hi[1] = load_global4(x_hi + at + 16);
-  r.lo[0] = load_global4(x_lo + at);
-  r.lo[1] = load_global4(x_lo + at + 16);
-  return r;
+// The first uint4 of fragment (tile n, step s, block b, plane p).
+__host__ __device__ inline size_t fragment_at(int n, int steps, int s, int b, int p) {
+  return ((((size_t)n * steps + s) * 4 + b) * 2 + p) * 64;
 }
 
-__device__ __forceinline__ void stage_inputs(Stage& st, const InputLoad& in, int tk, int sub) {
-  const int cb = tk >> 5, l = slot_of(tk & 31, sub);
-  st.x[cb][0][0][l] = in.hi[0];
-  st.x[cb][0][1][l] = in.lo[0];
-  st.x[cb][1][0][l] = in.hi[1];
-  st.x[cb][1][1][l] = in.lo[1];
+// A thread a (tile, K block, block, half h, row of the block): the row's
+// half block as pairs into the fragment planes; rows past the matrix are
+// zeros. Consecutive threads write consecutive lanes.
+template <int FORMAT, bool GATED>
+__global__ __launch_bounds__(256) void unpack_planes_kernel(QMatrix w, QMatrix up, int tiles,
+                                                            uint4* __restrict__ out) {
+  const int blocks = w.cols / 32, steps = w.cols / 16;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)tiles * blocks * 256) return;
+  const int r = (int)(i & 31), h = (int)((i >> 5) & 1), b = (int)((i >> 6) & 3);
+  const size_t rest = i >> 8;
+  const int kb = (int)(rest % (size_t)blocks), n = (int)(rest / (size_t)blocks);
+  const int row = GATED ? n * 64 + 32 * (b & 1) + r : n * kTileRows + 32 * b + r;
+  uint4 q[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q[j] = make_uint4(0, 0, 0, 0);
+  if (row < w.rows) {
+    const MemberRow src = GATED && b >= 2 ? member_row(up, row) : member_row(w, row);
+    decode_pairs<FORMAT>(load_weights<FORMAT>(src, blocks, kb, h), q);
+  }
+  if (FORMAT == kQ8_0) {
+    const size_t f = fragment_at(n, steps, 2 * kb + h, b, 0);
+    out[f + r] = q[0];
+    out[f + 64 + r] = q[1];
+    out[f + 32 + r] = q[2];
+    out[f + 96 + r] = q[3];
+  } else {
+    const size_t f0 = fragment_at(n, steps, 2 * kb, b, 0) + 32 * h + r;
+    const size_t f1 = fragment_at(n, steps, 2 * kb + 1, b, 0) + 32 * h + r;
+    out[f0] = q[0];
+    out[f0 + 64] = q[1];
+    out[f1] = q[2];
+    out[f1 + 64] = q[3];
+  }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -232,43 +212,60 @@ __device__ __noinline__ float pin_one(const uint32_t* __restrict__ t, uint32_t f
   return apply_pin_words(t, first, count, (uint32_t)n, position, value);
 }
 
-template <int FORMAT, bool GATED>
-__global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* __restrict__ step,
+// A load from global memory, said so: through a flat pointer the
+// compiler's waits for it would also hold back LDS reads.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_global4(const void* p) {
+  const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// GELU, tanh form, from the hardware's exp2 and reciprocal: 0.5 g (1 +
+// tanh z) = g / (1 + e^-2z). Within 2^-20 relative of the exact form
+// (matmul.wgsl:141-147) for the fast mode's tolerance, not its bits.
+__device__ __forceinline__ float gelu_fast(float g) {
+  const float z = 0.7978845608028654f * __builtin_fmaf(0.044715f * g * g, g, g);
+  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * z);  // -2 z log2(e)
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// A wave's share of one K block (two steps of 16 k): its weight block's
+// fragments [step][hi, lo], staged in LDS for the workgroup, and its two
+// token blocks' [block][step][hi, lo], which only it reads.
+struct WeightLoad2 {
+  uint4 w[2][2];
+};
+struct TokenLoad {
+  uint4 x[2][2][2];
+};
+
+template <bool GATED>
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* __restrict__ step,
                                                                 Bf16Gemm g) {
-  __shared__ Stage stage[2];
+  // The weights of one K block: [step][row block][hi, lo][lane].
+  __shared__ uint4 stage[2][2][4][2][64];
   const int tokens = (int)step->tokens;
-  const int n0 = blockIdx.y * kTileTokens;
+  // Workgroups go to the eight XCDs in turn (linear id mod 8); the tile
+  // order gives each XCD a contiguous run of tiles, so that the token tiles
+  // of one row tile (the same weights) share an L2.
+  const int total = (int)gridDim.x, wid = (int)blockIdx.x;
+  const int xcd = wid & 7, per = total >> 3, extra = total & 7;
+  const int tile = xcd * per + min(xcd, extra) + (wid >> 3);
+  const int tt = tile % g.token_tiles, rest = tile / g.token_tiles;
+  const int z = rest % g.splits, rt = rest / g.splits;
+  const int n0 = tt * kTileTokens;
   if (n0 >= tokens) return;  // the whole workgroup: past the step's rows
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  const int my_slot = slot_of(lane & 31, lane >> 5);
-  const int blocks = g.w.cols / 32;
-  const int kb0 = blockIdx.z * g.k_blocks;
-  const int kb1 = min(blocks, kb0 + g.k_blocks);
+  const int steps = g.cols / 16;
+  const int kb0 = z * g.k_blocks;
+  const int kb1 = min(g.cols / 32, kb0 + g.k_blocks);
 
-  // This thread's weight row (r of the tile) and half block h (a pair of
-  // threads reads one row's 16 code bytes).
-  const int r = tid >> 1, h = tid & 1;
-  int out_rows, row;
-  MemberRow src;
-  if (GATED) {
-    out_rows = g.w.rows;
-    const int n = blockIdx.x * (kTileRows / 2) + (r & 63);
-    row = min(n, out_rows - 1);
-    src = member_row(r < 64 ? g.w : g.up, row);
-  } else {
-    out_rows = g.w.rows;
-    row = min((int)blockIdx.x * kTileRows + r, out_rows - 1);
-    src = member_row(g.w, row);
-  }
-  // This thread's input token and k sub-block (a pair reads 64 bytes of a
-  // row).
-  const int tk = tid >> 1, kh = tid & 1;
-  const size_t x_row = (size_t)min(n0 + tk, tokens - 1) * g.ldx;
-
-  f32x16 acc[2][2];
+  // acc[row block][token block of the wave], transposed: the instruction
+  // takes the tokens as its A operand and the weights as B, so a lane holds
+  // one output row (lane % 32) for 16 tokens.
+  f32x16 acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -278,161 +275,180 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const DevStep* _
   // writes zero partial sums.
   if (kb0 >= kb1) {
     if (!GATED) {
-      float* y = g.y + (size_t)blockIdx.z * g.part_stride;
+      float* y = g.y + (size_t)z * g.part_stride;
       for (int i = tid; i < kTileRows * kTileTokens; i += kThreads) {
-        const int o = blockIdx.x * kTileRows + (i % kTileRows), t = n0 + i / kTileRows;
-        if (o < out_rows && t < tokens) y[(size_t)t * g.ldy + o] = 0.0f;
+        const int o = rt * kTileRows + (i % kTileRows), t = n0 + i / kTileRows;
+        if (o < g.rows && t < tokens) y[(size_t)t * g.ldy + o] = 0.0f;
       }
     }
     return;
   }
-  // Loads run three blocks ahead, into three register sets a, b, c: while
-  // block kb computes from one LDS buffer, block kb + 1 (loaded two blocks
-  // ago) is decoded into the other, and block kb + 3 is requested into the
-  // set block kb came from. Every load is issued whatever kb (past the last
-  // block it reloads the last), so the waits count exactly the loads they
-  // need.
-  WeightLoad<FORMAT> wa = load_weights<FORMAT>(src, blocks, kb0, h);
-  InputLoad xa = load_inputs(g.x_hi, g.x_lo, x_row, kb0, kh);
-  WeightLoad<FORMAT> wb = load_weights<FORMAT>(src, blocks, min(kb0 + 1, kb1 - 1), h);
-  InputLoad xb = load_inputs(g.x_hi, g.x_lo, x_row, min(kb0 + 1, kb1 - 1), kh);
-  WeightLoad<FORMAT> wc_ = load_weights<FORMAT>(src, blocks, min(kb0 + 2, kb1 - 1), h);
-  InputLoad xc = load_inputs(g.x_hi, g.x_lo, x_row, min(kb0 + 2, kb1 - 1), kh);
-  stage_weights<FORMAT>(stage[0], wa, r, h);
-  stage_inputs(stage[0], xa, tk, kh);
-  __syncthreads();
-  auto block_step = [&](int kb, const Stage& cur, Stage& next, WeightLoad<FORMAT>& w_free,
-                        InputLoad& x_free, const WeightLoad<FORMAT>& w_next,
-                        const InputLoad& x_next) {
-    // The next block is staged into the other buffer first (it was last
-    // read before the previous barrier), so its decode can run while this
-    // block's products do.
-    stage_weights<FORMAT>(next, w_next, r, h);
-    stage_inputs(next, x_next, tk, kh);
-    const int ahead = min(kb + 3, kb1 - 1);
-    w_free = load_weights<FORMAT>(src, blocks, ahead, h);
-    x_free = load_inputs(g.x_hi, g.x_lo, x_row, ahead, kh);
+  // Wave w moves weight block w of the row tile into LDS, and reads its
+  // token blocks 2 w and 2 w + 1 of the tile (the last block with rows, for
+  // blocks past them) straight into registers; every fragment is a 1 KB
+  // run of its planes, 16 bytes a lane.
+  const uint4* wsrc = g.w + fragment_at(rt, steps, 0, wave, 0) + lane;
+  const int last_tb = (tokens - 1) >> 5;
+  const size_t x_at0 = plane_index(32 * min(n0 / 32 + 2 * wave, last_tb), 0, g.ldx) + 8 * lane;
+  const size_t x_at1 = plane_index(32 * min(n0 / 32 + 2 * wave + 1, last_tb), 0, g.ldx) + 8 * lane;
+  auto load_w = [&](int kb) {
+    WeightLoad2 r;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 ah[2], al[2], bh[2], bl[2];
+    for (int u = 0; u < 2; ++u) {
+      const size_t s = 2 * (size_t)kb + u;
+      r.w[u][0] = load_global4(wsrc + s * (kStepBytes / 16));
+      r.w[u][1] = load_global4(wsrc + s * (kStepBytes / 16) + 64);
+    }
+    return r;
+  };
+  auto load_x = [&](int kb) {
+    TokenLoad r;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ah[i] = as_bf16x8(cur.w[wr + 2 * i][ks][0][my_slot]);
-        al[i] = as_bf16x8(cur.w[wr + 2 * i][ks][1][my_slot]);
-        bh[i] = as_bf16x8(cur.x[2 * wc + i][ks][0][my_slot]);
-        bl[i] = as_bf16x8(cur.x[2 * wc + i][ks][1][my_slot]);
+    for (int u = 0; u < 2; ++u) {
+      const size_t s = 2 * (size_t)kb + u;
+      r.x[0][u][0] = load_global4(g.x_hi + x_at0 + 512 * s);
+      r.x[0][u][1] = load_global4(g.x_lo + x_at0 + 512 * s);
+      r.x[1][u][0] = load_global4(g.x_hi + x_at1 + 512 * s);
+      r.x[1][u][1] = load_global4(g.x_lo + x_at1 + 512 * s);
+    }
+    return r;
+  };
+  auto put = [&](uint4 (&st)[2][4][2][64], const WeightLoad2& r) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) st[u][wave][p][lane] = r.w[u][p];
+  };
+  auto compute = [&](const uint4 (&st)[2][4][2][64], const TokenLoad& r) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bf16x8 wh[4], wl[4], xh[2], xl[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wh[i] = as_bf16x8(st[u][i][0][lane]);
+        wl[i] = as_bf16x8(st[u][i][1][lane]);
       }
-      // The three products of each pair, four independent accumulators
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        xh[j] = as_bf16x8(r.x[j][u][0]);
+        xl[j] = as_bf16x8(r.x[j][u][1]);
+      }
+      // The three products of each pair, eight independent accumulators
       // between two that update the same one.
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[j], wh[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[j], wh[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[j], wl[i], acc[i][j], 0, 0, 0);
     }
+  };
+  // Weights run three blocks ahead in three register sets, tokens two
+  // ahead in two. Block kb: the next block's weights (loaded two blocks
+  // ago) go to the other LDS buffer and block kb + 3's are requested into
+  // their set; this block's products run from this buffer and this block's
+  // token fragments; then block kb + 2's tokens are requested into theirs.
+  // Every load is issued whatever kb (past the last block it reloads the
+  // last), so the waits count exactly the loads they need.
+  WeightLoad2 wa = load_w(kb0);
+  TokenLoad xa = load_x(kb0);
+  WeightLoad2 wb = load_w(min(kb0 + 1, kb1 - 1));
+  TokenLoad xb = load_x(min(kb0 + 1, kb1 - 1));
+  WeightLoad2 wc = load_w(min(kb0 + 2, kb1 - 1));
+  put(stage[0], wa);
+  __syncthreads();
+  auto block_step = [&](int kb, const uint4 (&cur)[2][4][2][64], uint4 (&next)[2][4][2][64],
+                        WeightLoad2& w_free, const WeightLoad2& w_next, TokenLoad& x_cur) {
+    put(next, w_next);  // read before the previous barrier
+    w_free = load_w(min(kb + 3, kb1 - 1));
+    compute(cur, x_cur);
+    x_cur = load_x(min(kb + 2, kb1 - 1));
     __syncthreads();
   };
-  // LDS buffers alternate every block, register sets every third: six
-  // blocks a turn.
+  // LDS buffers and token sets alternate every block, weight sets every
+  // third: six blocks a turn.
   for (int kb = kb0; kb < kb1; kb += 6) {
-    block_step(kb, stage[0], stage[1], wa, xa, wb, xb);
+    block_step(kb, stage[0], stage[1], wa, wb, xa);
     if (kb + 1 >= kb1) break;
-    block_step(kb + 1, stage[1], stage[0], wb, xb, wc_, xc);
+    block_step(kb + 1, stage[1], stage[0], wb, wc, xb);
     if (kb + 2 >= kb1) break;
-    block_step(kb + 2, stage[0], stage[1], wc_, xc, wa, xa);
+    block_step(kb + 2, stage[0], stage[1], wc, wa, xa);
     if (kb + 3 >= kb1) break;
-    block_step(kb + 3, stage[1], stage[0], wa, xa, wb, xb);
+    block_step(kb + 3, stage[1], stage[0], wa, wb, xb);
     if (kb + 4 >= kb1) break;
-    block_step(kb + 4, stage[0], stage[1], wb, xb, wc_, xc);
+    block_step(kb + 4, stage[0], stage[1], wb, wc, xa);
     if (kb + 5 >= kb1) break;
-    block_step(kb + 5, stage[1], stage[0], wc_, xc, wa, xa);
+    block_step(kb + 5, stage[1], stage[0], wc, wa, xb);
   }
 
-  // Lane l's register e of a 32 x 32 block: row (e / 4) 8 + (l / 32) 4 +
-  // e % 4, token l % 32.
-  const int row_in = (lane >> 5) * 4;
-  const int tok_in = lane & 31;
+  // Lane l's register e of a 32 x 32 block: token (e / 4) 8 + (l / 32) 4 +
+  // e % 4 of the token block, row l % 32 of the row block. A register's
+  // 32 lanes are 32 consecutive rows of one token: 128 bytes a store.
+  const int row_in = lane & 31;
+  const int tok_in = (lane >> 5) * 4;
   if (GATED) {
+    // Row blocks 0 and 1 are the tile's 64 neurons' gate rows, 2 and 3
+    // their up rows.
     const uint32_t first = g.edits ? g.edits[2 * g.layer] : 0u;
     const uint32_t count = g.edits ? g.edits[2 * g.layer + 1] : 0u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = n0 + (2 * wc + j) * 32 + tok_in;
-      const uint32_t position = step->position + (uint32_t)t;
+    for (int i = 0; i < 2; ++i) {
+      const int n = rt * (kTileRows / 2) + i * 32 + row_in;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nb = blockIdx.x * (kTileRows / 2) + wr * 32 + q * 8 + row_in;
-        float v[4];
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(acc[0][j][4 * q + e]) * acc[1][j][4 * q + e];
-        if (count) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = pin_one(g.edits, first, count, nb + e, position, v[e]);
+        for (int e = 0; e < 16; ++e) {
+          const int t = n0 + (2 * wave + j) * 32 + (e >> 2) * 8 + tok_in + (e & 3);
+          float v = gelu_fast(acc[i][j][e]) * acc[i + 2][j][e];
+          if (count) v = pin_one(g.edits, first, count, n, step->position + (uint32_t)t, v);
+          if (t >= tokens || n >= g.rows) continue;
+          if (g.y) g.y[(size_t)t * g.ldy + n] = v;
+          const __bf16 h = (__bf16)v, l = (__bf16)(v - (float)h);
+          const size_t at = plane_index(t, n, g.ldy);
+          g.y_hi[at] = __builtin_bit_cast(uint16_t, h);
+          g.y_lo[at] = __builtin_bit_cast(uint16_t, l);
         }
-        if (t >= tokens || nb >= out_rows) continue;
-        const size_t at = (size_t)t * g.ldy + nb;
-        if (g.y) *reinterpret_cast<float4*>(g.y + at) = make_float4(v[0], v[1], v[2], v[3]);
-        uint32_t hw[2], lw[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const __bf16 a = (__bf16)v[2 * e], b = (__bf16)v[2 * e + 1];
-          const __bf16 c = (__bf16)(v[2 * e] - (float)a), d = (__bf16)(v[2 * e + 1] - (float)b);
-          hw[e] = (uint32_t)__builtin_bit_cast(uint16_t, a) |
-                  ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-          lw[e] = (uint32_t)__builtin_bit_cast(uint16_t, c) |
-                  ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
-        }
-        *reinterpret_cast<uint2*>(g.y_hi + at) = make_uint2(hw[0], hw[1]);
-        *reinterpret_cast<uint2*>(g.y_lo + at) = make_uint2(lw[0], lw[1]);
-      }
     }
     return;
   }
-  float* y = g.y + (size_t)blockIdx.z * g.part_stride;
+  float* y = g.y + (size_t)z * g.part_stride;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const int o = rt * kTileRows + i * 32 + row_in;
+    if (o >= g.rows) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = n0 + (2 * wc + j) * 32 + tok_in;
-      if (t >= tokens) continue;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int o = blockIdx.x * kTileRows + (wr + 2 * i) * 32 + q * 8 + row_in;
-        if (o >= out_rows) continue;
-        *reinterpret_cast<float4*>(y + (size_t)t * g.ldy + o) =
-            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                        acc[i][j][4 * q + 3]);
+      for (int e = 0; e < 16; ++e) {
+        const int t = n0 + (2 * wave + j) * 32 + (e >> 2) * 8 + tok_in + (e & 3);
+        if (t < tokens) y[(size_t)t * g.ldy + o] = acc[i][j][e];
       }
-    }
+  }
 }
 
-// Rows of fp32 values into bf16 pair planes: hi[t][k] = bf16(x), lo[t][k] =
-// bf16(x - hi). A workgroup a row, eight values a thread a step.
+// Rows of fp32 values into bf16 pair planes (plane_index order): hi =
+// bf16(x), lo = bf16(x - hi). A workgroup a row, four values a thread a
+// step.
 __global__ __launch_bounds__(256) void split_rows_kernel(const DevStep* __restrict__ step,
                                                          const float* __restrict__ x, int ldx,
                                                          int width, uint16_t* __restrict__ hi,
-                                                         uint16_t* __restrict__ lo, int ldo) {
+                                                         uint16_t* __restrict__ lo) {
   const int t = blockIdx.x;
   if (t >= (int)step->tokens) return;
   const float* xr = x + (size_t)t * ldx;
-  for (int k = 8 * threadIdx.x; k < width; k += 8 * 256) {
+  for (int k = 4 * threadIdx.x; k < width; k += 4 * 256) {
     const float4 a = *reinterpret_cast<const float4*>(xr + k);
-    const float4 b = *reinterpret_cast<const float4*>(xr + k + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint4 h, l;
-    split8(v, h, l);
-    *reinterpret_cast<uint4*>(hi + (size_t)t * ldo + k) = h;
-    *reinterpret_cast<uint4*>(lo + (size_t)t * ldo + k) = l;
+    const float v[4] = {a.x, a.y, a.z, a.w};
+    store_pairs4(hi, lo, t, k, width, v);
   }
 }
 
@@ -452,12 +468,16 @@ __global__ __launch_bounds__(256) void sum_parts_kernel(const DevStep* __restric
   }
 }
 
+int row_tiles_of(int rows, bool gated) {
+  return gated ? (rows + kTileRows / 2 - 1) / (kTileRows / 2) : (rows + kTileRows - 1) / kTileRows;
+}
+
 template <int FORMAT, bool GATED>
-hipError_t launch_one(hipStream_t s, const DevStep* step, const Bf16Gemm& g, int max_tokens,
-                      int splits) {
-  const int m_tiles = GATED ? (g.w.rows + 63) / 64 : (g.w.rows + kTileRows - 1) / kTileRows;
-  const dim3 grid(m_tiles, (max_tokens + kTileTokens - 1) / kTileTokens, splits);
-  hipLaunchKernelGGL((gemm_bf16_kernel<FORMAT, GATED>), grid, dim3(kThreads), 0, s, step, g);
+hipError_t launch_unpack(hipStream_t s, const QMatrix& w, const QMatrix& up, uint4* out) {
+  const int tiles = row_tiles_of(w.rows, GATED);
+  const size_t threads = (size_t)tiles * (w.cols / 32) * 256;
+  hipLaunchKernelGGL((unpack_planes_kernel<FORMAT, GATED>), dim3((unsigned)(threads / 256)),
+                     dim3(256), 0, s, w, up, tiles, out);
   return hipGetLastError();
 }
 
@@ -468,35 +488,60 @@ bool bf16_gemm_shape_ok(const QMatrix& w, int ldx, int ldy) {
          (w.format == kQ4_0 || w.format == kQ4_1 || w.format == kQ8_0);
 }
 
-int bf16_splits_for(const QMatrix& w, int max_tokens, bool gated) {
-  // Enough workgroups to fill 256 CUs twice, in whole K blocks a split.
-  const int tiles = (gated ? (w.rows + 63) / 64 : (w.rows + kTileRows - 1) / kTileRows) *
-                    ((max_tokens + kTileTokens - 1) / kTileTokens);
+size_t bf16_planes_bytes(int rows, int cols, bool gated) {
+  return (size_t)row_tiles_of(rows, gated) * (cols / 16) * kStepBytes;
+}
+
+hipError_t launch_unpack_planes(hipStream_t s, const QMatrix& w, const QMatrix* up, uint4* out) {
+  const QMatrix none{};
+  if (up) {
+    if (up->format != w.format || up->rows != w.rows || up->cols != w.cols)
+      return hipErrorInvalidValue;
+    switch (w.format) {
+      case kQ4_1: return launch_unpack<kQ4_1, true>(s, w, *up, out);
+      case kQ8_0: return launch_unpack<kQ8_0, true>(s, w, *up, out);
+      default: return launch_unpack<kQ4_0, true>(s, w, *up, out);
+    }
+  }
+  switch (w.format) {
+    case kQ4_1: return launch_unpack<kQ4_1, false>(s, w, none, out);
+    case kQ8_0: return launch_unpack<kQ8_0, false>(s, w, none, out);
+    default: return launch_unpack<kQ4_0, false>(s, w, none, out);
+  }
+}
+
+int bf16_splits_for(int rows, int cols, int max_tokens, bool gated) {
+  // As many workgroups as the 256 CUs hold (one each), at least two K
+  // blocks a split, and no split left empty.
   if (gated) return 1;
-  int splits = 1;
-  const int blocks = w.cols / 32;
-  while (tiles * splits < 384 && splits < 8 && blocks / (2 * splits) >= 4) splits *= 2;
-  return splits;
+  const int tiles = row_tiles_of(rows, false) * ((max_tokens + kTileTokens - 1) / kTileTokens);
+  const int blocks = cols / 32;
+  int splits = std::min({kMaxBf16Splits, std::max(1, 256 / tiles), std::max(1, blocks / 2)});
+  const int per = (blocks + splits - 1) / splits;
+  return (blocks + per - 1) / per;
 }
 
 hipError_t launch_gemm_bf16(hipStream_t s, const DevStep* step, Bf16Gemm g, int max_tokens,
                             int splits) {
-  const int blocks = g.w.cols / 32;
-  const bool gated = g.up.codes != nullptr;
-  if (gated || splits < 1) splits = 1;
+  // The activation planes are as wide as K; the gated product's output
+  // planes as wide as its rows.
+  if (!g.w || g.cols % 32 || g.rows <= 0 || g.ldx != g.cols || max_tokens <= 0 ||
+      max_tokens > kPrefillBlock || (g.gated && g.ldy % 16))
+    return hipErrorInvalidValue;
+  const int blocks = g.cols / 32;
+  if (g.gated || splits < 1) splits = 1;
+  g.splits = splits;
   g.k_blocks = (blocks + splits - 1) / splits;
-  switch (g.w.format) {
-    case kQ4_1:
-      return gated ? launch_one<kQ4_1, true>(s, step, g, max_tokens, 1)
-                   : launch_one<kQ4_1, false>(s, step, g, max_tokens, splits);
-    case kQ8_0:
-      return gated ? launch_one<kQ8_0, true>(s, step, g, max_tokens, 1)
-                   : launch_one<kQ8_0, false>(s, step, g, max_tokens, splits);
-    default:
-      return gated ? launch_one<kQ4_0, true>(s, step, g, max_tokens, 1)
-                   : launch_one<kQ4_0, false>(s, step, g, max_tokens, splits);
+  g.token_tiles = (max_tokens + kTileTokens - 1) / kTileTokens;
+  const int tiles = row_tiles_of(g.rows, g.gated) * splits * g.token_tiles;
+  if (g.gated) {
+    hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(tiles), dim3(kThreads), 0, s, step, g);
+  } else {
+    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(tiles), dim3(kThreads), 0, s, step, g);
   }
+  return hipGetLastError();
 }
+
 
 hipError_t launch_sum_parts(hipStream_t s, const DevStep* step, const float* parts,
                             size_t stride, int count, int width, int ld, float* y,
@@ -507,9 +552,10 @@ hipError_t launch_sum_parts(hipStream_t s, const DevStep* step, const float* par
 }
 
 hipError_t launch_split_rows(hipStream_t s, const DevStep* step, const float* x, int ldx,
-                             int width, uint16_t* hi, uint16_t* lo, int ldo, int max_tokens) {
+                             int width, uint16_t* hi, uint16_t* lo, int max_tokens) {
+  if (width % 16) return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_rows_kernel, dim3(max_tokens), dim3(256), 0, s, step, x, ldx, width,
-                     hi, lo, ldo);
+                     hi, lo);
   return hipGetLastError();
 }
 

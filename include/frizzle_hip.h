@@ -116,7 +116,8 @@ int frz_op_gated(frz_device* dev, const void* gate_codes,
 /* The fast prefill mode's products (FRZ_PREFILL_BF16), op by op: y = W x
  * over bf16 pair operands, K split over `splits` (1 to 16; 0: as the model
  * splits it) and the splits added in order; and the gated product with its
- * pins. x is split into pair planes first. Within about 2^-16 of each
+ * pins (rows a multiple of 16). The weights are unpacked into bf16 pair
+ * planes and x split into pair planes first. Within about 2^-16 of each
  * product of the exact sum, not the reference's order (no counterpart in
  * the reference, which computes in fp32). */
 int frz_op_gemm_bf16(frz_device* dev, int format, const void* codes, const void* scales,
