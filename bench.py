@@ -93,6 +93,10 @@ def parse():
                    help="only the floors: an empty kernel's launch (on the stream and "
                         "graph-replayed) and streaming reads of each decode product's "
                         "weight bytes (one JSON line)")
+    p.add_argument("--library-gemm", action="store_true",
+                   help="only: the vendor bf16 GEMM (torch matmul, hipBLASLt) at the fast "
+                        "prefill's product shapes, one product each, for scale (one JSON "
+                        "line)")
     p.add_argument("--gemv-stream", action="store_true",
                    help="with --roofline-only, time the GEMV launches back to back on the "
                         "stream (not each between its own events); with --probes, the "
@@ -385,6 +389,33 @@ def timed_decode(model, dev, prompt, warmup, steps, greedy):
     return prefill_s, time.perf_counter() - t0, us_events
 
 
+def library_gemm():
+    """The vendor bf16 GEMM (torch.matmul over hipBLASLt) at the fast prefill's
+    product shapes, one product each: tokens x rows x K, HIP events over 50
+    calls after 5 warm-up calls."""
+    import torch
+    out = []
+    for tokens, rows, k, name in [(512, 13824, 1152, "gate+up"), (512, 1152, 6912, "down"),
+                                  (512, 1536, 1152, "qkv"), (512, 1152, 1024, "o"),
+                                  (2048, 13824, 1152, "gate+up at 2,048 tokens")]:
+        a = torch.randn(tokens, k, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(rows, k, device="cuda", dtype=torch.bfloat16)
+        for _ in range(5):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(50):
+            c = a @ b.t()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 50
+        out.append({"product": name, "tokens": tokens, "rows": rows, "k": k, "us": us,
+                    "tflops": 2 * tokens * rows * k / (us * 1e-6) / 1e12})
+        del c
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -408,6 +439,10 @@ def main():
 
     if args.gguf_load:
         gguf_load(fz, args.seed)
+        return
+
+    if args.library_gemm:
+        print(json.dumps({"library_gemm": True, "products": library_gemm()}))
         return
 
     if args.probes:
