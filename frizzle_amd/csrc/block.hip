@@ -21,6 +21,35 @@ __device__ __forceinline__ float dot4v(float4 a, float4 b) {
   return dot4(a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w);
 }
 
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// a and b plus `count` rows of partial sums each (rows `stride` floats
+// apart from pa and pb), added in row order. Eight rows are requested
+// before any is added, so a split product's later sums cost a memory round
+// trip for every eight, not for every one.
+__device__ __forceinline__ void add_parts(float4& a, float4& b, const float* pa, const float* pb,
+                                          size_t stride, int count) {
+  for (int j0 = 0; j0 < count; j0 += 8) {
+    float4 sa[8], sb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j0 + j < count) {
+        sa[j] = ld4(pa + (size_t)(j0 + j) * stride);
+        if (pb) sb[j] = ld4(pb + (size_t)(j0 + j) * stride);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j0 + j < count) {
+        a = add4(a, sa[j]);
+        if (pb) b = add4(b, sb[j]);
+      }
+    }
+  }
+}
+
 // ---- RMSNorm (norm.wgsl:96-198) -----------------------------------------
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxVec4 = 4;  // rows up to 4,096 wide
@@ -62,13 +91,9 @@ __global__ __launch_bounds__(kNormThreads) void norm_kernel(
         // A split product's output: the prefix of its first ranges, then
         // the later range sums added in range order.
         if (a.parts) {
-          for (int j = 0; j < a.part_count; ++j) {
-            const float4 s = ld4(a.parts + j * a.parts_stride + base + 4 * q);
-            y[k].x = y[k].x + s.x;
-            y[k].y = y[k].y + s.y;
-            y[k].z = y[k].z + s.z;
-            y[k].w = y[k].w + s.w;
-          }
+          float4 unused;
+          add_parts(y[k], unused, a.parts + base + 4 * q, nullptr, a.parts_stride,
+                    a.part_count);
         }
       }
     }
@@ -176,12 +201,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const DevStep* __restrict__ s
     va = ld4(src + 4 * lane);
     vb = ld4(src + half + 4 * lane);
     // A K-split product's later partial sums, added in split order.
-    for (int z = 1; z < a.part_count; ++z) {
-      const float4 pa = ld4(src + z * a.part_stride + 4 * lane);
-      const float4 pb = ld4(src + z * a.part_stride + half + 4 * lane);
-      va = make_float4(va.x + pa.x, va.y + pa.y, va.z + pa.z, va.w + pa.w);
-      vb = make_float4(vb.x + pb.x, vb.y + pb.y, vb.z + pb.z, vb.w + pb.w);
-    }
+    add_parts(va, vb, src + a.part_stride + 4 * lane, src + a.part_stride + half + 4 * lane,
+              a.part_stride, a.part_count - 1);
   }
   partial[t] = rope_lane_squares(va, vb);
   __syncthreads();
