@@ -93,6 +93,11 @@ def parse():
                    help="only the floors: an empty kernel's launch (on the stream and "
                         "graph-replayed) and streaming reads of each decode product's "
                         "weight bytes (one JSON line)")
+    p.add_argument("--profile-roles", action="store_true",
+                   help="only: a decode step after the --prompt tokens and a 512-token "
+                        "prefill step, each profiled launch by launch "
+                        "(frz_model_profile_decode / _step), the launches named by the "
+                        "graph's roles and timed (one JSON line)")
     p.add_argument("--library-gemm", action="store_true",
                    help="only: the vendor bf16 GEMM (torch matmul, hipBLASLt) at the fast "
                         "prefill's product shapes, one product each, for scale (one JSON "
@@ -389,6 +394,47 @@ def timed_decode(model, dev, prompt, warmup, steps, greedy):
     return prefill_s, time.perf_counter() - t0, us_events
 
 
+def profile_roles(fz, model, dev, cfg, prompt_len, seed, reps=20):
+    """A fed decode step after a `prompt_len`-token prompt and a 512-token
+    prefill step, each profiled: every launch's time (HIP events either side
+    of it, launched one by one), grouped by its roles (the graph's names) and
+    by local and global layers, averaged over `reps` steps."""
+    rng = np.random.default_rng(seed + 7)
+    prompt = rng.integers(0, cfg.vocab, prompt_len).astype(np.uint32)
+    for p0 in range(0, prompt_len, 512):
+        model.step(p0, prompt[p0:p0 + 512], logits=p0 + 512 >= prompt_len)
+
+    def group(runs):
+        by = {}
+        for launches in runs:
+            for roles, layer, us in launches:
+                kind = ("output" if layer is None and roles.startswith("output") else
+                        "embed" if layer is None else
+                        "global" if (layer + 1) % cfg.pattern == 0 else "local")
+                key = f"{kind}: {roles}"
+                by.setdefault(key, []).append(us)
+        n = len(runs)
+        return {k: {"us_each": sum(v) / len(v), "launches_a_step": len(v) / n,
+                    "us_a_step": sum(v) / n} for k, v in by.items()}
+
+    decode_runs = []
+    for i in range(reps + 2):
+        launches, _ = model.profile_decode(prompt_len + i)
+        if i >= 2:
+            decode_runs.append(launches)
+    ids = rng.integers(0, cfg.vocab, 512).astype(np.uint32)
+    prefill_runs = [model.profile_step(0, ids, logits=True) for _ in range(3)][1:]
+    dec = group(decode_runs)
+    pre = group(prefill_runs)
+    return {"workload": f"Gemma-3-1B Q4_0 decode step after a {prompt_len}-token prompt, and a "
+                        "512-token prefill step (exact mode), launched one by one with HIP "
+                        "events either side of each launch",
+            "decode_us_a_step": sum(v["us_a_step"] for v in dec.values()),
+            "decode": dec,
+            "prefill_512_us_a_step": sum(v["us_a_step"] for v in pre.values()),
+            "prefill_512": pre}
+
+
 def library_gemm():
     """The vendor bf16 GEMM (torch.matmul over hipBLASLt) at the fast prefill's
     product shapes, one product each: tokens x rows x K, HIP events over 50
@@ -467,6 +513,12 @@ def main():
         model.set_graphs(False)
     greedy = fz.sampling()
 
+    if args.profile_roles:
+        out = profile_roles(fz, model, dev, cfg, args.prompt, args.seed)
+        model.close()
+        dev.close()
+        print(json.dumps({"profile_roles": True, **out}))
+        return
     if args.steered_only:
         out = steered_batch(fz, model, dev, cfg, args.seed)
         model.close()

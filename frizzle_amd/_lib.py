@@ -95,6 +95,20 @@ class CaptureSlots(ctypes.Structure):
                                                  "full_attention")]
 
 
+class LaunchTime(ctypes.Structure):
+    _fields_ = [("role", ctypes.c_char * 96), ("layer", c_uint32), ("graph_index", c_uint32),
+                ("microseconds", c_double)]
+
+
+class ProfileTimes(ctypes.Structure):
+    _fields_ = [("begin_ns", c_uint64), ("end_ns", c_uint64),
+                ("launch_index", POINTER(c_uint32)), ("launch_end_ns", POINTER(c_uint64)),
+                ("launches", POINTER(LaunchTime)), ("launch_count", c_uint32)]
+
+
+PROFILE_CALLBACK = ctypes.CFUNCTYPE(None, c_int, ctypes.c_char_p, c_void_p, c_uint32,
+                                    POINTER(ProfileTimes), c_void_p)
+
 _P = c_void_p
 _S = ctypes.c_char_p
 _SIGS = {
@@ -242,6 +256,13 @@ _SIGS = {
     "frz_program_cancel": (c_int, [_P]),
     "frz_program_destroy": (None, [_P]),
     "frz_program_mark_lost": (c_int, [_P]),
+    "frz_model_profile_step": (c_int, [_P, c_uint32, c_uint32, _P, c_int, _P, _P, c_uint32,
+                                       POINTER(c_uint32)]),
+    "frz_model_profile_decode": (c_int, [_P, c_uint32, _P, _P, c_uint32, POINTER(c_uint32),
+                                         POINTER(c_uint32)]),
+    "frz_program_run_profiled": (c_int, [_P, _P, _P, c_uint32, c_uint32, PROFILE_CALLBACK, _P]),
+    "frz_program_launch_count": (c_uint32, [_P]),
+    "frz_program_can_profile": (c_int, [_P]),
 }
 
 _lib = None

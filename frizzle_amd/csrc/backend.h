@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/frizzle_hip.h"
 #include "kernels.h"
@@ -33,5 +34,26 @@ int device_finish(frz_device* dev, hipError_t launched, const char* what);
 void fill_sampling(DevStep& s, const frz_sampling* sampling);
 // The most chunks a row reaches for a window over a cache of `slots`.
 int attention_max_chunks(int window, int slots);
+
+// A profiled step (frz_model_profile_step, frz_program_run_profiled): an
+// event recorded on the stream before each launch, with the roles the
+// launch runs (the graph's names, graph.h:99-106, "+" between the roles a
+// fused launch runs) and its layer, and one more after the last.
+struct StepProfile {
+  std::vector<hipEvent_t> events;
+  std::vector<const char*> roles;  // null for the closing event
+  std::vector<uint32_t> layers;
+  size_t used = 0;
+  StepProfile() = default;
+  StepProfile(const StepProfile&) = delete;
+  StepProfile& operator=(const StepProfile&) = delete;
+  ~StepProfile() {
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
+  }
+};
+// Each launch's time, from the event before it to the one after it, with its
+// names; `count` is the launches the step made (at most `cap` are written).
+// The step's events must have completed.
+int read_profile(const StepProfile& p, frz_launch_time* out, uint32_t cap, uint32_t* count);
 
 }  // namespace frz

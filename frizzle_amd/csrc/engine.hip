@@ -126,6 +126,9 @@ struct frz_model {
   };
   std::vector<WeightPlanes> weight_planes;
   bool planes_stale = true;
+  // While a profiled step is enqueued: its launches' events and names.
+  StepProfile* profile = nullptr;
+  StepProfile own_profile;  // frz_model_profile_step's
   float* parts = nullptr;
   size_t parts_stride = 0;  // floats a split's partial sums take
   // generation state: the tokens whose keys and values the caches hold, and
@@ -193,6 +196,25 @@ void release(frz_model* m, const void* p) {
   if (it == m->owned.end()) return;
   hipFree(*it);
   m->owned.erase(it);
+}
+
+// Before a launch of a profiled step: an event on the stream, and the
+// launch's roles and layer (role null: the event after the last launch).
+// Nothing while no profiled step is being enqueued.
+void mark(frz_model* m, const char* role, uint32_t layer = FRZ_NO_LAYER) {
+  StepProfile* p = m->profile;
+  if (!p) return;
+  if (p->used == p->events.size()) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    p->events.push_back(e);
+    p->roles.push_back(nullptr);
+    p->layers.push_back(FRZ_NO_LAYER);
+  }
+  if (hipEventRecord(p->events[p->used], m->dev->stream) != hipSuccess) return;
+  p->roles[p->used] = role;
+  p->layers[p->used] = layer;
+  ++p->used;
 }
 
 // The caches no longer hold what the prompt-reuse record says: weights
@@ -288,9 +310,11 @@ int upload_q4(frz_model* m, const QMatrix& w, int row0, int rows, const void* da
 // A fed decode step also advances the step parameters at its end.
 hipError_t enqueue_output(frz_model* m, int max_tokens, bool advance) {
   hipStream_t s = m->dev->stream;
+  mark(m, "output.head");
   hipError_t e = launch_gemv(s, m->step, m->embedding, m->normed, m->c.hidden, m->logits,
                              m->c.vocab, max_tokens, true);
   if (e == hipSuccess) {
+    mark(m, "output.select+output.draw");
     e = launch_select(s, m->step, m->logits, m->c.vocab, m->topk_scratch, m->candidates,
                       m->sampled, m->token_log, advance);
   }
@@ -311,9 +335,11 @@ hipError_t enqueue_readouts(frz_model* m) {
   auto slot = [m](int l, frz_capture_slot frz_capture_slots::*field) {
     return m->store + (m->slots[l].*field).first;
   };
+  mark(m, "output.readout");
   hipError_t e = launch_capture_copy(s, m->step, m->candidates, 0, 2 * kCandidates,
                                      slot(c.layers - 1, &frz_capture_slots::readout));
   for (int l = 0; l + 1 < c.layers && e == hipSuccess; ++l) {
+    mark(m, "readout", l);
     NormArgs n{m->output_norm, nullptr, nullptr, slot(l + 1, &frz_capture_slots::residual),
                m->ro_normed, c.epsilon, c.hidden, false};
     e = launch_norm(s, m->step, n, 1);
@@ -349,6 +375,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
   const int H = c.hidden, qw = c.query_heads * c.head_dim, kvw = c.kv_heads * c.head_dim;
   const int qkv_stride = qw + 2 * kvw;
   const float scale_log2e = scale_log2e_of(c);
+  mark(m, "embed");
   hipError_t e = launch_gather(s, m->step, m->embedding, v ? v->sampled : m->sampled, m->hidden,
                                std::sqrt((float)H), max_tokens);
   // The step that ends a prompt fills the capture store, when it is on.
@@ -407,9 +434,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     uint16_t* kcache = v ? v->kcache[l] : L.kcache;
     uint16_t* vcache = v ? v->vcache[l] : L.vcache;
     const size_t cache_stride = v ? (size_t)L.slots * kvw : 0;
+    mark(m, "attention.norm", l);
     e = launch_norm(s, m->step, attn_norm, max_tokens);
     int qkv_splits = 1;
     if (e == hipSuccess) {
+      mark(m, "attention.qkv", l);
       e = fast ? fast_product(m->weight_planes[l].qkv, L.qkv, H, m->parts, qkv_stride,
                               &qkv_splits)
                : launch_gemv(s, m->step, L.qkv, m->normed, H, m->qkv, qkv_stride, max_tokens,
@@ -425,9 +454,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                               L.max_chunks, c.epsilon, scale_log2e, qkv_stride, cache_stride};
         // The rows' position is known here: only its live chunks launch.
         d.grid_chunks = std::min(L.max_chunks, live_chunks(v->position, L.window));
+        mark(m, "attention.rope+attention.scores", l);
         e = launch_attention_decode(s, m->step, d, max_tokens);
       }
       if (e == hipSuccess) {
+        mark(m, "attention.combine", l);
         e = launch_attention_fold(
             s, m->step,
             FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window,
@@ -447,9 +478,11 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
           r.part_stride = m->parts_stride;
           r.part_count = qkv_splits;
         }
+        mark(m, "attention.rope", l);
         e = launch_rope(s, m->step, r, max_tokens);
       }
       if (cap && e == hipSuccess) {
+        mark(m, "attention.capture", l);
         e = launch_capture_copy(s, m->step, m->qkv, qkv_stride, qw,
                                 slot(l, &frz_capture_slots::query));
       }
@@ -462,6 +495,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                              m->partials, m->partials + m->partial_floats, L.slots, L.window,
                              c.head_dim,  c.query_heads, c.kv_heads,  L.max_chunks,
                              scale_log2e};
+        mark(m, "attention.scores", l);
         e = launch_attention_fast(
             s, m->step, fa, max_tokens,
             fast_attention_chunks((uint32_t)span.first, (uint32_t)span.last, L.window));
@@ -470,6 +504,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
                      L.max_chunks};
           f.out_hi = m->planes_hi;
           f.out_lo = m->planes_lo;
+          mark(m, "attention.combine", l);
           e = launch_attention_fold(s, m->step, f, max_tokens);
         }
       } else if (e == hipSuccess) {
@@ -487,8 +522,10 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
           a.store_stats = slot(l, &frz_capture_slots::stats);
           a.keys = (int)m->slots[l].keys;
         }
+        mark(m, "attention.scores+attention.combine", l);
         e = launch_attention(s, m->step, a, max_tokens);
         if (cap && e == hipSuccess) {
+          mark(m, "attention.weights", l);
           e = launch_capture_weights(s, m->step, a.store_scores, a.store_stats, a.keys,
                                      c.query_heads);
         }
@@ -498,12 +535,17 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     if (fast && e == hipSuccess) {
       // The fast attention's fold wrote the pair planes; the exact one's
       // output (a step that captures) is split here.
-      if (cap || span.first < 0)
+      if (cap || span.first < 0) {
+        mark(m, "attention.output", l);
         e = launch_split_rows(s, m->step, m->attn, qw, qw, m->planes_hi, m->planes_lo,
                               max_tokens);
-      if (e == hipSuccess)
+      }
+      if (e == hipSuccess) {
+        mark(m, "attention.output", l);
         e = fast_product(m->weight_planes[l].o, L.o, qw, m->parts, H, &o_splits);
+      }
     } else if (e == hipSuccess) {
+      mark(m, "attention.output", l);
       e = launch_gemv(s, m->step, L.o, m->attn, qw, m->output, H, max_tokens, false);
     }
     if (e == hipSuccess) {
@@ -519,6 +561,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
         ffn_norm.normed_lo = m->planes_lo;
       }
       if (cap) ffn_norm.store_added = slot(l, &frz_capture_slots::attention_added);
+      mark(m, "ffn.norm", l);
       e = launch_norm(s, m->step, ffn_norm, max_tokens);
     }
     if (fast && e == hipSuccess) {
@@ -538,12 +581,15 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
       // planes go after them.
       g.y_hi = m->planes_hi + (size_t)kPrefillBlock * H;
       g.y_lo = m->planes_lo + (size_t)kPrefillBlock * H;
+      mark(m, "ffn.gate_up+ffn.edit", l);
       e = launch_gemm_bf16(s, m->step, g, max_tokens, 1);
     } else if (e == hipSuccess) {
+      mark(m, "ffn.gate_up+ffn.edit", l);
       e = launch_gated(s, m->step, L.gate, L.up, m->normed, m->act, max_tokens,
                        v ? v->edits : m->edits, l, v ? v->edit_stride : 0);
     }
     if (cap && e == hipSuccess) {
+      mark(m, "ffn.capture", l);
       e = launch_capture_copy(s, m->step, m->act, c.ffn, c.ffn,
                               slot(l, &frz_capture_slots::neurons));
     }
@@ -561,6 +607,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
         g.ldy = H;
         g.part_stride = m->parts_stride;
         splits = bf16_splits_for(L.down.rows, L.down.cols, max_tokens, false);
+        mark(m, "ffn.down", l);
         e = launch_gemm_bf16(s, m->step, g, max_tokens, splits);
       }
       pending = L.gains[5];
@@ -573,6 +620,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     // next norm adds the later half's sums.
     const bool split = max_tokens <= kSplitRows && gemv_splits(L.down, max_tokens);
     if (e == hipSuccess) {
+      mark(m, "ffn.down", l);
       e = split ? launch_gemv_split(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens,
                                     m->split_parts, parts_stride)
                 : launch_gemv(s, m->step, L.down, m->act, c.ffn, m->output, H, max_tokens, false);
@@ -587,6 +635,7 @@ int enqueue_rows(frz_model* m, int max_tokens, bool logits, const frz_model::Var
     final_norm.parts_stride = parts_stride;
     final_norm.part_count = pending_count;
     if (cap) final_norm.store_added = slot(c.layers - 1, &frz_capture_slots::mlp_added);
+    mark(m, "output.norm");
     e = launch_norm(s, m->step, final_norm, max_tokens);
   }
   if (logits && e == hipSuccess) {
@@ -625,12 +674,14 @@ hipError_t enqueue_decode_layer(frz_model* m, int l, const float* pending) {
   in.sampled = m->sampled;
   in.scale = std::sqrt((float)H);
   in.epsilon = c.epsilon;
+  mark(m, l == 0 ? "embed+attention.norm+attention.qkv" : "attention.norm+attention.qkv", l);
   hipError_t e = launch_gemv_decode(s, m->step, L.qkv, in, l == 0 ? 2 : 1, m->qkv);
   if (e == hipSuccess) {
     DecodeAttentionArgs d{m->qkv,      L.turns,  L.gains[1],  L.gains[2], L.kcache,
                           L.vcache,    m->partials, m->partials + m->partial_floats, L.slots,
                           L.window,    c.head_dim, c.query_heads, c.kv_heads, L.max_chunks,
                           c.epsilon,   scale_log2e_of(c)};
+    mark(m, "attention.rope+attention.scores", l);
     e = launch_attention_decode(s, m->step, d);
   }
   // O: local layers fold their few chunks in the product's prologue.
@@ -640,14 +691,19 @@ hipError_t enqueue_decode_layer(frz_model* m, int l, const float* pending) {
       x.partials = m->partials;
       x.stats = m->partials + m->partial_floats;
       x.window = L.window;
+      mark(m, "attention.combine+attention.output", l);
       e = launch_gemv_decode(s, m->step, L.o, x, 3, m->output);
     } else {
+      mark(m, "attention.combine", l);
       e = launch_attention_fold(
           s, m->step,
           FoldArgs{m->partials, m->partials + m->partial_floats, m->attn, L.window, L.max_chunks},
           1);
       x.x = m->attn;
-      if (e == hipSuccess) e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+      if (e == hipSuccess) {
+        mark(m, "attention.output", l);
+        e = launch_gemv_decode(s, m->step, L.o, x, 0, m->output);
+      }
     }
   }
   if (e == hipSuccess) {
@@ -658,11 +714,13 @@ hipError_t enqueue_decode_layer(frz_model* m, int l, const float* pending) {
     g.gain = L.gains[4];
     g.hidden_out = m->hidden_b;
     g.epsilon = c.epsilon;
+    mark(m, "ffn.norm+ffn.gate_up+ffn.edit", l);
     e = launch_gated_decode(s, m->step, L.gate, L.up, g, 1, m->act, m->edits, l);
   }
   if (e == hipSuccess) {
     GemvInput x{};
     x.x = m->act;
+    mark(m, "ffn.down", l);
     e = launch_gemv_decode(s, m->step, L.down, x, 0, m->output);
   }
   return e;
@@ -691,8 +749,10 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
     h.gain = m->output_norm;
     h.normed_out = m->normed;
     h.epsilon = c.epsilon;
+    mark(m, "output.norm+output.head");
     e = launch_gemv_decode(s, m->step, m->embedding, h, 1, m->logits);
     if (e == hipSuccess) {
+      mark(m, "output.select+output.draw");
       e = launch_select(s, m->step, m->logits, c.vocab, m->topk_scratch, m->candidates,
                         m->sampled, m->token_log, advance);
     }
@@ -701,6 +761,7 @@ int enqueue_decode(frz_model* m, bool logits, bool advance) {
   if (e == hipSuccess) {
     NormArgs final_norm{m->output_norm, pending, m->output, m->hidden_b, m->normed,
                         c.epsilon, c.hidden, true};
+    mark(m, "output.norm");
     e = launch_norm(s, m->step, final_norm, 1);
   }
   if (logits && e == hipSuccess) e = enqueue_output(m, 1, advance);
@@ -1561,28 +1622,38 @@ namespace frz {
 // one when graphs are off), any other step runs the rows path; a step with
 // logits then copies the draw's 16-byte record to `readback` (pinned). The
 // caches are rewritten, so generation's prompt-reuse record is forgotten.
-int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback) {
+int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback,
+                 StepProfile* profile) {
   hipStream_t s = m->dev->stream;
   forget_prefix(m);
   const DevStep& st = *pinned_step;
   const bool decode = st.tokens == 1 && st.fed != 0 && st.logits != 0 && !st.variants;
-  if (decode && m->use_graphs) {
+  // A profiled step runs its launches one by one (no captured graph).
+  const bool graph = decode && m->use_graphs && !profile;
+  if (graph) {
     if (int rc = build_decode_graph(m)) return rc;
   }
   if (int rc = check_hip(hipMemcpyAsync(m->step, pinned_step, sizeof(DevStep),
                                         hipMemcpyHostToDevice, s),
                          "program step record"))
     return rc;
-  if (decode) {
-    if (int rc = launch_decode_step(m)) return rc;
+  if (profile) profile->used = 0;
+  m->profile = profile;
+  int rc = FRZ_OK;
+  if (graph) {
+    rc = launch_decode_step(m);
+  } else if (decode) {
+    rc = enqueue_step(m, 1, true, true);
   } else {
     // The record is host memory, written before this call: its positions
     // are known here.
     const int64_t last = (int64_t)st.position + (st.variants ? 0 : (int64_t)st.tokens - 1);
-    if (int rc = enqueue_step(m, (int)st.tokens, st.logits != 0, false,
-                              RowSpan{(int64_t)st.position, last}))
-      return rc;
+    rc = enqueue_step(m, (int)st.tokens, st.logits != 0, false,
+                      RowSpan{(int64_t)st.position, last});
   }
+  if (rc == FRZ_OK) mark(m, nullptr);
+  m->profile = nullptr;
+  if (rc != FRZ_OK) return rc;
   if (st.logits != 0 && readback) {
     return check_hip(hipMemcpyAsync(readback, m->sampled, 16, hipMemcpyDeviceToHost, s),
                      "program readback");
@@ -1592,9 +1663,77 @@ int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback) {
 
 hipStream_t model_stream(const frz_model* m) { return m->dev->stream; }
 
+int read_profile(const StepProfile& p, frz_launch_time* out, uint32_t cap, uint32_t* count) {
+  const uint32_t n = p.used > 0 ? (uint32_t)p.used - 1 : 0;
+  if (count) *count = n;
+  if (n > 0) {
+    if (int rc = check_hip(hipEventSynchronize(p.events[n]), "profiled step")) return rc;
+  }
+  for (uint32_t i = 0; i < n && i < cap && out; ++i) {
+    float ms = 0.0f;
+    if (int rc = check_hip(hipEventElapsedTime(&ms, p.events[i], p.events[i + 1]), "profile"))
+      return rc;
+    frz_launch_time& t = out[i];
+    std::memset(t.role, 0, sizeof t.role);
+    std::strncpy(t.role, p.roles[i] ? p.roles[i] : "", sizeof t.role - 1);
+    t.layer = p.layers[i];
+    t.graph_index = ~0u;
+    t.microseconds = (double)ms * 1000.0;
+  }
+  return FRZ_OK;
+}
+
 }  // namespace frz
 
 extern "C" {
+
+int frz_model_profile_step(frz_model* m, uint32_t position, uint32_t tokens,
+                           const uint32_t* ids, int logits, const frz_sampling* sampling,
+                           frz_launch_time* out, uint32_t cap, uint32_t* count) {
+  if (!m || !count) return fail(FRZ_ERR_ARGUMENT, "frz_model_profile_step: null argument");
+  forget_prefix(m);
+  m->own_profile.used = 0;
+  m->profile = &m->own_profile;
+  int rc = model_step(m, position, tokens, ids, logits, sampling);
+  if (rc == FRZ_OK) mark(m, nullptr);
+  m->profile = nullptr;
+  if (rc != FRZ_OK) return rc;
+  return read_profile(m->own_profile, out, cap, count);
+}
+
+int frz_model_profile_decode(frz_model* m, uint32_t position, const frz_sampling* sampling,
+                             frz_launch_time* out, uint32_t cap, uint32_t* count,
+                             uint32_t* token) {
+  if (!m || !count) return fail(FRZ_ERR_ARGUMENT, "frz_model_profile_decode: null argument");
+  if ((uint64_t)position + 1 > (uint64_t)m->c.context)
+    return fail(FRZ_ERR_ARGUMENT, "frz_model_profile_decode: past the context");
+  forget_prefix(m);
+  DevStep& s = *m->step_host;
+  std::memset(&s, 0, sizeof s);
+  s.position = position;
+  s.tokens = 1;
+  s.logits = 1;
+  s.fed = 1;
+  s.drawn = 0;
+  fill_sampling(s, sampling);
+  if (int rc = put_step(m)) return rc;
+  m->own_profile.used = 0;
+  m->profile = &m->own_profile;
+  int rc = enqueue_step(m, 1, true, true);
+  if (rc == FRZ_OK) mark(m, nullptr);
+  m->profile = nullptr;
+  if (rc != FRZ_OK) return rc;
+  if (int rc2 = read_profile(m->own_profile, out, cap, count)) return rc2;
+  uint32_t log[2] = {0, 0};
+  if (int rc2 = check_hip(hipMemcpyAsync(log, m->token_log, 8, hipMemcpyDeviceToHost,
+                                         m->dev->stream),
+                          "token log"))
+    return rc2;
+  if (int rc2 = check_hip(hipStreamSynchronize(m->dev->stream), "profile decode sync"))
+    return rc2;
+  if (token) *token = log[0];
+  return FRZ_OK;
+}
 
 int frz_generate(frz_model* m, const uint32_t* prompt, uint32_t prompt_len,
                  const uint32_t* edit_table, uint32_t edit_words, const frz_sampling* sampling,

@@ -25,7 +25,8 @@
 #include "kernels.h"
 
 namespace frz {
-int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback);
+int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback,
+                 StepProfile* profile = nullptr);
 hipStream_t model_stream(const frz_model* m);
 }  // namespace frz
 
@@ -390,8 +391,12 @@ struct frz_program {
   uint8_t* staging[kOutstanding] = {};  // pinned input bytes
   size_t staging_bytes[kOutstanding] = {};
   hipEvent_t done_event[kOutstanding] = {};
+  // The graph's launches' names (role, layer), for a profiled step's report.
+  std::vector<std::pair<std::string, uint32_t>> names;
+  StepProfile profiles[kOutstanding];  // a profiled step's events, by slot
   struct Slot {
     frz_step_callback done = nullptr;
+    frz_profile_callback profiled = nullptr;  // a profiled step's callback
     void* userdata = nullptr;
     int status = FRZ_OK;      // a failure found before it ran
     std::string message;
@@ -405,6 +410,25 @@ struct frz_program {
 namespace {
 
 uint32_t outstanding(const frz_program* p) { return (uint32_t)(p->next_run - p->next_report); }
+
+// The index in the graph of the last of its launches that a launch of this
+// backend runs: one of the launch's roles ("+" between them) in its layer.
+uint32_t graph_index_of(const std::vector<std::pair<std::string, uint32_t>>& names,
+                        const char* roles, uint32_t layer) {
+  uint32_t found = ~0u;
+  std::string all(roles ? roles : "");
+  for (size_t at = 0; at <= all.size();) {
+    size_t end = all.find('+', at);
+    if (end == std::string::npos) end = all.size();
+    const std::string one = all.substr(at, end - at);
+    for (uint32_t i = 0; i < names.size(); ++i) {
+      if (names[i].second == layer && names[i].first == one && (found == ~0u || i > found))
+        found = i;
+    }
+    at = end + 1;
+  }
+  return found;
+}
 
 // Reports the oldest outstanding step (its work, if any, waited for when
 // `wait`); false when it has not settled.
@@ -433,10 +457,40 @@ bool report_oldest(frz_program* p, bool wait, bool cancelled) {
   const bool with = status == FRZ_OK && s.logits;
   if (with) std::memcpy(record, p->readback[k], 16);
   const frz_step_callback done = s.done;
+  const frz_profile_callback profiled = s.profiled;
   void* ud = s.userdata;
+  // A profiled step's times: each launch's from its events, its end as the
+  // sum of those before it, and the graph's last launch it runs.
+  std::vector<frz_launch_time> launches;
+  std::vector<uint32_t> index;
+  std::vector<uint64_t> end_ns;
+  frz_profile_times times{};
+  if (profiled && status == FRZ_OK) {
+    uint32_t n = 0;
+    if (read_profile(p->profiles[k], nullptr, 0, &n) == FRZ_OK) {
+      launches.resize(n);
+      if (read_profile(p->profiles[k], launches.data(), n, &n) != FRZ_OK) launches.clear();
+    }
+    double at = 0.0;
+    for (frz_launch_time& t : launches) {
+      t.graph_index = graph_index_of(p->names, t.role, t.layer);
+      at += t.microseconds;
+      index.push_back(t.graph_index);
+      end_ns.push_back((uint64_t)(at * 1000.0 + 0.5));
+    }
+    times.end_ns = end_ns.empty() ? 0 : end_ns.back();
+    times.launch_index = index.data();
+    times.launch_end_ns = end_ns.data();
+    times.launches = launches.data();
+    times.launch_count = (uint32_t)launches.size();
+  }
   s = frz_program::Slot{};
   ++p->next_report;  // reported before the callback, which may run the next step
-  if (done) done(status, message.c_str(), with ? record : nullptr, with ? 16u : 0u, ud);
+  if (profiled) {
+    profiled(status, message.c_str(), with ? record : nullptr, with ? 16u : 0u, &times, ud);
+  } else if (done) {
+    done(status, message.c_str(), with ? record : nullptr, with ? 16u : 0u, ud);
+  }
   return true;
 }
 
@@ -470,6 +524,8 @@ int frz_program_build(frz_model* upload, const frz_plan* plan, const frz_launch*
   frz_model_config pc;
   (void)frz_plan_config(plan, &pc);
   auto* p = new frz_program();
+  for (uint32_t i = 0; i < count; ++i)
+    p->names.emplace_back(launches[i].role ? launches[i].role : "", launches[i].layer);
   p->model = upload;
   p->stream = model_stream(upload);
   p->context = (uint32_t)c.context;
@@ -528,22 +584,47 @@ static_assert(std::is_same<decltype(DevStep::temperature), decltype(frz_step_rec
                   std::is_same<decltype(DevStep::top_k), decltype(frz_step_record::top_k)>::value,
               "the step head's fields have the record's types");
 
-int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_input* inputs,
-                    uint32_t input_count, frz_step_callback done, void* userdata) {
-  if (!p || !step) return fail(FRZ_ERR_ARGUMENT, "frz_program_run: null argument");
+}  // extern "C"
+
+namespace {
+
+// frz_program_run and frz_program_run_profiled (`profiled` not null, with
+// `launches` the count asked for).
+int run_step(frz_program* p, const frz_step_record* step, const frz_run_input* inputs,
+             uint32_t input_count, frz_step_callback done, frz_profile_callback profiled,
+             uint32_t launches, void* userdata) {
+  const char* name = profiled ? "frz_program_run_profiled: " : "frz_program_run: ";
+  if (!p || !step) return fail(FRZ_ERR_ARGUMENT, std::string(name) + "null argument");
   // Refused at once, unrun and unnumbered.
   auto refuse = [&](int status, const std::string& why) {
-    if (done) done(status, why.c_str(), nullptr, 0, userdata);
-    return fail(status, "frz_program_run: " + why);
+    if (profiled) {
+      const frz_profile_times none{};
+      profiled(status, why.c_str(), nullptr, 0, &none, userdata);
+    } else if (done) {
+      done(status, why.c_str(), nullptr, 0, userdata);
+    }
+    return fail(status, name + why);
   };
   if (p->lost) return refuse(FRZ_ERR_DEVICE_LOST, "the device is lost");
   if (outstanding(p) >= (uint32_t)kOutstanding) return refuse(FRZ_ERR_STEP, "two steps are outstanding");
+  if (profiled) {
+    if (launches != (uint32_t)p->names.size())
+      return refuse(FRZ_ERR_STEP, "a prefix of " + std::to_string(launches) + " of the graph's " +
+                                      std::to_string(p->names.size()) +
+                                      " launches (this backend's launches each run several of "
+                                      "the graph's, so it runs whole steps)");
+    for (uint64_t n = p->next_report; n < p->next_run; ++n) {
+      if (!p->slot[n % kOutstanding].profiled)
+        return refuse(FRZ_ERR_STEP, "an unprofiled step is outstanding");
+    }
+  }
   if (step->tokens == 0 || step->tokens > (uint32_t)kPrefillBlock)
     return refuse(FRZ_ERR_STEP, "a step of " + std::to_string(step->tokens) + " tokens");
   const int k = (int)(p->next_run % kOutstanding);
   frz_program::Slot& s = p->slot[k];
   s = frz_program::Slot{};
   s.done = done;
+  s.profiled = profiled;
   s.userdata = userdata;
   s.logits = step->logits != 0;
   ++p->next_run;
@@ -596,7 +677,9 @@ int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_i
                        hipMemcpyHostToDevice, p->stream);
     at += in.to.size;
   }
-  int rc = e == hipSuccess ? program_step(p->model, p->step[k], p->readback[k]) : FRZ_ERR_DEVICE;
+  int rc = e == hipSuccess ? program_step(p->model, p->step[k], p->readback[k],
+                                          profiled ? &p->profiles[k] : nullptr)
+                           : FRZ_ERR_DEVICE;
   if (rc == FRZ_OK) e = hipEventRecord(p->done_event[k], p->stream);
   if (rc != FRZ_OK || e != hipSuccess) {
     const hipError_t last = e != hipSuccess ? e : hipGetLastError();
@@ -610,6 +693,28 @@ int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_i
   s.ran = true;
   return FRZ_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int frz_program_run(frz_program* p, const frz_step_record* step, const frz_run_input* inputs,
+                    uint32_t input_count, frz_step_callback done, void* userdata) {
+  return run_step(p, step, inputs, input_count, done, nullptr, 0, userdata);
+}
+
+int frz_program_run_profiled(frz_program* p, const frz_step_record* step,
+                             const frz_run_input* inputs, uint32_t input_count,
+                             uint32_t launches, frz_profile_callback done, void* userdata) {
+  if (!done) return fail(FRZ_ERR_ARGUMENT, "frz_program_run_profiled: null callback");
+  return run_step(p, step, inputs, input_count, nullptr, done, launches, userdata);
+}
+
+uint32_t frz_program_launch_count(const frz_program* p) {
+  return p ? (uint32_t)p->names.size() : 0;
+}
+
+int frz_program_can_profile(const frz_program* p) { return p ? 1 : 0; }
 
 int frz_poll(frz_program* p, int wait) {
   if (!p) return 0;

@@ -5,7 +5,7 @@ kernels::Order, order.h:68-104)."""
 import ctypes
 from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_uint32, c_void_p
 
-from . import graph
+from . import _lib, graph
 from ._lib import check as _check
 from ._lib import load
 
@@ -84,6 +84,8 @@ class Program:
         self._h = h
         self.reports = []  # (status, message, record) in the order they came
         self._cb = CALLBACK(self._on_done)
+        self._pcb = _lib.PROFILE_CALLBACK(self._on_profiled)
+        self.profiles = []  # a profiled step's (status, begin_ns, end_ns, launches)
         self._inputs = []
 
     def _on_done(self, status, message, readback, nbytes, userdata):
@@ -94,17 +96,51 @@ class Program:
         if self.on_report:
             self.on_report(status, rec, userdata)
 
+    def _on_profiled(self, status, message, readback, nbytes, times, userdata):
+        t = times.contents
+        launches = []
+        for i in range(t.launch_count):
+            lt = t.launches[i]
+            launches.append({"roles": lt.role.decode(),
+                             "layer": None if lt.layer == 0xFFFFFFFF else int(lt.layer),
+                             "us": float(lt.microseconds),
+                             "graph_index": int(t.launch_index[i]),
+                             "end_ns": int(t.launch_end_ns[i])})
+        self.profiles.append((status, int(t.begin_ns), int(t.end_ns), launches))
+        self._on_done(status, message, readback, nbytes, userdata)
+
     on_report = None
 
-    def run(self, record, inputs=(), tag=0):
+    @staticmethod
+    def _inputs_of(inputs):
         ins = (RunInput * max(1, len(inputs)))()
         keep = []
         for i, (binding, data) in enumerate(inputs):
             buf = ctypes.create_string_buffer(bytes(data), len(data))
             keep.append(buf)
             ins[i] = RunInput(graph.CBinding(*binding), ctypes.cast(buf, c_void_p))
+        return ins, keep
+
+    def run(self, record, inputs=(), tag=0):
+        ins, keep = self._inputs_of(inputs)
         return self._lib.frz_program_run(self._h, byref(record), ins, len(inputs), self._cb,
                                          c_void_p(tag))
+
+    def run_profiled(self, record, inputs=(), tag=0, launches=None):
+        """Program::run_profiled: the step timed launch by launch; its report
+        also lands in `profiles`. `launches` defaults to the whole graph."""
+        ins, keep = self._inputs_of(inputs)
+        n = self.launch_count if launches is None else launches
+        return self._lib.frz_program_run_profiled(self._h, byref(record), ins, len(inputs), n,
+                                                  self._pcb, c_void_p(tag))
+
+    @property
+    def launch_count(self):
+        return self._lib.frz_program_launch_count(self._h)
+
+    @property
+    def can_profile(self):
+        return bool(self._lib.frz_program_can_profile(self._h))
 
     def poll(self, wait=False):
         return self._lib.frz_poll(self._h, int(wait))

@@ -209,6 +209,11 @@ class DeviceArray:
             pass
 
 
+def _launches(out, count):
+    return [(out[i].role.decode(), None if out[i].layer == 0xFFFFFFFF else int(out[i].layer),
+             float(out[i].microseconds)) for i in range(count)]
+
+
 class Device:
     """One GPU (frz_open). Raises when there is none."""
 
@@ -330,6 +335,33 @@ class Model:
         check(self.lib.frz_model_decode(self.handle, position, steps, byref(s),
                                         toks.ctypes.data, failed.ctypes.data))
         return toks, failed
+
+    # A step's launches fit in this many entries (a prompt's last step with
+    # the capture store's readouts makes about 420 for Gemma-3-1B).
+    PROFILE_CAP = 2048
+
+    def profile_step(self, position, ids, logits=False, samp=None):
+        """frz_model_step, profiled: [(roles, layer, microseconds)] a launch,
+        roles the graph's names ('+' between a fused launch's), layer None for
+        the embedding and the output."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        s = samp or sampling()
+        n = c_uint32()
+        out = (_lib.LaunchTime * self.PROFILE_CAP)()
+        check(self.lib.frz_model_profile_step(self.handle, position, ids.size, ids.ctypes.data,
+                                              int(logits), byref(s), out, self.PROFILE_CAP,
+                                              byref(n)))
+        return _launches(out, min(n.value, self.PROFILE_CAP))
+
+    def profile_decode(self, position, samp=None):
+        """One fed decode step at `position` (the last step's draw), profiled:
+        (launches as profile_step gives them, the step's draw)."""
+        s = samp or sampling()
+        n, tok = c_uint32(), c_uint32()
+        out = (_lib.LaunchTime * self.PROFILE_CAP)()
+        check(self.lib.frz_model_profile_decode(self.handle, position, byref(s), out,
+                                                self.PROFILE_CAP, byref(n), byref(tok)))
+        return _launches(out, min(n.value, self.PROFILE_CAP)), int(tok.value)
 
     def time_decode(self, position, steps, samp=None):
         s = samp or sampling()

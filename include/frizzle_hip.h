@@ -899,6 +899,68 @@ void frz_program_destroy(frz_program* program);
  * path; a real loss (a HIP error on the stream) takes the same path. */
 int frz_program_mark_lost(frz_program* program);
 
+/* ---- profiled steps ------------------------------------------------------
+ * A step run as usual, launch by launch (no captured graph), with a HIP
+ * event recorded on the stream before each launch and after the last. Each
+ * launch is named by what it does in the model, as the reference's graph
+ * names its launches (kernels::Launch::role and ::layer, interface.h:356-362;
+ * the names of graph/graph.h:99-106): "embed", "attention.norm",
+ * "attention.qkv", "attention.rope", "attention.scores",
+ * "attention.combine", "attention.output", "ffn.norm", "ffn.gate_up",
+ * "ffn.edit", "ffn.down", "output.norm", "output.head", "output.select",
+ * "output.draw", and the capture store's "attention.capture",
+ * "attention.weights", "ffn.capture", "readout", "output.readout". A launch of this backend
+ * that runs several of the graph's roles (a product with its norm in its
+ * prologue) names them all, joined by "+". A step's results are those of an
+ * unprofiled one. */
+typedef struct frz_launch_time {
+  char role[96];
+  uint32_t layer;        /* FRZ_NO_LAYER for the embedding and the output */
+  uint32_t graph_index;  /* a program's: the graph's last launch it runs; else ~0 */
+  double microseconds;   /* from the event before it to the one after it */
+} frz_launch_time;
+/* frz_model_step, profiled (no reference counterpart at the model level: a
+ * diagnostic entry, as Program::run_profiled is the program's). `count` gets
+ * the step's launches; at most `cap` are written to `out`. */
+int frz_model_profile_step(frz_model* model, uint32_t position, uint32_t tokens,
+                           const uint32_t* ids, int logits, const frz_sampling* sampling,
+                           frz_launch_time* out, uint32_t cap, uint32_t* count);
+/* One fed decode step (the last step's draw at `position`, as one step of
+ * frz_model_decode), profiled; *token gets its draw. */
+int frz_model_profile_decode(frz_model* model, uint32_t position, const frz_sampling* sampling,
+                             frz_launch_time* out, uint32_t cap, uint32_t* count,
+                             uint32_t* token);
+/* Program::run_profiled's Timestamps (program.h:344-357): nanoseconds, the
+ * step's first event at 0 (begin_ns), its last at end_ns, and the end of each
+ * of this backend's launches by the index, in the graph, of the last of the
+ * graph's launches it runs. Valid only during the callback. */
+typedef struct frz_profile_times {
+  uint64_t begin_ns;
+  uint64_t end_ns;
+  const uint32_t* launch_index;
+  const uint64_t* launch_end_ns;
+  const frz_launch_time* launches;  /* the same launches, named and timed */
+  uint32_t launch_count;
+} frz_profile_times;
+typedef void (*frz_profile_callback)(int status, const char* message, const void* readback,
+                                     uint32_t readback_bytes, const frz_profile_times* times,
+                                     void* userdata);
+/* Program::run_profiled (program.h:359-365): runs one step as
+ * frz_program_run does, timed; `done` is called by frz_poll in run order,
+ * with zero times for a step refused or failed. `launches` must be the
+ * graph's whole count (frz_program_launch_count): this backend's launches
+ * each run several of the graph's, so it runs no prefix of a step. Refused
+ * at once, FRZ_ERR_STEP: a prefix, a step beside an unprofiled one
+ * outstanding, and frz_program_run's refusals. */
+int frz_program_run_profiled(frz_program* program, const frz_step_record* step,
+                             const frz_run_input* inputs, uint32_t input_count,
+                             uint32_t launches, frz_profile_callback done, void* userdata);
+/* Program::launch_count (program.h:367-368): the graph's launches. */
+uint32_t frz_program_launch_count(const frz_program* program);
+/* Program::can_profile (program.h:370-372): 1 (HIP events time every
+ * launch on this backend). */
+int frz_program_can_profile(const frz_program* program);
+
 #ifdef __cplusplus
 }
 #endif
