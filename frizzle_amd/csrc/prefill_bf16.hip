@@ -24,12 +24,13 @@
 // kernel that produced them (plane_index). Gemma-3-1B's weight planes take
 // 107 MB a layer, 2.8 GB in all.
 //
-// Tiles: a workgroup of four waves (one a SIMD) owns 128 output rows x 256
-// tokens and steps K one 32-weight block at a time. Wave w computes all
-// 128 rows for tokens 64 w .. 64 w + 63 (eight 32 x 32 accumulators): the
-// weights, which all four waves read, pass through LDS (double-buffered);
-// each wave's token fragments, which only it reads, go straight into its
-// registers. Loads run ahead and are copied as they are (no VALU). The
+// Tiles: a workgroup of eight waves (two a SIMD, so that one wave's
+// products run while the other waits) owns 128 output rows x 256 tokens and
+// steps K one 32-weight block at a time. Wave w computes all 128 rows for
+// tokens 32 w .. 32 w + 31 (four 32 x 32 accumulators): the weights, which
+// all eight waves read, pass through LDS (double-buffered), moved there by
+// waves 0-3; each wave's token fragments, which only it reads, go straight
+// into its registers. Loads run ahead and are copied as they are (no VALU). The
 // instruction takes the tokens as its A operand and the weights as B, so
 // that each output register's lanes are 32 consecutive rows of one token.
 // For the gated product, row blocks 0 and 1 are 64 neurons' gate rows and
@@ -53,7 +54,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileRows = 128;
 constexpr int kTileTokens = 256;
-constexpr int kThreads = 256;
+constexpr int kGemmThreads = 512;  // the products' workgroups: eight waves
 constexpr int kStepBytes = 8 * 1024;       // a tile's weights for one step: 4 blocks x 2 planes
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
@@ -230,17 +231,17 @@ __device__ __forceinline__ float gelu_fast(float g) {
 }
 
 // A wave's share of one K block (two steps of 16 k): its weight block's
-// fragments [step][hi, lo], staged in LDS for the workgroup, and its two
-// token blocks' [block][step][hi, lo], which only it reads.
+// fragments [step][hi, lo] (waves 0-3), staged in LDS for the workgroup, and
+// its token block's [step][hi, lo], which only it reads.
 struct WeightLoad2 {
   uint4 w[2][2];
 };
 struct TokenLoad {
-  uint4 x[2][2][2];
+  uint4 x[2][2];
 };
 
 template <bool GATED>
-__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* __restrict__ step,
+__global__ __launch_bounds__(kGemmThreads, 2) void gemm_bf16_kernel(const DevStep* __restrict__ step,
                                                                 Bf16Gemm g) {
   // The weights of one K block: [step][row block][hi, lo][lane].
   __shared__ uint4 stage[2][2][4][2][64];
@@ -263,41 +264,41 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* _
   // acc[row block][token block of the wave], transposed: the instruction
   // takes the tokens as its A operand and the weights as B, so a lane holds
   // one output row (lane % 32) for 16 tokens.
-  f32x16 acc[4][2];
+  f32x16 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
 
   // A split past the last block (splits that do not divide the blocks)
   // writes zero partial sums.
   if (kb0 >= kb1) {
     if (!GATED) {
       float* y = g.y + (size_t)z * g.part_stride;
-      for (int i = tid; i < kTileRows * kTileTokens; i += kThreads) {
+      for (int i = tid; i < kTileRows * kTileTokens; i += kGemmThreads) {
         const int o = rt * kTileRows + (i % kTileRows), t = n0 + i / kTileRows;
         if (o < g.rows && t < tokens) y[(size_t)t * g.ldy + o] = 0.0f;
       }
     }
     return;
   }
-  // Wave w moves weight block w of the row tile into LDS, and reads its
-  // token blocks 2 w and 2 w + 1 of the tile (the last block with rows, for
-  // blocks past them) straight into registers; every fragment is a 1 KB
-  // run of its planes, 16 bytes a lane.
-  const uint4* wsrc = g.w + fragment_at(rt, steps, 0, wave, 0) + lane;
+  // Wave w < 4 moves weight block w of the row tile into LDS; wave w reads
+  // its token block w of the tile (the last block with rows, for blocks
+  // past them) straight into registers. Every fragment is a 1 KB run of its
+  // planes, 16 bytes a lane.
+  const bool mover = wave < 4;  // uniform over the wave
+  const uint4* wsrc = g.w + fragment_at(rt, steps, 0, wave & 3, 0) + lane;
   const int last_tb = (tokens - 1) >> 5;
-  const size_t x_at0 = plane_index(32 * min(n0 / 32 + 2 * wave, last_tb), 0, g.ldx) + 8 * lane;
-  const size_t x_at1 = plane_index(32 * min(n0 / 32 + 2 * wave + 1, last_tb), 0, g.ldx) + 8 * lane;
+  const size_t x_at = plane_index(32 * min(n0 / 32 + wave, last_tb), 0, g.ldx) + 8 * lane;
   auto load_w = [&](int kb) {
     WeightLoad2 r;
+    if (mover) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const size_t s = 2 * (size_t)kb + u;
-      r.w[u][0] = load_global4(wsrc + s * (kStepBytes / 16));
-      r.w[u][1] = load_global4(wsrc + s * (kStepBytes / 16) + 64);
+      for (int u = 0; u < 2; ++u) {
+        const size_t s = 2 * (size_t)kb + u;
+        r.w[u][0] = load_global4(wsrc + s * (kStepBytes / 16));
+        r.w[u][1] = load_global4(wsrc + s * (kStepBytes / 16) + 64);
+      }
     }
     return r;
   };
@@ -306,10 +307,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* _
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const size_t s = 2 * (size_t)kb + u;
-      r.x[0][u][0] = load_global4(g.x_hi + x_at0 + 512 * s);
-      r.x[0][u][1] = load_global4(g.x_lo + x_at0 + 512 * s);
-      r.x[1][u][0] = load_global4(g.x_hi + x_at1 + 512 * s);
-      r.x[1][u][1] = load_global4(g.x_lo + x_at1 + 512 * s);
+      r.x[u][0] = load_global4(g.x_hi + x_at + 512 * s);
+      r.x[u][1] = load_global4(g.x_lo + x_at + 512 * s);
     }
     return r;
   };
@@ -317,39 +316,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* _
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) st[u][wave][p][lane] = r.w[u][p];
+      for (int p = 0; p < 2; ++p) {
+        if (mover) st[u][wave][p][lane] = r.w[u][p];
+      }
   };
   auto compute = [&](const uint4 (&st)[2][4][2][64], const TokenLoad& r) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      bf16x8 wh[4], wl[4], xh[2], xl[2];
+      bf16x8 wh[4], wl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         wh[i] = as_bf16x8(st[u][i][0][lane]);
         wl[i] = as_bf16x8(st[u][i][1][lane]);
       }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        xh[j] = as_bf16x8(r.x[j][u][0]);
-        xl[j] = as_bf16x8(r.x[j][u][1]);
-      }
-      // The three products of each pair, eight independent accumulators
+      const bf16x8 xh = as_bf16x8(r.x[u][0]), xl = as_bf16x8(r.x[u][1]);
+      // The three products of each pair, four independent accumulators
       // between two that update the same one.
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wh[i], acc[i], 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[j], wh[i], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, wh[i], acc[i], 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl[j], wh[i], acc[i][j], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh[j], wl[i], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wl[i], acc[i], 0, 0, 0);
     }
   };
   // Weights run three blocks ahead in three register sets, tokens two
@@ -404,19 +392,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* _
     for (int i = 0; i < 2; ++i) {
       const int n = rt * (kTileRows / 2) + i * 32 + row_in;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int t = n0 + (2 * wave + j) * 32 + (e >> 2) * 8 + tok_in + (e & 3);
-          float v = gelu_fast(acc[i][j][e]) * acc[i + 2][j][e];
-          if (count) v = pin_one(g.edits, first, count, n, step->position + (uint32_t)t, v);
-          if (t >= tokens || n >= g.rows) continue;
-          if (g.y) g.y[(size_t)t * g.ldy + n] = v;
-          const __bf16 h = (__bf16)v, l = (__bf16)(v - (float)h);
-          const size_t at = plane_index(t, n, g.ldy);
-          g.y_hi[at] = __builtin_bit_cast(uint16_t, h);
-          g.y_lo[at] = __builtin_bit_cast(uint16_t, l);
-        }
+      for (int e = 0; e < 16; ++e) {
+        const int t = n0 + wave * 32 + (e >> 2) * 8 + tok_in + (e & 3);
+        float v = gelu_fast(acc[i][e]) * acc[i + 2][e];
+        if (count) v = pin_one(g.edits, first, count, n, step->position + (uint32_t)t, v);
+        if (t >= tokens || n >= g.rows) continue;
+        if (g.y) g.y[(size_t)t * g.ldy + n] = v;
+        const __bf16 h = (__bf16)v, l = (__bf16)(v - (float)h);
+        const size_t at = plane_index(t, n, g.ldy);
+        g.y_hi[at] = __builtin_bit_cast(uint16_t, h);
+        g.y_lo[at] = __builtin_bit_cast(uint16_t, l);
+      }
     }
     return;
   }
@@ -426,12 +412,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(const DevStep* _
     const int o = rt * kTileRows + i * 32 + row_in;
     if (o >= g.rows) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = n0 + (2 * wave + j) * 32 + (e >> 2) * 8 + tok_in + (e & 3);
-        if (t < tokens) y[(size_t)t * g.ldy + o] = acc[i][j][e];
-      }
+    for (int e = 0; e < 16; ++e) {
+      const int t = n0 + wave * 32 + (e >> 2) * 8 + tok_in + (e & 3);
+      if (t < tokens) y[(size_t)t * g.ldy + o] = acc[i][e];
+    }
   }
 }
 
@@ -535,9 +519,9 @@ hipError_t launch_gemm_bf16(hipStream_t s, const DevStep* step, Bf16Gemm g, int 
   g.token_tiles = (max_tokens + kTileTokens - 1) / kTileTokens;
   const int tiles = row_tiles_of(g.rows, g.gated) * splits * g.token_tiles;
   if (g.gated) {
-    hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(tiles), dim3(kThreads), 0, s, step, g);
+    hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(tiles), dim3(kGemmThreads), 0, s, step, g);
   } else {
-    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(tiles), dim3(kThreads), 0, s, step, g);
+    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(tiles), dim3(kGemmThreads), 0, s, step, g);
   }
   return hipGetLastError();
 }
