@@ -44,6 +44,11 @@ struct StepProfile {
   std::vector<const char*> roles;  // null for the closing event
   std::vector<uint32_t> layers;
   size_t used = 0;
+  bool failed = false;  // an event could not be made or recorded: the times are not reported
+  void start() {
+    used = 0;
+    failed = false;
+  }
   StepProfile() = default;
   StepProfile(const StepProfile&) = delete;
   StepProfile& operator=(const StepProfile&) = delete;

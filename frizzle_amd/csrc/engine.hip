@@ -204,14 +204,21 @@ void release(frz_model* m, const void* p) {
 void mark(frz_model* m, const char* role, uint32_t layer = FRZ_NO_LAYER) {
   StepProfile* p = m->profile;
   if (!p) return;
+  if (p->failed) return;
   if (p->used == p->events.size()) {
     hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return;
+    if (hipEventCreate(&e) != hipSuccess) {
+      p->failed = true;
+      return;
+    }
     p->events.push_back(e);
     p->roles.push_back(nullptr);
     p->layers.push_back(FRZ_NO_LAYER);
   }
-  if (hipEventRecord(p->events[p->used], m->dev->stream) != hipSuccess) return;
+  if (hipEventRecord(p->events[p->used], m->dev->stream) != hipSuccess) {
+    p->failed = true;
+    return;
+  }
   p->roles[p->used] = role;
   p->layers[p->used] = layer;
   ++p->used;
@@ -1637,7 +1644,7 @@ int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback,
                                         hipMemcpyHostToDevice, s),
                          "program step record"))
     return rc;
-  if (profile) profile->used = 0;
+  if (profile) profile->start();
   m->profile = profile;
   int rc = FRZ_OK;
   if (graph) {
@@ -1664,6 +1671,7 @@ int program_step(frz_model* m, const DevStep* pinned_step, uint32_t* readback,
 hipStream_t model_stream(const frz_model* m) { return m->dev->stream; }
 
 int read_profile(const StepProfile& p, frz_launch_time* out, uint32_t cap, uint32_t* count) {
+  if (p.failed) return fail(FRZ_ERR_DEVICE, "profiled step: a launch's event could not be recorded");
   const uint32_t n = p.used > 0 ? (uint32_t)p.used - 1 : 0;
   if (count) *count = n;
   if (n > 0) {
@@ -1692,7 +1700,7 @@ int frz_model_profile_step(frz_model* m, uint32_t position, uint32_t tokens,
                            frz_launch_time* out, uint32_t cap, uint32_t* count) {
   if (!m || !count) return fail(FRZ_ERR_ARGUMENT, "frz_model_profile_step: null argument");
   forget_prefix(m);
-  m->own_profile.used = 0;
+  m->own_profile.start();
   m->profile = &m->own_profile;
   int rc = model_step(m, position, tokens, ids, logits, sampling);
   if (rc == FRZ_OK) mark(m, nullptr);
@@ -1717,7 +1725,7 @@ int frz_model_profile_decode(frz_model* m, uint32_t position, const frz_sampling
   s.drawn = 0;
   fill_sampling(s, sampling);
   if (int rc = put_step(m)) return rc;
-  m->own_profile.used = 0;
+  m->own_profile.start();
   m->profile = &m->own_profile;
   int rc = enqueue_step(m, 1, true, true);
   if (rc == FRZ_OK) mark(m, nullptr);

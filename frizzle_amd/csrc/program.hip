@@ -466,10 +466,18 @@ bool report_oldest(frz_program* p, bool wait, bool cancelled) {
   std::vector<uint64_t> end_ns;
   frz_profile_times times{};
   if (profiled && status == FRZ_OK) {
+    // A profile that cannot be read fails the report (the step's own work
+    // is done; its times are not known).
     uint32_t n = 0;
-    if (read_profile(p->profiles[k], nullptr, 0, &n) == FRZ_OK) {
+    int rc = read_profile(p->profiles[k], nullptr, 0, &n);
+    if (rc == FRZ_OK) {
       launches.resize(n);
-      if (read_profile(p->profiles[k], launches.data(), n, &n) != FRZ_OK) launches.clear();
+      rc = read_profile(p->profiles[k], launches.data(), n, &n);
+    }
+    if (rc != FRZ_OK) {
+      launches.clear();
+      status = rc;
+      message = frz_last_error();
     }
     double at = 0.0;
     for (frz_launch_time& t : launches) {
