@@ -83,6 +83,29 @@ def test_program_steps_are_generate(device, setup):
     b.close()
 
 
+def test_program_steps_in_the_fast_prefill_mode(device, setup):
+    """A model in the fast prefill mode runs the program's prompt steps on
+    the bf16 matrix cores, as its own generate does: the same tokens and
+    last logits, bit for bit (the decode steps are exact in both). The
+    program writes the capture store at the prompt's end, and a step that
+    captures takes the exact attention (the store's per-key weights come
+    from it), so generate's model captures too."""
+    cfg, path, plan = setup
+    a, b = _model(device, plan, path), _model(device, plan, path)
+    a.set_prefill(fz.PREFILL_BF16)
+    b.set_prefill(fz.PREFILL_BF16)
+    b.set_capture(True)
+    prog = fprog.Program(a, plan)
+    prompt = np.random.default_rng(83).integers(0, cfg.vocab, 700).astype(np.uint32)
+    got = _run_turn(prog, prompt, 16)
+    want = b.generate(prompt, max_tokens=16)
+    assert np.array_equal(got, want), (got, want)
+    assert_same_bits(a.logits(), b.logits(), "last logits")
+    prog.close()
+    a.close()
+    b.close()
+
+
 def test_program_edit_table_as_a_run_input(device, setup):
     cfg, path, plan = setup
     a, b = _model(device, plan, path), _model(device, plan, path)
