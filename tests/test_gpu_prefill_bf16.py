@@ -16,6 +16,7 @@ import _oracle as orc
 import frizzle_amd as fz
 from helpers import dequant, format_blocks, q4_blocks
 from test_gpu_bench_regimes import wandering_pair
+from test_gpu_model import MIXED, _mixed_tensors, _set_all, oracle_run, small_config
 
 pytestmark = pytest.mark.gpu
 
@@ -164,6 +165,31 @@ def test_fast_prefill_full_size_2048(device):
     want = oracle.prompt(prompt)
     err = _rel_err(got, want)
     print(f"fast prefill, 26 layers, 2,048 tokens: max |logit error| / max |logit| = {err:.2e}")
+    assert err < 1e-3
+    model.close()
+    oracle.close()
+
+
+def test_fast_prefill_mixed_formats(device):
+    # The pinned file's formats in the fast mode: a Q8_0 embedding (and so
+    # tied head) and Q4_1 / Q8_0 downs, whose weight planes keep their own
+    # unpack. A 600-token prompt in steps of 512 and 88: the prompt-end
+    # logits within 1e-3 (max-norm relative) of the oracle's over the same
+    # formats.
+    cfg = small_config()
+    t = _mixed_tensors(cfg, 43)
+    oracle = orc.OracleModel(cfg.as_dict(), t, formats=MIXED)
+    model = fz.Model(device, cfg)
+    _set_all(model, t, MIXED)
+    zeros = np.zeros(2 * cfg.layers, dtype=np.uint32)
+    model.set_edits(zeros)
+    prompt = np.random.default_rng(44).integers(0, cfg.vocab, 600).astype(np.uint32)
+    _, want = oracle_run(oracle, prompt, 0, cfg)
+    model.set_prefill(fz.PREFILL_BF16)
+    for p0 in range(0, len(prompt), 512):
+        model.step(p0, prompt[p0:p0 + 512], logits=p0 + 512 >= len(prompt))
+    err = _rel_err(model.logits(), want)
+    print(f"fast prefill, mixed formats, 600 tokens: max |logit error| / max |logit| = {err:.2e}")
     assert err < 1e-3
     model.close()
     oracle.close()
