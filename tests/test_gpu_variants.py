@@ -8,7 +8,8 @@ import pytest
 import _oracle as orc
 import frizzle_amd as fz
 from helpers import assert_same_bits
-from test_gpu_model import build_pair, oracle_run, placed, small_config
+from test_gpu_model import (MIXED, _mixed_tensors, _set_all, build_pair, oracle_run, placed,
+                            small_config)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +54,25 @@ def test_variants_are_the_replies_alone(device):
     # random-init model may keep its tokens, so they alone need not differ).
     last = res[0, -1]
     assert sum(not np.array_equal(last[0], last[v]) for v in range(1, len(variants))) >= 3
+    model.close()
+
+
+def test_variants_over_the_pinned_files_formats(device):
+    # A Q8_0 embedding and tied head, Q4_1 and Q8_0 downs: the 16-row
+    # products of those formats (the down split over two workgroups, the
+    # Q8_0 head) give each variant the tokens its reply gets alone, greedy
+    # and sampled.
+    cfg = small_config()
+    model = fz.Model(device, cfg)
+    _set_all(model, _mixed_tensors(cfg, 61), MIXED)
+    rng = np.random.default_rng(62)
+    prompt = rng.integers(0, cfg.vocab, 70).astype(np.uint32)
+    variants = seeded_variants(cfg, rng, 16)
+    for samp in (fz.sampling(), fz.sampling(temperature=1.0, top_k=64, seed=0x61)):
+        got = model.generate_variants(prompt, variants, samp=samp, max_tokens=12)
+        for v, edits in enumerate(variants):
+            alone = model.generate(prompt, edits, samp=samp, max_tokens=12)
+            assert np.array_equal(got[v], alone), (v, got[v], alone)
     model.close()
 
 
