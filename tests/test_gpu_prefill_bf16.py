@@ -117,6 +117,31 @@ def test_gated_bf16_within_bound_with_pins(device):
     assert float(np.max(np.abs(got - want) / np.maximum(tol, 1e-30))) <= 1.0
 
 
+def test_gated_bf16_partial_tile(device):
+    # 80 neurons: one whole 64-neuron tile and a tile of 16 whose rows past
+    # the end are read clamped and not stored; 40 tokens (a partial
+    # 32-token block); no pins.
+    rows, cols, tokens = 80, 128, 40
+    rng = np.random.default_rng(8)
+    g, u = q4_blocks(rng, rows, cols), q4_blocks(rng, rows, cols)
+    x = rng.normal(0, 1, (tokens, cols)).astype(np.float32)
+    gc, gs = _dev_blocks(device, fz.Q4_0, g)
+    uc, us = _dev_blocks(device, fz.Q4_0, u)
+    dx = device.array(x)
+    da = device.empty((tokens, rows), np.float32)
+    fz._lib.check(fz.load().frz_op_gated_bf16(device.handle, gc.ptr, gs.ptr, uc.ptr, us.ptr, rows,
+                                              cols, dx.ptr, da.ptr, tokens, 0, None, 0))
+    x64 = x.astype(np.float64)
+    wg, wu = dequant(g, rows, cols).astype(np.float64), dequant(u, rows, cols).astype(np.float64)
+    gv, uv = x64 @ wg.T, x64 @ wu.T
+    eg, eu = _bound(wg, x64), _bound(wu, x64)
+    z = np.sqrt(2 / np.pi) * (gv + 0.044715 * gv ** 3)
+    gelu = 0.5 * gv * (1 + np.tanh(z))
+    want = gelu * uv
+    tol = 1.13 * eg * np.abs(uv) + (np.abs(gelu) + 1.13 * eg) * eu + 2.0 ** -19 * np.abs(want) + 1e-30
+    assert float(np.max(np.abs(da.numpy().astype(np.float64) - want) / tol)) <= 1.0
+
+
 def _rel_err(got, want):
     return float(np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(want)))
 
